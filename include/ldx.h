@@ -1,0 +1,188 @@
+/* ldx.h -- C ABI of libldx.so, the MI355X (gfx950) dense hot path of 3-D latent
+ * diffusion: implicit-GEMM conv3d with fused GroupNorm/SiLU prologue and
+ * bias/shift/residual/scale epilogue, flash attention, GroupNorm statistics,
+ * LayerNorm, weight packing and the DDIM step.
+ *
+ * Conventions
+ *  - Activations are channels-last NDHWC float16 ("voxels x channels"); every
+ *    activation pointer comes with a voxel pitch in elements (>= channels), so a
+ *    kernel can read or write a channel slice of a wider tensor (zero-copy concat).
+ *  - All pointers are device pointers owned by the caller; no entry point allocates
+ *    device memory. Work is enqueued on `stream` (a hipStream_t, passed as void*;
+ *    NULL = the default stream) and is stream-ordered; nothing synchronises the host.
+ *  - Return 0 on success, LDX_EINVAL for an argument the kernels do not accept
+ *    (nothing is launched), LDX_EHIP for a HIP launch error. ldx_last_error() gives
+ *    the message of the calling thread's last failure.
+ *
+ * Reference correspondence (MedMLX/lesiondiffusion-mlx v0.3.0; the reference binds
+ * its kernels through mx.fast.metal_kernel, src/lesiondiffusion_mlx/_typing.py:35-66,
+ * and exposes the op-level functions cited at each entry point below).
+ */
+#ifndef LDX_H
+#define LDX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LDX_OK 0
+#define LDX_EINVAL (-1)
+#define LDX_EHIP (-2)
+
+/* Message of the calling thread's most recent failure ("" if none). */
+const char* ldx_last_error(void);
+/* ABI version; bumped on any change to the structs below. */
+int ldx_abi_version(void);
+
+/* ---------------------------------------------------------------- conv3d -------
+ * Replaces nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619) and the
+ * pointwise/dense paths of SourceLayers.conv/dense (mlx_model.py:159-220).
+ *
+ * y[b, v, o] = half( (sum_{tap,c} W[o, tap, c] * xin[b, v@tap, c] + bias[(b,) o])
+ *                    * output_scale + residual[b, v, o] )
+ * xin = half(silu(x * affine[b, c, 0] + affine[b, c, 1])) when affine/silu are set
+ * (rounded once, zero padding applied after it), else x. One rounding of the FP32
+ * sum. act = LDX_ACT_GELU further stores half(gelu_erf(float(y))) (the dense->GELU
+ * pair of mlx_model.py:549).
+ *
+ * Geometry: ksize 3 (padding 1) with stride 1 or 2, or with upsample = 1 (conv of
+ * the nearest 2x upsampling of x, weights from ldx_pack_upsample_weight); ksize 1
+ * (padding 0, stride 1) covers pointwise convs and dense layers (a dense layer over
+ * L tokens is a 1 x 1 x L volume). Output extents: n (stride 1), (n-1)/2+1
+ * (stride 2), 2n (upsample).
+ *
+ * x may be split over two tensors along channels (x1 may be NULL): channels
+ * [0, c0) come from x0 and [c0, c0 + c1) from x1 -- the UNet decoder's
+ * concat([x, skip]) without a copy.
+ */
+#define LDX_ACT_NONE 0
+#define LDX_ACT_GELU 1
+
+typedef struct ldx_conv3d_args {
+  int32_t batch, in_d, in_h, in_w;   /* input (source) grid */
+  int32_t c0, c1;                    /* channels of x0 and x1 (c1 = 0 without x1) */
+  int32_t out_c;                     /* output channels O */
+  int32_t ksize;                     /* 3 or 1 */
+  int32_t stride;                    /* 1 or 2 */
+  int32_t upsample;                  /* 0 or 1 */
+  const void* x0; int64_t x0_pitch;  /* fp16 NDHWC, voxel pitch in elements */
+  const void* x1; int64_t x1_pitch;
+  const void* weight;                /* packed fp16, ldx_pack_weight layout */
+  const float* bias;                 /* fp32 (O) or (batch, O) if bias_batched; may be NULL */
+  int32_t bias_batched;
+  const float* affine;               /* fp32 (batch, c0 + c1, 2) scale/offset pairs or NULL */
+  int32_t silu;                      /* apply SiLU to the prepared input */
+  const void* residual; int64_t residual_pitch;  /* fp16 NDHWC of the output grid or NULL */
+  float output_scale;                /* 1.0 = plain */
+  int32_t act;                       /* LDX_ACT_* */
+  void* y; int64_t y_pitch;          /* fp16 NDHWC output */
+} ldx_conv3d_args;
+
+int ldx_conv3d(const ldx_conv3d_args* args, void* stream);
+
+/* Pack a Torch-layout fp16 weight (O, C, K, K, K) (K = 3 or 1) into the kernel
+ * layout (O, K^3, C): W'[o, tap, c] = W[o, c, kd, kh, kw], tap = kd*9 + kh*3 + kw
+ * (the reference's pack_weight, _nax_conv.py:350-364, stores the transpose
+ * (27*C', O') with row tap*C' + c; this layout keeps each output channel's
+ * reduction contiguous for the MFMA A operand and needs no channel padding). */
+int ldx_pack_weight(const void* weight, int32_t out_c, int32_t in_c, int32_t ksize,
+                    void* packed, void* stream);
+
+/* Fold a Torch-layout fp16 (O, C, 3, 3, 3) weight into the 8 parity 2x2x2 filters
+ * of a nearest-2x-upsampled conv, layout (8, O, 8, C): [pd*4+ph*2+pw, o,
+ * td*4+th*2+tw, c]; merged taps summed in fp32 in the reference's order and rounded
+ * to fp16 once (pack_upsample_weight, _nax_conv.py:367-405). */
+int ldx_pack_upsample_weight(const void* weight, int32_t out_c, int32_t in_c,
+                             void* packed, void* stream);
+
+/* ------------------------------------------------------------- group norm -------
+ * Replaces medmlx_core group_norm_affine (call sites mlx_model.py:328-335,
+ * _scaled_vq.py:93-100): per-(b, group) mean / biased variance of x (optionally the
+ * channel concat of x0 and x1), folded with gamma/beta into fp32 (batch, C, 2)
+ * (scale = gamma * rsqrt(var + eps), offset = beta - scale * mean). Two
+ * deterministic passes (no float atomics) through a caller-provided workspace of
+ * ldx_group_norm_workspace_bytes() bytes. gamma/beta are fp32 (C). */
+size_t ldx_group_norm_workspace_bytes(int32_t batch, int64_t voxels, int32_t channels,
+                                      int32_t groups);
+int ldx_group_norm_affine(const void* x0, int64_t x0_pitch, int32_t c0,
+                          const void* x1, int64_t x1_pitch, int32_t c1,
+                          int32_t batch, int64_t voxels, int32_t groups,
+                          const float* gamma, const float* beta, float eps,
+                          float* affine, void* workspace, void* stream);
+
+/* LayerNorm over the last axis of fp16 (rows, features) (mx.fast.layer_norm,
+ * mlx_model.py:360-367): y = half((x - mean) * rsqrt(var + eps) * gamma + beta),
+ * statistics in fp32. gamma/beta fp32. */
+int ldx_layer_norm(const void* x, int64_t x_pitch, int64_t rows, int32_t features,
+                   const float* gamma, const float* beta, float eps,
+                   void* y, int64_t y_pitch, void* stream);
+
+/* -------------------------------------------------------------- attention -------
+ * Replaces flash_attention_half (_attention_half.py:129-147) and the fused
+ * mx.fast.scaled_dot_product_attention routes of LdmUnet.attention
+ * (mlx_model.py:443-493): o = softmax(q k^T * scale + mask) v per (batch, head),
+ * fp16 inputs/outputs, fp32 scores, online softmax and accumulation.
+ * Tensors are 4-D (batch, len, heads, head_dim) with arbitrary element strides
+ * (head_dim stride must be 1); both the projection layout (B, L, H*D) and
+ * (B, H, L, D) are views of this. head_dim in {16, 32, 64, 128, 256}.
+ * mask (optional) is additive fp32 with strides (batch, head, query, key), 0 for a
+ * broadcast axis; -inf removes a key; a query row with every key removed gives 0. */
+typedef struct ldx_attention_args {
+  int32_t batch, heads, q_len, kv_len, head_dim;
+  const void* q; int64_t q_stride[3];   /* batch, len, head strides (elements) */
+  const void* k; int64_t k_stride[3];
+  const void* v; int64_t v_stride[3];
+  void* o; int64_t o_stride[3];
+  float scale;
+  const float* mask; int64_t mask_stride[4];
+} ldx_attention_args;
+
+int ldx_attention(const ldx_attention_args* args, void* stream);
+
+/* ------------------------------------------------------------ small ops ---------
+ * Sinusoidal timestep features [cos(t f_i), sin(t f_i)], f_i = exp(-ln(1e4) i/half)
+ * (mlx_model.py:609-612), written as fp16 (batch, channels). timesteps int32. */
+int ldx_timestep_embedding(const int32_t* timesteps, int32_t batch, int32_t channels,
+                           void* out, void* stream);
+
+/* y = half(silu(float(x))) elementwise over n fp16 values (LdmUnet.silu,
+ * mlx_model.py:409-413). */
+int ldx_silu(const void* x, int64_t n, void* y, void* stream);
+
+/* Copy a channel slice: dst[v, dst_off + c] = src[v, src_off + c], c < channels,
+ * for `voxels` voxels of fp16 NDHWC tensors (concat / split without torch). */
+int ldx_copy_channels(const void* src, int64_t src_pitch, int32_t src_off,
+                      void* dst, int64_t dst_pitch, int32_t dst_off,
+                      int64_t voxels, int32_t channels, void* stream);
+
+/* Nearest 2x upsampling of fp16 NDHWC (B, D, H, W, C) into (B, 2D, 2H, 2W, C): output
+ * index i of each axis reads input floor(i / 2) (upsample_nearest2 / resize_nearest,
+ * src/lesiondiffusion_mlx/_spatial.py:41-69). The fused conv path (upsample = 1 in
+ * ldx_conv3d) never forms this tensor; this entry point serves callers that need it. */
+int ldx_upsample_nearest2(const void* x, int64_t x_pitch, int32_t batch, int32_t d, int32_t h,
+                          int32_t w, int32_t channels, void* y, int64_t y_pitch, void* stream);
+
+/* One masked DDIM step of the conditioned sampler (mlx_sampling.py:172-185) on
+ * NDHWC latents with `channels` channels (fp32 state x, fp16 network in/out):
+ *   prepare: with a mask, xm = x*m + (1-m)*cond, x = xm, and net_in[v] =
+ *       [half(xm) (C), half(cond*(1-m)) (cond_channels = C, or absent when 0),
+ *       half(m) (1)]; without a mask net_in[v] = [half(x) (C), half(cond)
+ *       (cond_channels)] (the mask-free form of mlx_sampling.py:177-178).
+ *   update: x = sqrt(prev)*(x - s1m*eps)/sqrt(a) + sqrt(1-prev-sig^2)*eps
+ *       + sig*noise, eps = float(net_out[v, 0:C))
+ * coef = {alpha, previous, sigma, sqrt_one_minus} (fp32 device array of 4). x, cond,
+ * noise are fp32 NDHWC with `channels` (cond: cond_channels without a mask)
+ * channels; mask is fp32 (voxels). */
+int ldx_ddim_prepare(float* x, const float* cond, const float* mask, int64_t voxels,
+                     int32_t channels, int32_t cond_channels, void* net_in,
+                     int64_t net_pitch, void* stream);
+int ldx_ddim_update(float* x, const void* net_out, int64_t net_pitch, const float* noise,
+                    const float* coef, int64_t voxels, int32_t channels, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LDX_H */

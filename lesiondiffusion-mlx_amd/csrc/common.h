@@ -1,0 +1,40 @@
+// Shared device/host helpers for libldx (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "ldx.h"
+
+typedef _Float16 f16;
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+namespace ldx {
+
+// ---------------------------------------------------------------- errors (host)
+void set_error(const char* fmt, ...);
+int fail(const char* fmt, ...);  // set_error + return LDX_EINVAL
+int check_launch(const char* what);  // hipGetLastError -> LDX_EHIP / LDX_OK
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ---------------------------------------------------------------- device math
+__device__ __forceinline__ float silu_f(float y) { return y / (1.0f + __expf(-y)); }
+
+// One 16x16x32 f16 MFMA: D(16x16) += A(16x32) * B(32x16).
+// Lane l: A row l%16, k = 8*(l/16)+e; B col l%16, k = 8*(l/16)+e;
+// D col l%16, rows 4*(l/16)+r.
+__device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace ldx

@@ -1,0 +1,494 @@
+// Small kernels of the hot path: weight packing, GroupNorm statistics, LayerNorm,
+// timestep features, SiLU, channel-slice copies and the DDIM step; plus the
+// library's error plumbing.
+
+#include "common.h"
+
+#include <cmath>
+
+namespace ldx {
+
+static thread_local std::string g_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+
+int fail(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return LDX_EINVAL;
+}
+
+int check_launch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: %s", what, hipGetErrorString(e));
+    return LDX_EHIP;
+  }
+  return LDX_OK;
+}
+
+static inline unsigned blocks_for(int64_t n, int per) { return (unsigned)((n + per - 1) / per); }
+static inline unsigned grid_cap(int64_t n, int per, unsigned cap) {
+  const int64_t g = (n + per - 1) / per;
+  return g < (int64_t)cap ? (unsigned)g : cap;
+}
+
+// ------------------------------------------------------------------ packing
+// packed[o][tap][c] = w[o][c][tap]   (pack_weight, _nax_conv.py:350-364, transposed)
+__global__ void pack_weight_kernel(const f16* __restrict__ w, int O, int C, int taps,
+                                   f16* __restrict__ out) {
+  const int64_t n = (int64_t)O * C * taps;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % C);
+    const int64_t r = i / C;
+    const int tap = (int)(r % taps);
+    const int o = (int)(r / taps);
+    out[i] = w[((int64_t)o * C + c) * taps + tap];
+  }
+}
+
+// Fold one axis: parity p, tap t -> the original taps it merges.
+__device__ __forceinline__ void fold_set(int p, int t, int& k_lo, int& k_hi) {
+  // p = 0: t = 0 -> {0}, t = 1 -> {1, 2};  p = 1: t = 0 -> {0, 1}, t = 1 -> {2}
+  if (p == 0) { k_lo = t == 0 ? 0 : 1; k_hi = t == 0 ? 0 : 2; }
+  else { k_lo = t == 0 ? 0 : 2; k_hi = t == 0 ? 1 : 2; }
+}
+
+// packed[parity][o][tap][c], parity = pd*4+ph*2+pw, tap = td*4+th*2+tw. Sums are
+// float32 and nest d (innermost), then h, then w, each left to right -- the order
+// of the reference's per-axis folds (_nax_conv.py:394-405).
+__global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
+                                     f16* __restrict__ out) {
+  const int64_t n = (int64_t)8 * O * 8 * C;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % C);
+    int64_t r = i / C;
+    const int tap = (int)(r % 8); r /= 8;
+    const int o = (int)(r % O);
+    const int parity = (int)(r / O);
+    const int pd = parity >> 2, ph = (parity >> 1) & 1, pw = parity & 1;
+    const int td = tap >> 2, th = (tap >> 1) & 1, tw = tap & 1;
+    int d_lo, d_hi, h_lo, h_hi, w_lo, w_hi;
+    fold_set(pd, td, d_lo, d_hi);
+    fold_set(ph, th, h_lo, h_hi);
+    fold_set(pw, tw, w_lo, w_hi);
+    const f16* base = w + ((int64_t)o * C + c) * 27;
+    float tot = 0.0f;
+    for (int kw = w_lo; kw <= w_hi; kw++) {
+      float hs = 0.0f;
+      for (int kh = h_lo; kh <= h_hi; kh++) {
+        float ds = 0.0f;
+        for (int kd = d_lo; kd <= d_hi; kd++) ds += (float)base[kd * 9 + kh * 3 + kw];
+        hs += ds;
+      }
+      tot += hs;
+    }
+    out[i] = (f16)tot;
+  }
+}
+
+// ------------------------------------------------------------ group norm
+// Pass 1: each workgroup reduces `chunk` voxels of one batch item to per-group
+// (count, mean, M2) partials; per-thread sums over a few voxels, converted to
+// (n, mean, M2) and merged (Chan et al.) in a fixed order, so results are
+// deterministic run to run.
+struct Moments { float n, mean, m2; };
+
+__device__ __forceinline__ Moments merge(Moments a, Moments b) {
+  const float n = a.n + b.n;
+  if (n == 0.0f) return a;
+  const float d = b.mean - a.mean;
+  const float fb = b.n / n;
+  return {n, a.mean + d * fb, a.m2 + b.m2 + d * d * a.n * fb};
+}
+
+template <int V>
+__global__ __launch_bounds__(256) void gn_partial_kernel(
+    const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,
+    int C, int G, int64_t S, int64_t chunk, float* __restrict__ partial, int nchunks) {
+  __shared__ float s_sum[256 * V];
+  __shared__ float s_sq[256 * V];
+  __shared__ float s_n[256];
+  const int b = blockIdx.y;
+  const int ch = blockIdx.x;
+  const int tpv = C / V;                // threads per voxel
+  const int vpi = 256 / tpv;            // voxels per iteration
+  const int t = threadIdx.x;
+  const int lane_c = (t % tpv) * V;     // first channel of this thread
+  const int vsub = t / tpv;
+  const bool active = vsub < vpi;
+  float sum[V], sq[V];
+#pragma unroll
+  for (int e = 0; e < V; e++) { sum[e] = 0.f; sq[e] = 0.f; }
+  float n = 0.f;
+  const int64_t v_begin = (int64_t)ch * chunk;
+  const int64_t v_end = min(S, v_begin + chunk);
+  if (active) {
+    for (int64_t v = v_begin + vsub; v < v_end; v += vpi) {
+      const int64_t vi = (int64_t)b * S + v;
+      const f16* src = lane_c < C0 ? x0 + vi * p0 + lane_c : x1 + vi * p1 + (lane_c - C0);
+      if constexpr (V == 8) {
+        const f16x8 h = *reinterpret_cast<const f16x8*>(src);
+#pragma unroll
+        for (int e = 0; e < 8; e++) { const float f = (float)h[e]; sum[e] += f; sq[e] += f * f; }
+      } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) { const float f = (float)src[e]; sum[e] += f; sq[e] += f * f; }
+      }
+      n += 1.f;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < V; e++) {
+    // per-thread per-channel mean and M2
+    const float mean = n > 0.f ? sum[e] / n : 0.f;
+    s_sum[t * V + e] = mean;
+    s_sq[t * V + e] = n > 0.f ? fmaxf(sq[e] - sum[e] * mean, 0.f) : 0.f;
+  }
+  s_n[t] = active ? n : 0.f;
+  __syncthreads();
+  const int gs = C / G;
+  for (int g = t; g < G; g += 256) {
+    Moments m = {0.f, 0.f, 0.f};
+    for (int vs = 0; vs < vpi; vs++) {
+      for (int c = g * gs; c < (g + 1) * gs; c++) {
+        const int tt = vs * tpv + c / V;
+        const int e = c % V;
+        m = merge(m, Moments{s_n[tt], s_sum[tt * V + e], s_sq[tt * V + e]});
+      }
+    }
+    float* out = partial + (((int64_t)b * nchunks + ch) * G + g) * 3;
+    out[0] = m.n; out[1] = m.mean; out[2] = m.m2;
+  }
+}
+
+// Pass 2: one workgroup per (group, batch item) merges the chunk partials in a
+// fixed tree order and writes the (scale, offset) pairs of the group's channels.
+__global__ __launch_bounds__(256) void gn_finalize_kernel(
+    const float* __restrict__ partial, int nchunks, int C, int G, const float* __restrict__ gamma,
+    const float* __restrict__ beta, float eps, float* __restrict__ affine) {
+  __shared__ float sn[256], sm[256], s2[256];
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  Moments m = {0.f, 0.f, 0.f};
+  for (int j = t; j < nchunks; j += 256) {
+    const float* pp = partial + (((int64_t)b * nchunks + j) * G + g) * 3;
+    m = merge(m, Moments{pp[0], pp[1], pp[2]});
+  }
+  sn[t] = m.n; sm[t] = m.mean; s2[t] = m.m2;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) {
+      const Moments r = merge(Moments{sn[t], sm[t], s2[t]}, Moments{sn[t + off], sm[t + off], s2[t + off]});
+      sn[t] = r.n; sm[t] = r.mean; s2[t] = r.m2;
+    }
+    __syncthreads();
+  }
+  const float mean = sm[0];
+  const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  const int gs = C / G;
+  for (int c = g * gs + t; c < (g + 1) * gs; c += 256) {
+    const float sc = gamma[c] * rstd;
+    affine[((int64_t)b * C + c) * 2] = sc;
+    affine[((int64_t)b * C + c) * 2 + 1] = beta[c] - sc * mean;
+  }
+}
+
+static int64_t gn_chunk(int64_t S, int batch) {
+  // aim for >= ~512 workgroups in pass 1, chunks of 64..4096 voxels
+  int64_t per = (S * batch + 511) / 512;
+  if (per < 64) per = 64;
+  if (per > 4096) per = 4096;
+  return per;
+}
+
+// ------------------------------------------------------------- layer norm
+// One wave per row; statistics in fp32 (two passes over registers).
+template <int MAXV>
+__global__ __launch_bounds__(256) void layer_norm_kernel(const f16* __restrict__ x, int64_t xp,
+                                                         int64_t rows, int F,
+                                                         const float* __restrict__ gamma,
+                                                         const float* __restrict__ beta, float eps,
+                                                         f16* __restrict__ y, int64_t yp) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const f16* xr = x + row * xp;
+  float v[MAXV];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; i++) {
+    const int c = lane + i * 64;
+    v[i] = c < F ? (float)xr[c] : 0.f;
+    s += v[i];
+  }
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off);
+  const float mean = s / F;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXV; i++) {
+    const int c = lane + i * 64;
+    const float d = c < F ? v[i] - mean : 0.f;
+    q += d * d;
+  }
+  for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off);
+  const float rstd = 1.0f / sqrtf(q / F + eps);
+  f16* yr = y + row * yp;
+#pragma unroll
+  for (int i = 0; i < MAXV; i++) {
+    const int c = lane + i * 64;
+    if (c < F) yr[c] = (f16)((v[i] - mean) * rstd * gamma[c] + beta[c]);
+  }
+}
+
+// --------------------------------------------------------------- small ops
+__global__ void timestep_kernel(const int32_t* __restrict__ t, int B, int channels,
+                                f16* __restrict__ out) {
+  const int half = channels / 2;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= B * half) return;
+  const int b = i / half, k = i % half;
+  const float freq = expf(-9.21034037197618273607f * (float)k / (float)half);
+  const float ph = (float)t[b] * freq;
+  out[(int64_t)b * channels + k] = (f16)cosf(ph);
+  out[(int64_t)b * channels + half + k] = (f16)sinf(ph);
+}
+
+__global__ void silu_kernel(const f16* __restrict__ x, int64_t n, f16* __restrict__ y) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const float v = (float)x[i];
+    y[i] = (f16)(v / (1.0f + expf(-v)));
+  }
+}
+
+__global__ void copy_channels_kernel(const f16* __restrict__ src, int64_t sp, int so,
+                                     f16* __restrict__ dst, int64_t dp, int dof, int64_t V, int C) {
+  const int64_t n = V * C;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = i / C;
+    const int c = (int)(i % C);
+    dst[v * dp + dof + c] = src[v * sp + so + c];
+  }
+}
+
+// Nearest 2x upsampling, NDHWC: out[2d+i, 2h+j, 2w+k] = in[d, h, w] (floor(i / 2) rule,
+// src/lesiondiffusion_mlx/_spatial.py:12-26).
+__global__ void upsample2_kernel(const f16* __restrict__ x, int64_t xp, int B, int D, int H, int W,
+                                 int C, f16* __restrict__ y, int64_t yp) {
+  const int64_t n = (int64_t)B * 8 * D * H * W * C;
+  const int OH = 2 * H, OW = 2 * W, OD = 2 * D;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % C);
+    int64_t r = i / C;
+    const int ow = (int)(r % OW); r /= OW;
+    const int oh = (int)(r % OH); r /= OH;
+    const int od = (int)(r % OD);
+    const int64_t b = r / OD;
+    const int64_t src = ((b * D + od / 2) * H + oh / 2) * W + ow / 2;
+    const int64_t dst = ((b * OD + od) * OH + oh) * (int64_t)OW + ow;
+    y[dst * yp + c] = x[src * xp + c];
+  }
+}
+
+__global__ void ddim_prepare_kernel(float* __restrict__ x, const float* __restrict__ cond,
+                                    const float* __restrict__ mask, int64_t V, int C, int CC,
+                                    f16* __restrict__ net, int64_t np) {
+  for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < V;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    f16* row = net + v * np;
+    if (mask) {
+      const float m = mask[v];
+      for (int c = 0; c < C; c++) {
+        const float cv = cond[v * C + c];
+        const float xm = x[v * C + c] * m + (1.0f - m) * cv;
+        x[v * C + c] = xm;
+        row[c] = (f16)xm;
+        if (CC) row[C + c] = (f16)(cv * (1.0f - m));
+      }
+      row[C + CC] = (f16)m;
+    } else {
+      for (int c = 0; c < C; c++) row[c] = (f16)x[v * C + c];
+      for (int c = 0; c < CC; c++) row[C + c] = (f16)cond[v * CC + c];
+    }
+  }
+}
+
+__global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict__ net, int64_t np,
+                                   const float* __restrict__ noise, const float* __restrict__ coef,
+                                   int64_t V, int C) {
+  const float a = coef[0], prev = coef[1], sig = coef[2], s1m = coef[3];
+  const float c_dir = sqrtf(1.0f - prev - sig * sig);
+  const int64_t n = V * C;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t v = i / C;
+    const int c = (int)(i % C);
+    const float eps = (float)net[v * np + c];
+    const float pred = (x[i] - s1m * eps) / sqrtf(a);
+    x[i] = sqrtf(prev) * pred + c_dir * eps + sig * noise[i];
+  }
+}
+
+}  // namespace ldx
+
+using namespace ldx;
+
+extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
+extern "C" int ldx_abi_version(void) { return 1; }
+
+extern "C" int ldx_pack_weight(const void* weight, int32_t O, int32_t C, int32_t k, void* packed,
+                               void* stream) {
+  if (!weight || !packed) return fail("pack_weight: null pointer");
+  if (O < 1 || C < 1 || (k != 1 && k != 3)) return fail("pack_weight: bad shape O=%d C=%d k=%d", O, C, k);
+  const int taps = k * k * k;
+  const int64_t n = (int64_t)O * C * taps;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
+                     as_stream(stream), (const f16*)weight, O, C, taps, (f16*)packed);
+  return check_launch("pack_weight");
+}
+
+extern "C" int ldx_pack_upsample_weight(const void* weight, int32_t O, int32_t C, void* packed,
+                                        void* stream) {
+  if (!weight || !packed) return fail("pack_upsample_weight: null pointer");
+  if (O < 1 || C < 1) return fail("pack_upsample_weight: bad shape O=%d C=%d", O, C);
+  const int64_t n = (int64_t)64 * O * C;
+  hipLaunchKernelGGL(pack_upsample_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
+                     as_stream(stream), (const f16*)weight, O, C, (f16*)packed);
+  return check_launch("pack_upsample_weight");
+}
+
+extern "C" size_t ldx_group_norm_workspace_bytes(int32_t batch, int64_t voxels, int32_t channels,
+                                                 int32_t groups) {
+  if (batch < 1 || voxels < 1 || groups < 1) return 0;
+  (void)channels;
+  const int64_t chunk = gn_chunk(voxels, batch);
+  const int64_t nchunks = (voxels + chunk - 1) / chunk;
+  return (size_t)(batch * nchunks * groups * 3) * sizeof(float);
+}
+
+extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, const void* x1,
+                                     int64_t p1, int32_t c1, int32_t batch, int64_t voxels,
+                                     int32_t groups, const float* gamma, const float* beta,
+                                     float eps, float* affine, void* workspace, void* stream) {
+  if (!x0 || !gamma || !beta || !affine || !workspace) return fail("group_norm_affine: null pointer");
+  if (c1 > 0 && !x1) return fail("group_norm_affine: c1 > 0 but x1 is null");
+  const int C = c0 + (c1 > 0 ? c1 : 0);
+  if (batch < 1 || voxels < 1 || c0 < 1 || groups < 1 || C % groups)
+    return fail("group_norm_affine: bad shape (batch %d voxels %lld C %d groups %d)", batch,
+                (long long)voxels, C, groups);
+  if (p0 < c0 || (c1 > 0 && p1 < c1)) return fail("group_norm_affine: pitch < channels");
+  const bool vec = C % 8 == 0 && c0 % 8 == 0 && p0 % 8 == 0 && (c1 <= 0 || p1 % 8 == 0) &&
+                   (uintptr_t)x0 % 16 == 0 && (c1 <= 0 || (uintptr_t)x1 % 16 == 0) && C / 8 <= 256;
+  if (!vec && C > 256) return fail("group_norm_affine: unaligned input with more than 256 channels");
+  const int64_t chunk = gn_chunk(voxels, batch);
+  const int64_t nchunks = (voxels + chunk - 1) / chunk;
+  if (nchunks > 0x7fffffff || batch > 65535 || groups > 65535) return fail("group_norm_affine: too large");
+  hipStream_t st = as_stream(stream);
+  float* part = (float*)workspace;
+  if (vec)
+    hipLaunchKernelGGL(gn_partial_kernel<8>, dim3((unsigned)nchunks, batch), dim3(256), 0, st,
+                       (const f16*)x0, p0, c0, (const f16*)x1, p1, C, groups, voxels, chunk, part,
+                       (int)nchunks);
+  else
+    hipLaunchKernelGGL(gn_partial_kernel<1>, dim3((unsigned)nchunks, batch), dim3(256), 0, st,
+                       (const f16*)x0, p0, c0, (const f16*)x1, p1, C, groups, voxels, chunk, part,
+                       (int)nchunks);
+  int rc = check_launch("group_norm_affine: partial");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, batch), dim3(256), 0, st, part, (int)nchunks, C,
+                     groups, gamma, beta, eps, affine);
+  return check_launch("group_norm_affine: finalize");
+}
+
+extern "C" int ldx_layer_norm(const void* x, int64_t xp, int64_t rows, int32_t F, const float* gamma,
+                              const float* beta, float eps, void* y, int64_t yp, void* stream) {
+  if (!x || !y || !gamma || !beta) return fail("layer_norm: null pointer");
+  if (rows < 1 || F < 1 || xp < F || yp < F) return fail("layer_norm: bad shape");
+  if (F > 1024) return fail("layer_norm: features %d > 1024", F);
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+  hipStream_t st = as_stream(stream);
+  if (F <= 256)
+    hipLaunchKernelGGL(layer_norm_kernel<4>, dim3(grid), dim3(256), 0, st, (const f16*)x, xp, rows, F,
+                       gamma, beta, eps, (f16*)y, yp);
+  else
+    hipLaunchKernelGGL(layer_norm_kernel<16>, dim3(grid), dim3(256), 0, st, (const f16*)x, xp, rows, F,
+                       gamma, beta, eps, (f16*)y, yp);
+  return check_launch("layer_norm");
+}
+
+extern "C" int ldx_timestep_embedding(const int32_t* t, int32_t B, int32_t channels, void* out,
+                                      void* stream) {
+  if (!t || !out) return fail("timestep_embedding: null pointer");
+  if (B < 1 || channels < 2 || channels % 2) return fail("timestep_embedding: bad shape");
+  hipLaunchKernelGGL(timestep_kernel, dim3(blocks_for((int64_t)B * channels / 2, 256)), dim3(256), 0,
+                     as_stream(stream), t, B, channels, (f16*)out);
+  return check_launch("timestep_embedding");
+}
+
+extern "C" int ldx_silu(const void* x, int64_t n, void* y, void* stream) {
+  if (!x || !y) return fail("silu: null pointer");
+  if (n < 1) return fail("silu: empty");
+  hipLaunchKernelGGL(silu_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
+                     as_stream(stream), (const f16*)x, n, (f16*)y);
+  return check_launch("silu");
+}
+
+extern "C" int ldx_copy_channels(const void* src, int64_t sp, int32_t so, void* dst, int64_t dp,
+                                 int32_t dof, int64_t V, int32_t C, void* stream) {
+  if (!src || !dst) return fail("copy_channels: null pointer");
+  if (V < 1 || C < 1 || so < 0 || dof < 0 || so + C > sp || dof + C > dp)
+    return fail("copy_channels: bad shape");
+  const int64_t n = V * C;
+  hipLaunchKernelGGL(copy_channels_kernel, dim3(grid_cap(n, 256, 8192)), dim3(256), 0,
+                     as_stream(stream), (const f16*)src, sp, so, (f16*)dst, dp, dof, V, C);
+  return check_launch("copy_channels");
+}
+
+extern "C" int ldx_upsample_nearest2(const void* x, int64_t xp, int32_t B, int32_t D, int32_t H,
+                                     int32_t W, int32_t C, void* y, int64_t yp, void* stream) {
+  if (!x || !y) return fail("upsample_nearest2: null pointer");
+  if (B < 1 || D < 1 || H < 1 || W < 1 || C < 1 || xp < C || yp < C)
+    return fail("upsample_nearest2: bad shape");
+  const int64_t n = (int64_t)B * 8 * D * H * W * C;
+  hipLaunchKernelGGL(upsample2_kernel, dim3(grid_cap(n, 256, 16384)), dim3(256), 0,
+                     as_stream(stream), (const f16*)x, xp, B, D, H, W, C, (f16*)y, yp);
+  return check_launch("upsample_nearest2");
+}
+
+extern "C" int ldx_ddim_prepare(float* x, const float* cond, const float* mask, int64_t V, int32_t C,
+                                int32_t CC, void* net, int64_t np, void* stream) {
+  if (!x || !cond || !net) return fail("ddim_prepare: null pointer");
+  if (V < 1 || C < 1 || CC < 0) return fail("ddim_prepare: bad shape");
+  if (mask && CC != 0 && CC != C) return fail("ddim_prepare: masked cond channels must be 0 or C");
+  const int64_t need = mask ? (int64_t)C + CC + 1 : (int64_t)C + CC;
+  if (np < need) return fail("ddim_prepare: pitch %lld < %lld", (long long)np, (long long)need);
+  hipLaunchKernelGGL(ddim_prepare_kernel, dim3(grid_cap(V, 256, 4096)), dim3(256), 0,
+                     as_stream(stream), x, cond, mask, V, C, CC, (f16*)net, np);
+  return check_launch("ddim_prepare");
+}
+
+extern "C" int ldx_ddim_update(float* x, const void* net, int64_t np, const float* noise,
+                               const float* coef, int64_t V, int32_t C, void* stream) {
+  if (!x || !net || !noise || !coef) return fail("ddim_update: null pointer");
+  if (V < 1 || C < 1 || np < C) return fail("ddim_update: bad shape");
+  const int64_t n = V * C;
+  hipLaunchKernelGGL(ddim_update_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
+                     as_stream(stream), x, (const f16*)net, np, noise, coef, V, C);
+  return check_launch("ddim_update");
+}

@@ -1,0 +1,403 @@
+"""Op-level API over ``libldx.so``: the drop-in replacements for the reference's
+``nax_conv3d`` / ``pack_weight`` / ``pack_upsample_weight`` / ``conv3d_ncdhw`` /
+``flash_attention`` / ``mx.fast.scaled_dot_product_attention`` /
+``group_norm_affine`` / ``mx.fast.layer_norm``.
+
+Tensors are ``torch`` CUDA (HIP) tensors used only as device memory; every op runs a
+hand-written gfx950 kernel through the C ABI on torch's current stream. Activations
+are channels-last NDHWC ``(B, D, H, W, C)`` float16, optionally a channel slice of a
+wider tensor (the voxel pitch is read from the strides). Argument errors raise
+``ValueError`` before anything is launched; HIP errors raise ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import ACT_GELU, ACT_NONE, AttnArgs, ConvArgs, check, lib
+
+__all__ = [
+    "PackedWeight", "pack_weight", "pack_upsample_weight", "nax_conv3d", "conv3d", "dense",
+    "group_norm_affine", "layer_norm", "attention", "flash_attention", "timestep_embedding",
+    "silu", "upsample_nearest2", "resize_nearest", "output_extent",
+]
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _require_cuda(t: torch.Tensor, name: str, dtype: torch.dtype | None = torch.float16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor (got {t.device}); there is no CPU path")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def voxel_pitch(x: torch.Tensor, name: str = "x") -> int:
+    """Voxel pitch (elements) of an NDHWC tensor whose voxels are evenly spaced and
+    whose channels are contiguous -- a contiguous tensor or a channel slice of one."""
+    if x.dim() != 5:
+        raise ValueError(f"{name} must be NDHWC (B, D, H, W, C), got shape {tuple(x.shape)}")
+    b, d, h, w, c = x.shape
+    st = x.stride()
+    if c > 1 and st[4] != 1:
+        raise ValueError(f"{name}: channels must be contiguous")
+    pitch = st[3] if w > 1 else (st[2] // max(w, 1) if h > 1 else (st[1] // (h * w) if d > 1 else (
+        st[0] // (d * h * w) if b > 1 else c)))
+    if pitch < c:
+        raise ValueError(f"{name}: voxel pitch {pitch} < channels {c}")
+    if ((w > 1 and st[3] != pitch) or (h > 1 and st[2] != w * pitch)
+            or (d > 1 and st[1] != h * w * pitch) or (b > 1 and st[0] != d * h * w * pitch)):
+        raise ValueError(f"{name}: voxels must be evenly spaced (strides {st})")
+    return int(pitch)
+
+
+def output_extent(n: int, *, stride: int = 1, upsample: bool = False) -> int:
+    """``n`` (stride 1), ``(n - 1) // 2 + 1`` (stride 2), ``2 n`` (upsample)
+    (_nax_conv.py:513-516, 552)."""
+    if upsample:
+        return 2 * n
+    if stride == 1:
+        return n
+    if stride == 2:
+        return (n - 1) // 2 + 1
+    raise ValueError("stride must be 1 or 2")
+
+
+# ------------------------------------------------------------------ weights
+
+@dataclass
+class PackedWeight:
+    """A conv/dense weight in the kernel layout: ``(O, K^3, C)`` or, folded for a
+    nearest-2x-upsampled conv, ``(8, O, 8, C)``."""
+
+    data: torch.Tensor
+    out_channels: int
+    in_channels: int
+    ksize: int
+    upsample: bool = False
+
+
+def pack_weight(weight: torch.Tensor) -> PackedWeight:
+    """Pack a Torch-layout ``(O, C, K, K, K)`` (K = 1 or 3) or dense ``(O, C)`` fp16
+    weight (the reference's ``pack_weight``, _nax_conv.py:350-364, in this library's
+    layout)."""
+    _require_cuda(weight, "weight")
+    if weight.dim() == 2:
+        weight = weight.reshape(*weight.shape, 1, 1, 1)
+    if weight.dim() != 5 or weight.shape[2] != weight.shape[3] or weight.shape[3] != weight.shape[4] \
+            or weight.shape[2] not in (1, 3):
+        raise ValueError(f"weight must be (O, C, K, K, K) with K in (1, 3), got {tuple(weight.shape)}")
+    o, c, k = int(weight.shape[0]), int(weight.shape[1]), int(weight.shape[2])
+    w = weight.contiguous()
+    out = torch.empty((o, k ** 3, c), dtype=torch.float16, device=weight.device)
+    check(lib.ldx_pack_weight(_ptr(w), o, c, k, _ptr(out), _stream()), "pack_weight")
+    return PackedWeight(out, o, c, k, False)
+
+
+def pack_upsample_weight(weight: torch.Tensor) -> PackedWeight:
+    """Fold a ``(O, C, 3, 3, 3)`` fp16 weight into 8 parity 2x2x2 filters for a conv of a
+    nearest 2x upsampling (_nax_conv.py:367-405)."""
+    _require_cuda(weight, "weight")
+    if weight.dim() != 5 or tuple(weight.shape[2:]) != (3, 3, 3):
+        raise ValueError(f"weight must be (O, C, 3, 3, 3), got {tuple(weight.shape)}")
+    o, c = int(weight.shape[0]), int(weight.shape[1])
+    w = weight.contiguous()
+    out = torch.empty((8, o, 8, c), dtype=torch.float16, device=weight.device)
+    check(lib.ldx_pack_upsample_weight(_ptr(w), o, c, _ptr(out), _stream()), "pack_upsample_weight")
+    return PackedWeight(out, o, c, 3, True)
+
+
+def _bias32(bias: torch.Tensor | None, batch: int, out_c: int) -> tuple[torch.Tensor | None, int]:
+    if bias is None:
+        return None, 0
+    if not bias.is_cuda:
+        raise ValueError("bias must be a device tensor")
+    if bias.shape[-1] != out_c or bias.dim() not in (1, 2) or (bias.dim() == 2 and bias.shape[0] != batch):
+        raise ValueError(f"bias shape {tuple(bias.shape)} does not fit ({batch}, {out_c})")
+    return bias.to(torch.float32).contiguous(), int(bias.dim() == 2)
+
+
+# ------------------------------------------------------------------ conv3d
+
+def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = None, *,
+               affine: torch.Tensor | None = None, silu: bool = False, stride: int = 1,
+               upsample: bool = False, output_scale: float = 1.0,
+               residual: torch.Tensor | None = None, x1: torch.Tensor | None = None,
+               act: str | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused conv of NDHWC ``x`` (optionally ``concat([x, x1], channels)``) with a packed
+    weight: ``half((conv(prep(x)) + bias) * output_scale + residual)``, ``prep`` = the
+    per-(b, c) ``affine`` then SiLU, rounded to fp16 once (nax_conv3d,
+    _nax_conv.py:451-500). ``act="gelu"`` additionally stores ``half(gelu(y))``.
+
+    Returns NDHWC ``(B, D', H', W', O)`` fp16 (written into ``out`` when given, which may
+    be a channel slice of a wider tensor).
+    """
+    _require_cuda(x, "x")
+    xp = voxel_pitch(x, "x")
+    b, d, h, w, c0 = (int(s) for s in x.shape)
+    c1, x1p = 0, 0
+    if x1 is not None:
+        _require_cuda(x1, "x1")
+        x1p = voxel_pitch(x1, "x1")
+        if tuple(x1.shape[:4]) != (b, d, h, w):
+            raise ValueError(f"x1 grid {tuple(x1.shape[:4])} != x grid {(b, d, h, w)}")
+        c1 = int(x1.shape[4])
+    if packed.in_channels != c0 + c1:
+        raise ValueError(f"packed weight expects {packed.in_channels} input channels, got {c0 + c1}")
+    if packed.upsample != bool(upsample):
+        raise ValueError("upsample convs need pack_upsample_weight weights (and only they)")
+    if packed.ksize == 1 and (stride != 1 or upsample):
+        raise ValueError("pointwise conv supports stride 1 only")
+    o = packed.out_channels
+    if upsample:
+        grid = (2 * d, 2 * h, 2 * w)
+    elif packed.ksize == 3:
+        grid = tuple(output_extent(n, stride=stride) for n in (d, h, w))
+    else:
+        grid = (d, h, w)
+    bias32, batched = _bias32(bias, b, o)
+    aff = None
+    if affine is not None:
+        if affine.dtype != torch.float32 or not affine.is_cuda or affine.numel() != b * (c0 + c1) * 2:
+            raise ValueError("affine must be device float32 with batch * C * 2 values")
+        aff = affine.contiguous()
+    resp = 0
+    if residual is not None:
+        _require_cuda(residual, "residual")
+        if tuple(residual.shape) != (b, *grid, o):
+            raise ValueError(f"residual shape {tuple(residual.shape)} != output {(b, *grid, o)}")
+        resp = voxel_pitch(residual, "residual")
+    if out is None:
+        out = torch.empty((b, *grid, o), dtype=torch.float16, device=x.device)
+    else:
+        _require_cuda(out, "out")
+        if tuple(out.shape) != (b, *grid, o):
+            raise ValueError(f"out shape {tuple(out.shape)} != {(b, *grid, o)}")
+    yp = voxel_pitch(out, "out")
+    a = ConvArgs()
+    a.batch, a.in_d, a.in_h, a.in_w = b, d, h, w
+    a.c0, a.c1, a.out_c = c0, c1, o
+    a.ksize, a.stride, a.upsample = packed.ksize, stride, int(bool(upsample))
+    a.x0, a.x0_pitch = x.data_ptr(), xp
+    a.x1, a.x1_pitch = (x1.data_ptr() if x1 is not None else None), x1p
+    a.weight = packed.data.data_ptr()
+    a.bias, a.bias_batched = (bias32.data_ptr() if bias32 is not None else None), batched
+    a.affine, a.silu = (aff.data_ptr() if aff is not None else None), int(bool(silu))
+    a.residual, a.residual_pitch = (residual.data_ptr() if residual is not None else None), resp
+    a.output_scale = float(output_scale)
+    a.act = {None: ACT_NONE, "gelu": ACT_GELU}[act]
+    a.y, a.y_pitch = out.data_ptr(), yp
+    check(lib.ldx_conv3d(ctypes.byref(a), _stream()), "conv3d")
+    return out
+
+
+def conv3d(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
+           stride: int = 1, padding: int | None = None) -> torch.Tensor:
+    """The reference's op-level ``conv3d(x, w, b, stride, pad)`` on NDHWC ``x`` with a
+    Torch-layout ``(O, C, K, K, K)`` weight: K = 3 with padding 1, or K = 1 with
+    padding 0 (mlx_model.py:159-202). Packs the weight on each call; modules prepack."""
+    k = int(weight.shape[2]) if weight.dim() == 5 else 1
+    pad = k // 2 if padding is None else padding
+    if pad != k // 2:
+        raise ValueError(f"only padding {k // 2} is supported for a {k}x{k}x{k} kernel")
+    return nax_conv3d(x, pack_weight(weight), bias, stride=stride)
+
+
+def dense(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = None, *,
+          residual: torch.Tensor | None = None, act: str | None = None,
+          out: torch.Tensor | None = None) -> torch.Tensor:
+    """``half(x @ W^T + bias (+ residual))`` over the last axis of fp16 ``x`` with fp32
+    accumulation and one rounding (SourceLayers.dense native path, mlx_model.py:204-217)."""
+    if packed.ksize != 1:
+        raise ValueError("dense needs a (O, C) weight packed with pack_weight")
+    lead = x.shape[:-1]
+    rows = math.prod(lead)
+    x5 = x.reshape(1, 1, 1, rows, x.shape[-1])
+    r5 = None if residual is None else residual.reshape(1, 1, 1, rows, packed.out_channels)
+    o5 = None if out is None else out.reshape(1, 1, 1, rows, packed.out_channels)
+    y = nax_conv3d(x5, packed, bias, residual=r5, act=act, out=o5)
+    return y.reshape(*lead, packed.out_channels)
+
+
+# ------------------------------------------------------------ normalisation
+
+def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, *, groups: int,
+                      eps: float, x1: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-(b, c) ``(scale, offset)`` fp32 ``(B, C, 2)`` of GroupNorm over NDHWC ``x``
+    (optionally ``concat([x, x1])``), ``scale = gamma * rsqrt(var + eps)``, ``offset =
+    beta - scale * mean`` (medmlx_core group_norm_affine; mlx_model.py:328-335)."""
+    _require_cuda(x, "x")
+    xp = voxel_pitch(x, "x")
+    b, d, h, w, c0 = (int(s) for s in x.shape)
+    c1, x1p = 0, 0
+    if x1 is not None:
+        _require_cuda(x1, "x1")
+        x1p = voxel_pitch(x1, "x1")
+        c1 = int(x1.shape[4])
+    c = c0 + c1
+    if c % groups:
+        raise ValueError(f"groups {groups} must divide channels {c}")
+    g32 = gamma.to(torch.float32).contiguous()
+    b32 = beta.to(torch.float32).contiguous()
+    voxels = d * h * w
+    ws = torch.empty(max(1, lib.ldx_group_norm_workspace_bytes(b, voxels, c, groups)),
+                     dtype=torch.uint8, device=x.device)
+    out = torch.empty((b, c, 2), dtype=torch.float32, device=x.device)
+    check(lib.ldx_group_norm_affine(_ptr(x), xp, c0, _ptr(x1), x1p, c1, b, voxels, groups,
+                                    _ptr(g32), _ptr(b32), float(eps), _ptr(out), _ptr(ws), _stream()),
+          "group_norm_affine")
+    return out
+
+
+def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """LayerNorm over the last axis of fp16 ``x`` (mx.fast.layer_norm, mlx_model.py:360-367)."""
+    _require_cuda(x, "x")
+    f = int(x.shape[-1])
+    x2 = x.reshape(-1, f)
+    if x2.stride(-1) != 1:
+        raise ValueError("layer_norm: features must be contiguous")
+    if out is None:
+        out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+    o2 = out.reshape(-1, f)
+    check(lib.ldx_layer_norm(_ptr(x2), x2.stride(0), x2.shape[0], f,
+                             _ptr(gamma.to(torch.float32).contiguous()),
+                             _ptr(beta.to(torch.float32).contiguous()), float(eps),
+                             _ptr(o2), o2.stride(0), _stream()), "layer_norm")
+    return out
+
+
+# ----------------------------------------------------------------- attention
+
+def _attn_args(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, o4: torch.Tensor,
+               scale: float, mask: torch.Tensor | None) -> AttnArgs:
+    """Build the C arguments from (B, L, H, D) views."""
+    a = AttnArgs()
+    b, lq, h, d = (int(s) for s in q4.shape)
+    a.batch, a.heads, a.q_len, a.kv_len, a.head_dim = b, h, lq, int(k4.shape[1]), d
+    for name, t in (("q", q4), ("k", k4), ("v", v4), ("o", o4)):
+        if t.stride(3) != 1:
+            raise ValueError(f"attention: {name} head_dim must be contiguous")
+        setattr(a, name, t.data_ptr())
+        getattr(a, name + "_stride")[:] = [t.stride(0), t.stride(1), t.stride(2)]
+    a.scale = float(scale)
+    a.mask = None
+    if mask is not None:
+        a.mask = mask.data_ptr()
+        a.mask_stride[:] = [mask.stride(0), mask.stride(1), mask.stride(2), mask.stride(3)]
+    return a
+
+
+def _prepare_mask(mask: torch.Tensor | None, b: int, h: int, lq: int, lk: int,
+                  device: torch.device) -> torch.Tensor | None:
+    if mask is None:
+        return None
+    if not mask.is_cuda:
+        raise ValueError("mask must be a device tensor")
+    if mask.dtype == torch.bool:
+        mask = torch.zeros(mask.shape, dtype=torch.float32, device=device).masked_fill(~mask, -math.inf)
+    mask = mask.to(torch.float32)
+    while mask.dim() < 4:
+        mask = mask.unsqueeze(0)
+    return mask.expand(b, h, lq, lk)
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
+              mask: torch.Tensor | None = None) -> torch.Tensor:
+    """``softmax(q k^T * scale + mask) v`` for fp16 ``(B, H, L, D)`` tensors, the contract
+    of ``mx.fast.scaled_dot_product_attention`` (mlx_model.py:485-487, 860-862). ``mask``
+    is additive (``-inf`` removes a key) or boolean (``True`` keeps a key), broadcast to
+    ``(B, H, L, LK)``. Returns ``(B, H, L, D)``."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_cuda(t, name)
+        if t.dim() != 4:
+            raise ValueError(f"{name} must be (B, H, L, D)")
+    b, h, lq, d = (int(s) for s in q.shape)
+    lk = int(k.shape[2])
+    if tuple(k.shape) != (b, h, lk, d) or tuple(v.shape) != (b, h, lk, d):
+        raise ValueError(f"k/v shapes {tuple(k.shape)}, {tuple(v.shape)} do not fit q {tuple(q.shape)}")
+    out = torch.empty((b, h, lq, d), dtype=torch.float16, device=q.device)
+    m = _prepare_mask(mask, b, h, lq, lk, q.device)
+    a = _attn_args(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2), scale, m)
+    check(lib.ldx_attention(ctypes.byref(a), _stream()), "attention")
+    return out
+
+
+def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads: int, scale: float,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """Multi-head attention on head-interleaved projections ``(B, L, heads * d)``
+    (head ``h`` = columns ``h*d .. h*d+d-1``), returning that layout
+    (flash_attention, _attention.py:331-351). Key length may differ from query length."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _require_cuda(t, name)
+        if t.dim() != 3:
+            raise ValueError(f"{name} must be (B, L, heads * d)")
+    b, lq, f = (int(s) for s in q.shape)
+    if f % heads:
+        raise ValueError(f"features {f} not divisible by heads {heads}")
+    d = f // heads
+    lk = int(k.shape[1])
+    if tuple(k.shape) != (b, lk, f) or tuple(v.shape) != (b, lk, f):
+        raise ValueError("k/v must be (B, LK, heads * d) matching q")
+    if out is None:
+        out = torch.empty((b, lq, f), dtype=torch.float16, device=q.device)
+    a = _attn_args(q.view(b, lq, heads, d) if q.is_contiguous() else q.unflatten(2, (heads, d)),
+                   k.unflatten(2, (heads, d)), v.unflatten(2, (heads, d)), out.unflatten(2, (heads, d)),
+                   scale, None)
+    check(lib.ldx_attention(ctypes.byref(a), _stream()), "attention")
+    return out
+
+
+# ---------------------------------------------------------------- small ops
+
+def timestep_embedding(timesteps: torch.Tensor, channels: int) -> torch.Tensor:
+    """fp16 ``[cos(t f), sin(t f)]`` (mlx_model.py:609-612) for int32 ``timesteps``."""
+    _require_cuda(timesteps, "timesteps", torch.int32)
+    t = timesteps.contiguous()
+    out = torch.empty((t.shape[0], channels), dtype=torch.float16, device=t.device)
+    check(lib.ldx_timestep_embedding(_ptr(t), t.shape[0], channels, _ptr(out), _stream()),
+          "timestep_embedding")
+    return out
+
+
+def silu(x: torch.Tensor) -> torch.Tensor:
+    """``half(silu(float(x)))`` (LdmUnet.silu, mlx_model.py:409-413)."""
+    _require_cuda(x, "x")
+    xc = x.contiguous()
+    out = torch.empty_like(xc)
+    check(lib.ldx_silu(_ptr(xc), xc.numel(), _ptr(out), _stream()), "silu")
+    return out
+
+
+def upsample_nearest2(x: torch.Tensor) -> torch.Tensor:
+    """Nearest 2x upsampling of NDHWC ``x`` (_spatial.py:41-57)."""
+    _require_cuda(x, "x")
+    xp = voxel_pitch(x)
+    b, d, h, w, c = (int(s) for s in x.shape)
+    out = torch.empty((b, 2 * d, 2 * h, 2 * w, c), dtype=torch.float16, device=x.device)
+    check(lib.ldx_upsample_nearest2(_ptr(x), xp, b, d, h, w, c, _ptr(out), c, _stream()),
+          "upsample_nearest2")
+    return out
+
+
+def resize_nearest(x: torch.Tensor, shape: tuple[int, int, int]) -> torch.Tensor:
+    """Nearest resize of NDHWC ``x`` to spatial ``shape``; only the factor-two case the
+    model uses runs on the device (_spatial.py:60-69)."""
+    if len(shape) != 3:
+        raise ValueError("nearest resizing needs three spatial axes")
+    if tuple(shape) == tuple(2 * int(s) for s in x.shape[1:4]):
+        return upsample_nearest2(x)
+    raise ValueError("only nearest 2x resizing is supported")

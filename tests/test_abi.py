@@ -1,0 +1,124 @@
+"""The C ABI on the CPU: libldx.so loads, exports every function ``include/ldx.h``
+declares, the ctypes structs match the C layout, and argument errors are rejected
+before any device work (no GPU needed)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from tests.conftest import REPO
+
+HEADER = REPO / "include" / "ldx.h"
+
+
+def declared_functions() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ldx_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(pkg) -> None:
+    names = declared_functions()
+    assert len(names) >= 14
+    out = subprocess.run(["nm", "-D", "--defined-only", str(pkg._lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\b(ldx_[a-z0-9_]+)\b", out))
+    missing = [n for n in names if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    assert set(names) == set(pkg._lib.SIGNATURES), "ctypes signature table out of sync with ldx.h"
+
+
+def test_ctypes_structs_match_c_layout(pkg, tmp_path) -> None:
+    lib = pkg._lib
+    fields = {"ldx_conv3d_args": lib.ConvArgs, "ldx_attention_args": lib.AttnArgs}
+    src = ["#include <stdio.h>", "#include <stddef.h>", '#include "ldx.h"', "int main(void) {"]
+    for cname, cls in fields.items():
+        src.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for fname, _ in cls._fields_:
+            src.append(f'printf("{cname} {fname} %zu\\n", offsetof({cname}, {fname}));')
+    src.append("return 0; }")
+    c = tmp_path / "layout.c"
+    c.write_text("\n".join(src))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(REPO / "include"), str(c), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split("\n")
+    for line in filter(None, got):
+        cname, what, val = line.split()
+        cls = fields[cname]
+        want = ctypes.sizeof(cls) if what == "size" else getattr(cls, what).offset
+        assert int(val) == want, f"{cname}.{what}: C {val} != ctypes {want}"
+
+
+def test_abi_version(pkg) -> None:
+    assert pkg._lib.lib.ldx_abi_version() == pkg._lib.ABI_VERSION
+
+
+def _conv_args(lib, **kw):
+    a = lib.ConvArgs()
+    a.batch, a.in_d, a.in_h, a.in_w = 1, 4, 4, 4
+    a.c0, a.c1, a.out_c, a.ksize, a.stride = 8, 0, 8, 3, 1
+    a.x0, a.x0_pitch, a.weight, a.y, a.y_pitch = 16, 8, 16, 16, 8
+    a.output_scale = 1.0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("bad", [
+    {"ksize": 5}, {"stride": 3}, {"batch": 0}, {"in_d": 0}, {"c0": 0}, {"out_c": 0},
+    {"ksize": 1, "stride": 2}, {"upsample": 1, "stride": 2}, {"x0": None}, {"weight": None},
+    {"c1": 8}, {"x0_pitch": 4}, {"y_pitch": 4}, {"act": 7}, {"residual": 16, "residual_pitch": 2},
+])
+def test_conv3d_rejects_bad_arguments_before_launch(pkg, bad) -> None:
+    lib = pkg._lib
+    a = _conv_args(lib, **bad)
+    rc = lib.lib.ldx_conv3d(ctypes.byref(a), None)
+    assert rc == lib.LDX_EINVAL
+    assert "conv3d" in lib.last_error()
+
+
+def test_attention_rejects_bad_arguments_before_launch(pkg) -> None:
+    lib = pkg._lib
+    a = lib.AttnArgs()
+    a.batch, a.heads, a.q_len, a.kv_len, a.head_dim = 1, 1, 8, 8, 48
+    a.q = a.k = a.v = a.o = 256
+    assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
+    assert "head_dim" in lib.last_error()
+    a.head_dim = 64
+    a.q_stride[1] = 12
+    assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
+    a.q_stride[1] = 64
+    a.kv_len = 0
+    assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
+
+
+def test_small_ops_reject_bad_arguments(pkg) -> None:
+    l = pkg._lib.lib
+    E = pkg._lib.LDX_EINVAL
+    assert l.ldx_pack_weight(16, 0, 4, 3, 16, None) == E
+    assert l.ldx_pack_weight(16, 4, 4, 2, 16, None) == E
+    assert l.ldx_pack_upsample_weight(None, 4, 4, 16, None) == E
+    assert l.ldx_group_norm_affine(16, 8, 12, None, 0, 0, 1, 10, 5, 16, 16, 1e-5, 16, 16, None) == E
+    assert l.ldx_layer_norm(16, 8, 1, 2000, 16, 16, 1e-5, 16, 2000, None) == E
+    assert l.ldx_timestep_embedding(16, 1, 7, 16, None) == E
+    assert l.ldx_copy_channels(16, 8, 4, 16, 8, 0, 10, 8, None) == E
+    assert l.ldx_ddim_prepare(16, 16, 16, 10, 4, 2, 16, 9, None) == E
+    assert l.ldx_upsample_nearest2(16, 2, 1, 1, 1, 1, 4, 16, 4, None) == E
+    assert l.ldx_group_norm_workspace_bytes(0, 10, 8, 2) == 0
+    assert l.ldx_group_norm_workspace_bytes(1, 51200, 64, 32) > 0
+
+
+def test_ops_fail_loudly_on_cpu_tensors(pkg) -> None:
+    import torch
+
+    x = torch.zeros((1, 2, 2, 2, 8), dtype=torch.float16)
+    w = torch.zeros((8, 8, 3, 3, 3), dtype=torch.float16)
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.ops.conv3d(x, w)
+    with pytest.raises(ValueError, match="no CPU path"):
+        pkg.ops.attention(torch.zeros(1, 1, 4, 64, dtype=torch.float16),
+                          torch.zeros(1, 1, 4, 64, dtype=torch.float16),
+                          torch.zeros(1, 1, 4, 64, dtype=torch.float16), 0.125)

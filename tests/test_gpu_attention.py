@@ -1,0 +1,95 @@
+"""Flash-attention parity on the MI355X against the float64 softmax oracle
+(tests/test_native_kernels.py:380-450: fp16 atol = rtol = 2e-3) and the fp16 bar."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from tests.conftest import assert_fp16_bar
+
+pytestmark = pytest.mark.gpu
+
+
+def to_dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def host(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+@pytest.mark.parametrize(("batch", "length", "heads", "ties"), [
+    (2, 32, 1, False), (1, 96, 2, False), (1, 96, 2, True), (1, 1056, 2, False),
+    (1, 512, 4, False), (1, 512, 8, False), (1, 512, 16, False),
+])
+def test_projection_layout_head32_matches_float64(pkg, dev, batch, length, heads, ties) -> None:
+    """The reference's nax-half cases (tests/test_native_kernels.py:395-450): inputs
+    q, k * 2, v * 1 from rng(length + keys), head-interleaved (B, L, heads * 32)."""
+    rng = np.random.default_rng(length + length)
+    q, k, v = (rng.normal(size=(batch, length, heads * 32)) * s for s in (2.0, 2.0, 1.0))
+    if ties:
+        q = np.zeros_like(q)
+    q, k, v = (a.astype(np.float16) for a in (q, k, v))
+    out = pkg.ops.flash_attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), heads=heads,
+                                  scale=32 ** -0.5)
+    torch.cuda.synchronize()
+    exp = oatt.attention_projected(q.astype(np.float64), k.astype(np.float64), v.astype(np.float64),
+                                   heads, 32 ** -0.5)
+    act = host(out)
+    assert out.dtype == torch.float16 and np.all(np.isfinite(act))
+    np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
+
+
+@pytest.mark.parametrize(("b", "h", "lq", "lk", "d"), [
+    (1, 8, 1600, 1600, 64),   # config 2 self-attention
+    (1, 8, 1600, 77, 64),     # config 2 cross-attention
+    (2, 4, 100, 77, 32),      # LINet lowest-level cross attention
+    (1, 2, 64, 64, 16),       # the fixture UNet's 16-wide heads
+    (1, 1, 300, 300, 256),    # VQ mid attention head width
+    (1, 2, 129, 200, 128),
+    (2, 3, 1, 5, 64),         # single query, ragged keys
+])
+def test_attention_matches_float64(pkg, dev, b, h, lq, lk, d) -> None:
+    rng = np.random.default_rng(lq * 7 + lk + d)
+    q = rng.normal(size=(b, h, lq, d)).astype(np.float16)
+    k = rng.normal(size=(b, h, lk, d)).astype(np.float16)
+    v = rng.normal(size=(b, h, lk, d)).astype(np.float16)
+    out = pkg.ops.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), d ** -0.5)
+    torch.cuda.synchronize()
+    exp = oatt.attention(q, k, v, d ** -0.5)
+    act = host(out)
+    np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
+    assert_fp16_bar(act, exp)
+
+
+def test_attention_additive_and_boolean_masks(pkg, dev) -> None:
+    """Additive -inf / boolean key masks (mlx_model.py:843-847); a fully masked row is 0."""
+    rng = np.random.default_rng(3)
+    b, h, lq, lk, d = 2, 3, 40, 77, 64
+    q, k, v = (rng.normal(size=(b, h, n, d)).astype(np.float16) for n in (lq, lk, lk))
+    keep = rng.random((b, 1, 1, lk)) > 0.3
+    keep[..., 0] = True
+    add = np.where(keep, 0.0, -np.inf).astype(np.float32)
+    add2 = add + rng.normal(size=(b, 1, lq, lk)).astype(np.float32)  # general additive bias
+    for m_host, m_dev in ((add, to_dev(keep, dev)), (add2, to_dev(add2, dev))):
+        out = pkg.ops.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), 0.125, m_dev)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(host(out), oatt.attention(q, k, v, 0.125, m_host), rtol=2e-3, atol=2e-3)
+    none = np.zeros((b, 1, lq, lk), bool)
+    out = pkg.ops.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), 0.125, to_dev(none, dev))
+    torch.cuda.synchronize()
+    assert np.all(host(out) == 0)
+
+
+def test_attention_large_magnitudes_keep_running_max(pkg, dev) -> None:
+    """Peaked rows whose maximum moves across key tiles."""
+    rng = np.random.default_rng(5)
+    q = (rng.normal(size=(1, 2, 200, 64)) * 3).astype(np.float16)
+    k = (rng.normal(size=(1, 2, 700, 64)) * 3).astype(np.float16)
+    v = rng.normal(size=(1, 2, 700, 64)).astype(np.float16)
+    out = pkg.ops.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), 0.125)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(host(out), oatt.attention(q, k, v, 0.125), rtol=2e-3, atol=2e-3)

@@ -1,0 +1,239 @@
+"""conv3d parity on the MI355X: the HIP implicit-GEMM kernel against the float64
+oracle, at the reference's own error model (tests/test_native_kernels.py:37-39, 98-104:
+``|err| <= 1/2 ulp_fp16 + 8 * 2^-23 * sum|terms|`` (+ ``2^-11 * sum|terms|`` for a
+re-rounded operand)) and the fp16 bar (max abs <= 2e-2, rel L2 <= 1e-3)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import conv as ocv
+from oracle import norm as onm
+from tests.conftest import ACCUMULATION_EPS, OPERAND_ROUNDING, assert_fp16_bar, half_spacing
+
+pytestmark = pytest.mark.gpu
+
+
+def ndhwc(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a.transpose(0, 2, 3, 4, 1))
+
+
+def ncdhw(a: np.ndarray) -> np.ndarray:
+    return np.ascontiguousarray(a.transpose(0, 4, 1, 2, 3))
+
+
+def case(shape, out_c, k, seed):
+    """Seeded fp16 case (tests/test_native_kernels.py:52-67): x ~ N(0,1) NCDHW, weight
+    ~ N(0, 1/(C k^3)), bias ~ N(0, 0.1^2)."""
+    rng = np.random.default_rng(seed)
+    c = shape[1]
+    x = rng.normal(size=shape).astype(np.float16)
+    w = (rng.normal(size=(out_c, c, k, k, k)) * (c * k ** 3) ** -0.5).astype(np.float16)
+    b = (rng.normal(size=(out_c,)) * 0.1).astype(np.float16)
+    return x, w, b
+
+
+def to_dev(a, dev, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    return t if dtype is None else t.to(dtype)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def check_single_rounding(actual_ndhwc, x, w, b, stride=1, extra_operand_rounding=False):
+    expected = ocv.conv3d(x, w, b, stride=stride)
+    mag = ocv.conv3d_magnitude(x, w, b, stride=stride)
+    actual = ncdhw(actual_ndhwc)
+    err = np.abs(actual - expected)
+    bound = half_spacing(expected) + (ACCUMULATION_EPS + (OPERAND_ROUNDING if extra_operand_rounding else 0)) * mag
+    assert np.all(err <= bound), f"max excess {np.max(err - bound):.3e}"
+    assert_fp16_bar(actual, expected)
+
+
+@pytest.mark.parametrize(("shape", "out_c", "stride"), [
+    ((1, 16, 5, 7, 9), 32, 1),   # odd extents
+    ((2, 32, 4, 6, 3), 128, 1),  # batched, 128 outputs
+    ((1, 48, 9, 3, 5), 64, 1),
+    ((1, 5, 6, 4, 7), 4, 1),     # C and O not multiples of 8 (scalar path)
+    ((2, 24, 7, 6, 9), 40, 2),   # stride 2, odd and even extents
+    ((1, 512, 4, 4, 4), 128, 1),  # large C, few bricks
+    ((1, 64, 32, 40, 40), 64, 1),  # config 1
+    ((1, 9, 8, 10, 10), 64, 1),   # 9-channel network input
+    ((1, 64, 8, 10, 10), 1, 1),   # single output channel
+    ((1, 256, 4, 5, 5), 256, 1),
+    ((1, 128, 8, 10, 10), 128, 2),
+])
+def test_conv3d_matches_float64_and_rounds_once(pkg, dev, shape, out_c, stride) -> None:
+    """tests/test_native_kernels.py:143-168, plus the config shapes."""
+    x, w, b = case(shape, out_c, 3, sum(shape))
+    y = pkg.ops.conv3d(to_dev(ndhwc(x), dev), to_dev(w, dev), to_dev(b, dev), stride=stride)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float16
+    ext = tuple(ocv.output_extent(n, stride=stride) for n in shape[2:])
+    assert tuple(y.shape) == (shape[0], *ext, out_c)
+    check_single_rounding(host(y), x.astype(np.float64), w.astype(np.float64), b.astype(np.float64), stride)
+
+
+def test_conv3d_reads_a_strided_channel_slice(pkg, dev) -> None:
+    """A channel slice of a wider NDHWC tensor (voxel pitch > C), as a view, not a copy."""
+    x, w, b = case((1, 32, 5, 6, 7), 48, 3, 3)
+    wide = np.zeros((1, 5, 6, 7, 72), np.float16)
+    wide[..., 16:48] = ndhwc(x)
+    xt = to_dev(wide, dev)[..., 16:48]
+    out_wide = torch.zeros((1, 5, 6, 7, 64), dtype=torch.float16, device=dev)
+    pk = pkg.ops.pack_weight(to_dev(w, dev))
+    pkg.ops.nax_conv3d(xt, pk, to_dev(b, dev), out=out_wide[..., 8:56])
+    torch.cuda.synchronize()
+    o = host(out_wide)
+    assert np.all(o[..., :8] == 0) and np.all(o[..., 56:] == 0)
+    check_single_rounding(o[..., 8:56], x.astype(np.float64), w.astype(np.float64), b.astype(np.float64))
+
+
+def test_conv3d_two_input_concat(pkg, dev) -> None:
+    """concat([x, skip]) read from two tensors without forming it."""
+    x, w, b = case((2, 48, 4, 5, 6), 32, 3, 4)
+    a, s = x[:, :32], x[:, 32:]
+    pk = pkg.ops.pack_weight(to_dev(w, dev))
+    y = pkg.ops.nax_conv3d(to_dev(ndhwc(a), dev), pk, to_dev(b, dev), x1=to_dev(ndhwc(s), dev))
+    torch.cuda.synchronize()
+    check_single_rounding(host(y), x.astype(np.float64), w.astype(np.float64), b.astype(np.float64))
+
+
+@pytest.mark.parametrize("output_scale", [1.0, 0.25])
+@pytest.mark.parametrize("channels", [32, 512])
+def test_conv3d_batch_bias_residual_scale(pkg, dev, output_scale, channels) -> None:
+    """tests/test_native_kernels.py:171-193: ((conv + bias[b]) * scale + residual), one rounding."""
+    x, w, _ = case((2, channels, 4, 4, 4), 64, 3, channels)
+    rng = np.random.default_rng(1)
+    bias = rng.normal(size=(2, 64)).astype(np.float32)
+    res = rng.normal(size=(2, 64, 4, 4, 4)).astype(np.float16)
+    y = pkg.ops.nax_conv3d(to_dev(ndhwc(x), dev), pkg.ops.pack_weight(to_dev(w, dev)), to_dev(bias, dev),
+                           residual=to_dev(ndhwc(res), dev), output_scale=output_scale)
+    torch.cuda.synchronize()
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    products = ocv.conv3d(x64, w64)
+    mag = ocv.conv3d_magnitude(x64, w64)
+    expected = (products + bias.astype(np.float64)[:, :, None, None, None]) * output_scale + res
+    err = np.abs(ncdhw(host(y)) - expected)
+    assert np.all(err <= half_spacing(expected) + ACCUMULATION_EPS * mag * output_scale)
+
+
+@pytest.mark.parametrize("upsample", [False, True])
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_conv3d_scales_overflowing_branch_before_store(pkg, dev, upsample, with_residual) -> None:
+    """tests/test_native_kernels.py:113-140: a 75000 branch (beyond fp16) scaled by 0.25
+    before the single store, residual unscaled: exactly 18750 (+ 8192)."""
+    x = torch.zeros((1, 2, 2, 2, 16), dtype=torch.float16, device=dev)
+    w = torch.zeros((1, 16, 3, 3, 3), dtype=torch.float16, device=dev)
+    bias = torch.tensor([75000.0], dtype=torch.float32, device=dev)
+    sp = 4 if upsample else 2
+    res = torch.full((1, sp, sp, sp, 1), 8192.0, dtype=torch.float16, device=dev) if with_residual else None
+    pk = (pkg.ops.pack_upsample_weight if upsample else pkg.ops.pack_weight)(w)
+    y = pkg.ops.nax_conv3d(x, pk, bias, upsample=upsample, residual=res, output_scale=0.25)
+    torch.cuda.synchronize()
+    want = np.full((1, sp, sp, sp, 1), 75000.0 * 0.25 + (8192.0 if with_residual else 0), np.float16)
+    np.testing.assert_array_equal(host(y), want.astype(np.float64))
+
+
+@pytest.mark.parametrize("shape,out_c", [((2, 32, 3, 5, 4), 64), ((1, 256, 8, 10, 10), 256),
+                                         ((1, 128, 16, 20, 20), 128)])
+def test_upsample_conv_matches_conv_of_nearest_upsampling(pkg, dev, shape, out_c) -> None:
+    """tests/test_native_kernels.py:196-210: folded weights round merged taps once."""
+    x, w, b = case(shape, out_c, 3, 21)
+    y = pkg.ops.nax_conv3d(to_dev(ndhwc(x), dev), pkg.ops.pack_upsample_weight(to_dev(w, dev)),
+                           to_dev(b, dev), upsample=True)
+    torch.cuda.synchronize()
+    up = ocv.upsample_nearest2(x.astype(np.float64))
+    w64, b64 = w.astype(np.float64), b.astype(np.float64)
+    expected = ocv.conv3d(up, w64, b64)
+    mag = ocv.conv3d_magnitude(up, w64, b64)
+    actual = ncdhw(host(y))
+    assert actual.shape == expected.shape
+    err = np.abs(actual - expected)
+    assert np.all(err <= half_spacing(expected) + (ACCUMULATION_EPS + OPERAND_ROUNDING) * mag)
+    assert_fp16_bar(actual, expected)
+
+
+def test_pack_weight_layout_is_the_reference_layout_transposed(pkg, dev) -> None:
+    """Bit-exact: packed[o, tap, c] == reference_packed[tap * C' + c, o]."""
+    rng = np.random.default_rng(9)
+    w = rng.standard_normal((20, 5, 3, 3, 3)).astype(np.float16)
+    ours = pkg.ops.pack_weight(to_dev(w, dev)).data.cpu().numpy()
+    ref = ocv.pack_weight_reference_layout(w)
+    assert ours.shape == (20, 27, 5)
+    for tap in range(27):
+        np.testing.assert_array_equal(ours[:, tap, :].T, ref[tap * 16:tap * 16 + 5, :20])
+
+
+def test_pack_upsample_weight_is_bit_exact(pkg, dev) -> None:
+    rng = np.random.default_rng(10)
+    w = rng.standard_normal((7, 12, 3, 3, 3)).astype(np.float16)
+    ours = pkg.ops.pack_upsample_weight(to_dev(w, dev)).data.cpu().numpy()
+    ref = ocv.pack_upsample_weight_reference_layout(w)  # (8, 8 * 16, 16)
+    assert ours.shape == (8, 7, 8, 12)
+    for par in range(8):
+        for t in range(8):
+            np.testing.assert_array_equal(ours[par, :, t, :].T, ref[par, t * 16:t * 16 + 12, :7])
+
+
+def test_norm_silu_conv_fuses_normalisation_shift_and_residual(pkg, dev) -> None:
+    """tests/test_native_kernels.py:309-338: fused GN-affine + SiLU prologue, shift and
+    residual vs the separately normalised input, one rounding of the sum."""
+    rng = np.random.default_rng(13)
+    x, w, b = case((2, 32, 4, 5, 6), 64, 3, 13)
+    gamma = rng.normal(size=(32,)).astype(np.float16)
+    beta = rng.normal(size=(32,)).astype(np.float16)
+    shift = rng.normal(size=(2, 64)).astype(np.float16)
+    res = rng.normal(size=(2, 64, 4, 5, 6)).astype(np.float16)
+    xt = to_dev(ndhwc(x), dev)
+    aff = pkg.ops.group_norm_affine(xt, to_dev(gamma, dev), to_dev(beta, dev), groups=8, eps=1e-5)
+    bias = to_dev(b, dev).float()[None] + to_dev(shift, dev).float()
+    y = pkg.ops.nax_conv3d(xt, pkg.ops.pack_weight(to_dev(w, dev)), bias, affine=aff, silu=True,
+                           residual=to_dev(ndhwc(res), dev))
+    torch.cuda.synchronize()
+    x64 = x.astype(np.float64)
+    normalized = ocv.f16(onm.silu(onm.group_norm(x64, gamma, beta, groups=8, eps=1e-5)))
+    w64 = w.astype(np.float64)
+    expected = ocv.conv3d(normalized, w64, b.astype(np.float64)) + shift[:, :, None, None, None] + res
+    mag = ocv.conv3d_magnitude(normalized, w64, b.astype(np.float64))
+    err = np.abs(ncdhw(host(y)) - expected)
+    assert np.all(err <= half_spacing(expected) + (ACCUMULATION_EPS + OPERAND_ROUNDING) * mag)
+
+
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_pointwise_conv(pkg, dev, with_bias) -> None:
+    """tests/test_native_kernels.py:361-377 (this kernel rounds once, inside that bound)."""
+    x, w, b = case((2, 48, 3, 5, 7), 40, 1, 11)
+    y = pkg.ops.conv3d(to_dev(ndhwc(x), dev), to_dev(w, dev), to_dev(b, dev) if with_bias else None,
+                       padding=0)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (2, 3, 5, 7, 40)
+    x64, w64, b64 = x.astype(np.float64), w.astype(np.float64), b.astype(np.float64)
+    products = ocv.conv3d(x64, w64, padding=0)
+    expected = products + (b64[None, :, None, None, None] if with_bias else 0)
+    mag = ocv.conv3d_magnitude(x64, w64, padding=0)
+    bound = half_spacing(products) + ACCUMULATION_EPS * mag + (half_spacing(expected) if with_bias else 0)
+    assert np.all(np.abs(ncdhw(host(y)) - expected) <= bound)
+
+
+def test_dense_rounds_once_and_fuses_gelu(pkg, dev) -> None:
+    """tests/test_native_kernels.py:341-358, plus the dense -> GELU pair."""
+    rng = np.random.default_rng(17)
+    x = rng.normal(size=(2, 33, 48)).astype(np.float16)
+    w = (rng.normal(size=(40, 48)) / 7).astype(np.float16)
+    b = rng.normal(size=(40,)).astype(np.float16)
+    pk = pkg.ops.pack_weight(to_dev(w, dev))
+    y = pkg.ops.dense(to_dev(x, dev), pk, to_dev(b, dev))
+    g = pkg.ops.dense(to_dev(x, dev), pk, to_dev(b, dev), act="gelu")
+    torch.cuda.synchronize()
+    terms = x.astype(np.float64) @ w.astype(np.float64).T
+    expected = terms + b
+    mag = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T + np.abs(b.astype(np.float64))
+    yy = host(y)
+    assert np.all(np.abs(yy - expected) <= half_spacing(expected) + ACCUMULATION_EPS * mag)
+    want = onm.gelu(yy)  # GELU of the stored half value, rounded once more
+    assert np.all(np.abs(host(g) - want) <= half_spacing(want) * 1.001 + 1e-7)
