@@ -1,0 +1,206 @@
+"""Benchmark of the MI355X dense hot path (one GPU).
+
+Headline (``value``): config 1 -- one 3x3x3 stride-1 conv3d, NDHWC fp16, N=1,
+C_in = C_out = 64, 32x40x40 -- in TFLOP/s, with its MFMA roofline. The same JSON line
+also carries config 2 (flash attention, self 1x8x1600x64 and 1600 x 77 cross) and,
+when the model layer is present, the config-3/4/5 figures.
+
+A "step" is one launch of the op over one batch of synthetic input resident in HBM.
+K steps are captured in one HIP graph and replayed; HIP events recorded on the stream
+the kernels are launched on bracket the K launches (after a device synchronise on both
+sides), so the per-launch time excludes host launch overhead.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-model] [--skip-cpu]``
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO))
+
+METRIC = "conv3d & flash-attn TFLOP/s (% MFMA peak); ms per 3D-UNet denoise step"
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def _graph_time(launch, steps: int, warmup: int) -> float:
+    """Average ms per launch: ``warmup`` eager launches, then ``steps`` launches captured
+    in one graph, replayed once untimed and once timed between HIP events."""
+    import torch
+
+    for _ in range(max(warmup, 1)):
+        launch()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        launch()  # first call on the capture stream outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for _ in range(steps):
+            launch()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_conv(pkg, steps: int, warmup: int) -> dict:
+    import torch
+
+    ops, lib = pkg.ops, pkg._lib
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+    x = torch.from_numpy(rng.standard_normal((1, 32, 40, 40, 64)).astype(np.float16)).to(dev)
+    w = torch.from_numpy((rng.standard_normal((64, 64, 3, 3, 3)) / math.sqrt(27 * 64)).astype(np.float16)).to(dev)
+    b = torch.from_numpy((rng.standard_normal(64) * 0.01).astype(np.float32)).to(dev)
+    pk = ops.pack_weight(w)
+    y = torch.empty((1, 32, 40, 40, 64), dtype=torch.float16, device=dev)
+    a = lib.ConvArgs()
+    a.batch, a.in_d, a.in_h, a.in_w = 1, 32, 40, 40
+    a.c0, a.c1, a.out_c, a.ksize, a.stride, a.upsample = 64, 0, 64, 3, 1, 0
+    a.x0, a.x0_pitch, a.weight = x.data_ptr(), 64, pk.data.data_ptr()
+    a.bias, a.bias_batched, a.output_scale, a.act = b.data_ptr(), 0, 1.0, 0
+    a.y, a.y_pitch = y.data_ptr(), 64
+    ref = ctypes.byref(a)
+
+    def launch():
+        lib.check(lib.lib.ldx_conv3d(ref, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "conv3d")
+
+    ms = _graph_time(launch, steps, warmup)
+    flop = 2.0 * 51200 * 64 * 64 * 27
+    tflops = flop / (ms * 1e-3) / 1e12
+    return {"ms": ms, "tflops": tflops, "flop": flop,
+            "bytes": (51200 * 64 * 2) * 2 + 64 * 64 * 27 * 2, "x": x, "w": w, "b": b}
+
+
+def bench_attention(pkg, steps: int, warmup: int) -> dict:
+    import torch
+
+    ops, lib = pkg.ops, pkg._lib
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+    q = torch.from_numpy(rng.standard_normal((1, 8, 1600, 64)).astype(np.float16)).to(dev)
+    k = torch.from_numpy(rng.standard_normal((1, 8, 1600, 64)).astype(np.float16)).to(dev)
+    v = torch.from_numpy(rng.standard_normal((1, 8, 1600, 64)).astype(np.float16)).to(dev)
+    ctx = torch.from_numpy(rng.standard_normal((1, 77, 768)).astype(np.float16)).to(dev)
+    wk = torch.from_numpy((rng.standard_normal((512, 768)) / math.sqrt(768)).astype(np.float16)).to(dev)
+    wv = torch.from_numpy((rng.standard_normal((512, 768)) / math.sqrt(768)).astype(np.float16)).to(dev)
+    kc = ops.dense(ctx, ops.pack_weight(wk)).view(1, 77, 8, 64).transpose(1, 2)
+    vc = ops.dense(ctx, ops.pack_weight(wv)).view(1, 77, 8, 64).transpose(1, 2)
+    out = {}
+    for name, kk, vv, lk in (("self", k, v, 1600), ("cross", kc, vc, 77)):
+        o = torch.empty((1, 8, 1600, 64), dtype=torch.float16, device=dev)
+        a = ops._attn_args(q.transpose(1, 2), kk.transpose(1, 2), vv.transpose(1, 2), o.transpose(1, 2),
+                           0.125, None)
+        ref = ctypes.byref(a)
+
+        def launch(ref=ref):
+            lib.check(lib.lib.ldx_attention(ref, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                      "attention")
+
+        ms = _graph_time(launch, steps, warmup)
+        flop = 4.0 * 8 * 1600 * lk * 64
+        byts = 2.0 * (2 * 8 * 1600 * 64 + 2 * 8 * lk * 64)
+        out[name] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
+                     "frac_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
+                     "gbs": byts / (ms * 1e-3) / 1e9}
+    out["_tensors"] = (q, k, v)
+    return out
+
+
+def cpu_baseline_conv(x, w, b, budget_s: float = 12.0) -> dict:
+    """The float64 oracle conv (oracle/conv.py) on the host cores, on a bounded sample:
+    repeated full config-1 convolutions until ``budget_s`` seconds have elapsed."""
+    from oracle import conv as ocv
+
+    xn = x.float().cpu().numpy().astype(np.float64).transpose(0, 4, 1, 2, 3)
+    wn = w.float().cpu().numpy().astype(np.float64)
+    bn = b.float().cpu().numpy().astype(np.float64)
+    ocv.conv3d(xn[:, :, :4], wn, bn)  # warm BLAS
+    n, t0 = 0, time.perf_counter()
+    while True:
+        ocv.conv3d(xn, wn, bn)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or n >= 50:
+            break
+    flop = 2.0 * 51200 * 64 * 64 * 27
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": flop * n / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full config-1 convolutions (float64 NumPy oracle, per-tap BLAS products) in {el:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-model", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(collectives and sharding are out of scope); run with --gpus 1.", file=sys.stderr)
+        return 2
+    import torch
+
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    torch.cuda.synchronize()
+    conv = bench_conv(pkg, args.steps, args.warmup)
+    att = bench_attention(pkg, args.steps, args.warmup)
+    line = {
+        "metric": METRIC,
+        "value": round(conv["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(conv["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "config 1: conv3d 3x3x3 stride 1 pad 1, NDHWC fp16, N=1, C_in=C_out=64, "
+                               "D x H x W = 32 x 40 x 40, seed 0", "global_batch": 1},
+        "roofline": {"bound": "mfma", "achieved": round(conv["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(conv["tflops"] / PEAK_FP16_TFLOPS, 4),
+                     "traffic": None},
+        "attention": {
+            "self_tflops": round(att["self"]["tflops"], 2), "self_ms": round(att["self"]["ms"], 5),
+            "self_frac_peak": round(att["self"]["frac_peak"], 4),
+            "cross_tflops": round(att["cross"]["tflops"], 2), "cross_ms": round(att["cross"]["ms"], 5),
+            "cross_gbs": round(att["cross"]["gbs"], 1),
+            "config": "config 2: fp16, B=1, 8 heads x 64, 1600 queries; self 1600 keys, cross 77 keys "
+                      "(context 77x768 projected by to_k/to_v)"},
+    }
+    if not args.skip_cpu:
+        line["cpu_baseline"] = cpu_baseline_conv(conv["x"], conv["w"], conv["b"])
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -34,7 +34,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version; bumped on any change to the structs below. */
+/* ABI version (2); bumped on any change to the structs below. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -79,22 +79,33 @@ typedef struct ldx_conv3d_args {
   float output_scale;                /* 1.0 = plain */
   int32_t act;                       /* LDX_ACT_* */
   void* y; int64_t y_pitch;          /* fp16 NDHWC output */
+  void* workspace;                   /* optional device scratch for split-K partial sums */
+  size_t workspace_bytes;
 } ldx_conv3d_args;
 
+/* Bytes of workspace with which ldx_conv3d splits the reduction over channel chunks
+ * across workgroups (small grids); 0 when it would not split. Without it the conv
+ * runs in one pass -- same results up to fp32 summation order. */
+size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* args);
 int ldx_conv3d(const ldx_conv3d_args* args, void* stream);
 
-/* Pack a Torch-layout fp16 weight (O, C, K, K, K) (K = 3 or 1) into the kernel
- * layout (O, K^3, C): W'[o, tap, c] = W[o, c, kd, kh, kw], tap = kd*9 + kh*3 + kw
- * (the reference's pack_weight, _nax_conv.py:350-364, stores the transpose
- * (27*C', O') with row tap*C' + c; this layout keeps each output channel's
- * reduction contiguous for the MFMA A operand and needs no channel padding). */
+/* Pack a Torch-layout fp16 weight (O, C, K, K, K) (K = 3 or 1; a dense (O, C)
+ * weight is K = 1) into the kernel's fragment-major layout of
+ * ldx_packed_weight_elems(O, C, K, 0) halves: with NOB = 4*ceil(O/128), NKC =
+ * 4*ceil(C/64), tap = kd*9 + kh*3 + kw, fragment ((ob*K^3 + tap)*NKC + kc) holds 512
+ * halves, lane l's eight at offset l*8 being W[ob*32 + l%32, kc*16 + 8*(l/32) + e,
+ * kd, kh, kw] (zero past O or C) -- the A operand of v_mfma_f32_32x32x16_f16. The reference's pack_weight
+ * (_nax_conv.py:350-364) stores the same values as (27*C', O') with row tap*C' + c;
+ * this order makes every MFMA A-operand load one contiguous 1 KB wave read. */
+size_t ldx_packed_weight_elems(int32_t out_c, int32_t in_c, int32_t ksize, int32_t upsample);
 int ldx_pack_weight(const void* weight, int32_t out_c, int32_t in_c, int32_t ksize,
                     void* packed, void* stream);
 
 /* Fold a Torch-layout fp16 (O, C, 3, 3, 3) weight into the 8 parity 2x2x2 filters
- * of a nearest-2x-upsampled conv, layout (8, O, 8, C): [pd*4+ph*2+pw, o,
- * td*4+th*2+tw, c]; merged taps summed in fp32 in the reference's order and rounded
- * to fp16 once (pack_upsample_weight, _nax_conv.py:367-405). */
+ * of a nearest-2x-upsampled conv (pack_upsample_weight, _nax_conv.py:367-405):
+ * merged taps summed in fp32 in the reference's order and rounded to fp16 once,
+ * stored fragment-major as above with parity = pd*4+ph*2+pw leading and tap =
+ * td*4+th*2+tw: fragment (((parity*NOB + ob)*8 + tap)*NKC + kc). */
 int ldx_pack_upsample_weight(const void* weight, int32_t out_c, int32_t in_c,
                              void* packed, void* stream);
 

@@ -41,6 +41,7 @@ class ConvArgs(ctypes.Structure):
         ("residual", c_vp), ("residual_pitch", c_i64),
         ("output_scale", c_f32), ("act", c_i32),
         ("y", c_vp), ("y_pitch", c_i64),
+        ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -63,7 +64,9 @@ class AttnArgs(ctypes.Structure):
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_last_error": (ctypes.c_char_p, []),
     "ldx_abi_version": (c_i32, []),
+    "ldx_conv3d_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(ConvArgs)]),
     "ldx_conv3d": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
+    "ldx_packed_weight_elems": (ctypes.c_size_t, [c_i32, c_i32, c_i32, c_i32]),
     "ldx_pack_weight": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "ldx_pack_upsample_weight": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_group_norm_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i64, c_i32, c_i32]),
@@ -79,7 +82,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_ddim_update": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i32, c_vp]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def _load() -> ctypes.CDLL:

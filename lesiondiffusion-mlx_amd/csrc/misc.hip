@@ -45,17 +45,33 @@ static inline unsigned grid_cap(int64_t n, int per, unsigned cap) {
 }
 
 // ------------------------------------------------------------------ packing
-// packed[o][tap][c] = w[o][c][tap]   (pack_weight, _nax_conv.py:350-364, transposed)
+// Fragment-major layout of the 32x32x16 MFMA A operand (32 output rows x 16 reduction
+// values per fragment, 1 KB): fragment (ob, tap, kc) holds, at lane l's 16 bytes
+// (offset l * 8 halves), W[o = ob*32 + l%32][tap][c = kc*16 + 8*(l/32) + e], e < 8,
+// zero past O or C. NOB = ceil(O/128)*4 and NKC = ceil(C/64)*4, so any 128-row x
+// 64-channel tile of fragments exists. Upsample weights prefix the parity:
+// ((parity*NOB + ob)*8 + tap).
+__device__ __forceinline__ void frag_coords(int64_t i, int NKC, int taps, int& e, int& l, int& kc,
+                                            int& tap, int64_t& obp) {
+  e = (int)(i & 7);
+  l = (int)((i >> 3) & 63);
+  const int64_t frag = i >> 9;
+  kc = (int)(frag % NKC);
+  tap = (int)((frag / NKC) % taps);
+  obp = frag / ((int64_t)NKC * taps);
+}
+
 __global__ void pack_weight_kernel(const f16* __restrict__ w, int O, int C, int taps,
                                    f16* __restrict__ out) {
-  const int64_t n = (int64_t)O * C * taps;
+  const int NOB = (O + 127) / 128 * 4, NKC = (C + 63) / 64 * 4;
+  const int64_t n = (int64_t)NOB * taps * NKC * 512;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % C);
-    const int64_t r = i / C;
-    const int tap = (int)(r % taps);
-    const int o = (int)(r / taps);
-    out[i] = w[((int64_t)o * C + c) * taps + tap];
+    int e, l, kc, tap; int64_t ob;
+    frag_coords(i, NKC, taps, e, l, kc, tap, ob);
+    const int o = (int)ob * 32 + (l & 31);
+    const int c = kc * 16 + 8 * (l >> 5) + e;
+    out[i] = (o < O && c < C) ? w[((int64_t)o * C + c) * taps + tap] : (f16)0;
   }
 }
 
@@ -66,19 +82,21 @@ __device__ __forceinline__ void fold_set(int p, int t, int& k_lo, int& k_hi) {
   else { k_lo = t == 0 ? 0 : 2; k_hi = t == 0 ? 1 : 2; }
 }
 
-// packed[parity][o][tap][c], parity = pd*4+ph*2+pw, tap = td*4+th*2+tw. Sums are
-// float32 and nest d (innermost), then h, then w, each left to right -- the order
-// of the reference's per-axis folds (_nax_conv.py:394-405).
+// parity = pd*4+ph*2+pw, tap = td*4+th*2+tw. Sums are float32 and nest d (innermost),
+// then h, then w, each left to right -- the order of the reference's per-axis folds
+// (_nax_conv.py:394-405) -- and are rounded to fp16 once.
 __global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
                                      f16* __restrict__ out) {
-  const int64_t n = (int64_t)8 * O * 8 * C;
+  const int NOB = (O + 127) / 128 * 4, NKC = (C + 63) / 64 * 4;
+  const int64_t n = (int64_t)8 * NOB * 8 * NKC * 512;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % C);
-    int64_t r = i / C;
-    const int tap = (int)(r % 8); r /= 8;
-    const int o = (int)(r % O);
-    const int parity = (int)(r / O);
+    int e, l, kc, tap; int64_t pob;
+    frag_coords(i, NKC, 8, e, l, kc, tap, pob);
+    const int parity = (int)(pob / NOB), ob = (int)(pob % NOB);
+    const int o = ob * 32 + (l & 31);
+    const int c = kc * 16 + 8 * (l >> 5) + e;
+    if (o >= O || c >= C) { out[i] = (f16)0; continue; }
     const int pd = parity >> 2, ph = (parity >> 1) & 1, pw = parity & 1;
     const int td = tap >> 2, th = (tap >> 1) & 1, tw = tap & 1;
     int d_lo, d_hi, h_lo, h_hi, w_lo, w_hi;
@@ -350,14 +368,20 @@ __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict_
 using namespace ldx;
 
 extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
-extern "C" int ldx_abi_version(void) { return 1; }
+extern "C" int ldx_abi_version(void) { return 2; }
+
+extern "C" size_t ldx_packed_weight_elems(int32_t O, int32_t C, int32_t k, int32_t upsample) {
+  if (O < 1 || C < 1 || (k != 1 && k != 3) || (upsample && k != 3)) return 0;
+  const int taps = upsample ? 8 : k * k * k;
+  return (size_t)(upsample ? 8 : 1) * ((O + 127) / 128 * 4) * taps * ((C + 63) / 64 * 4) * 512;
+}
 
 extern "C" int ldx_pack_weight(const void* weight, int32_t O, int32_t C, int32_t k, void* packed,
                                void* stream) {
   if (!weight || !packed) return fail("pack_weight: null pointer");
   if (O < 1 || C < 1 || (k != 1 && k != 3)) return fail("pack_weight: bad shape O=%d C=%d k=%d", O, C, k);
   const int taps = k * k * k;
-  const int64_t n = (int64_t)O * C * taps;
+  const int64_t n = (int64_t)ldx_packed_weight_elems(O, C, k, 0);
   hipLaunchKernelGGL(pack_weight_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
                      as_stream(stream), (const f16*)weight, O, C, taps, (f16*)packed);
   return check_launch("pack_weight");
@@ -367,7 +391,7 @@ extern "C" int ldx_pack_upsample_weight(const void* weight, int32_t O, int32_t C
                                         void* stream) {
   if (!weight || !packed) return fail("pack_upsample_weight: null pointer");
   if (O < 1 || C < 1) return fail("pack_upsample_weight: bad shape O=%d C=%d", O, C);
-  const int64_t n = (int64_t)64 * O * C;
+  const int64_t n = (int64_t)ldx_packed_weight_elems(O, C, 3, 1);
   hipLaunchKernelGGL(pack_upsample_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
                      as_stream(stream), (const f16*)weight, O, C, (f16*)packed);
   return check_launch("pack_upsample_weight");

@@ -80,8 +80,9 @@ def output_extent(n: int, *, stride: int = 1, upsample: bool = False) -> int:
 
 @dataclass
 class PackedWeight:
-    """A conv/dense weight in the kernel layout: ``(O, K^3, C)`` or, folded for a
-    nearest-2x-upsampled conv, ``(8, O, 8, C)``."""
+    """A conv/dense weight in the kernel's fragment-major layout (a flat fp16 tensor of
+    ``ldx_packed_weight_elems`` values; see ``include/ldx.h``), or folded into the
+    8 parity filters of a nearest-2x-upsampled conv."""
 
     data: torch.Tensor
     out_channels: int
@@ -102,7 +103,7 @@ def pack_weight(weight: torch.Tensor) -> PackedWeight:
         raise ValueError(f"weight must be (O, C, K, K, K) with K in (1, 3), got {tuple(weight.shape)}")
     o, c, k = int(weight.shape[0]), int(weight.shape[1]), int(weight.shape[2])
     w = weight.contiguous()
-    out = torch.empty((o, k ** 3, c), dtype=torch.float16, device=weight.device)
+    out = torch.empty(lib.ldx_packed_weight_elems(o, c, k, 0), dtype=torch.float16, device=weight.device)
     check(lib.ldx_pack_weight(_ptr(w), o, c, k, _ptr(out), _stream()), "pack_weight")
     return PackedWeight(out, o, c, k, False)
 
@@ -115,9 +116,24 @@ def pack_upsample_weight(weight: torch.Tensor) -> PackedWeight:
         raise ValueError(f"weight must be (O, C, 3, 3, 3), got {tuple(weight.shape)}")
     o, c = int(weight.shape[0]), int(weight.shape[1])
     w = weight.contiguous()
-    out = torch.empty((8, o, 8, c), dtype=torch.float16, device=weight.device)
+    out = torch.empty(lib.ldx_packed_weight_elems(o, c, 3, 1), dtype=torch.float16, device=weight.device)
     check(lib.ldx_pack_upsample_weight(_ptr(w), o, c, _ptr(out), _stream()), "pack_upsample_weight")
     return PackedWeight(out, o, c, 3, True)
+
+
+def unpack_weight(packed: PackedWeight) -> "np.ndarray":
+    """Host copy of a packed weight in the plain ``(parities, O, taps, C)`` order (a test
+    and debugging aid; the kernels read the fragment-major form)."""
+    import numpy as np
+
+    taps = 8 if packed.upsample else packed.ksize ** 3
+    par = 8 if packed.upsample else 1
+    nob = -(-packed.out_channels // 128) * 4
+    nkc = -(-packed.in_channels // 64) * 4
+    f = packed.data.cpu().numpy().reshape(par, nob, taps, nkc, 2, 32, 8)  # lane = g*32 + r
+    # -> (par, ob, r, taps, kc, g, e) -> (par, O', taps, C')
+    full = f.transpose(0, 1, 5, 2, 3, 4, 6).reshape(par, nob * 32, taps, nkc * 16)
+    return full[:, :packed.out_channels, :, :packed.in_channels]
 
 
 def _bias32(bias: torch.Tensor | None, batch: int, out_c: int) -> tuple[torch.Tensor | None, int]:
@@ -200,6 +216,11 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     a.output_scale = float(output_scale)
     a.act = {None: ACT_NONE, "gelu": ACT_GELU}[act]
     a.y, a.y_pitch = out.data_ptr(), yp
+    ws_bytes = lib.ldx_conv3d_workspace_bytes(ctypes.byref(a))
+    ws = None
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
     check(lib.ldx_conv3d(ctypes.byref(a), _stream()), "conv3d")
     return out
 

@@ -162,17 +162,22 @@ def test_pack_weight_layout_is_the_reference_layout_transposed(pkg, dev) -> None
     """Bit-exact: packed[o, tap, c] == reference_packed[tap * C' + c, o]."""
     rng = np.random.default_rng(9)
     w = rng.standard_normal((20, 5, 3, 3, 3)).astype(np.float16)
-    ours = pkg.ops.pack_weight(to_dev(w, dev)).data.cpu().numpy()
+    packed = pkg.ops.pack_weight(to_dev(w, dev))
+    ours = pkg.ops.unpack_weight(packed)[0]
     ref = ocv.pack_weight_reference_layout(w)
     assert ours.shape == (20, 27, 5)
+    assert packed.data.numel() == 4 * 27 * 4 * 512  # zero-padded to 128 outputs, 64 channels
     for tap in range(27):
         np.testing.assert_array_equal(ours[:, tap, :].T, ref[tap * 16:tap * 16 + 5, :20])
+    full = packed.data.cpu().numpy().reshape(4, 27, 4, 2, 32, 8)  # (ob, tap, kc, g, r, e)
+    assert np.all(full[1:] == 0) and np.all(full[0, :, :, :, 20:, :] == 0) and np.all(full[0, :, 1:] == 0)
+    assert np.all(full[0, :, 0, 0, :, 5:] == 0) and np.all(full[0, :, 0, 1] == 0)
 
 
 def test_pack_upsample_weight_is_bit_exact(pkg, dev) -> None:
     rng = np.random.default_rng(10)
     w = rng.standard_normal((7, 12, 3, 3, 3)).astype(np.float16)
-    ours = pkg.ops.pack_upsample_weight(to_dev(w, dev)).data.cpu().numpy()
+    ours = pkg.ops.unpack_weight(pkg.ops.pack_upsample_weight(to_dev(w, dev)))
     ref = ocv.pack_upsample_weight_reference_layout(w)  # (8, 8 * 16, 16)
     assert ours.shape == (8, 7, 8, 12)
     for par in range(8):
