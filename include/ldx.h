@@ -34,19 +34,22 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (2); bumped on any change to the structs below. */
+/* ABI version (3); bumped on any change to the structs below. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
  * Replaces nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619) and the
  * pointwise/dense paths of SourceLayers.conv/dense (mlx_model.py:159-220).
  *
- * y[b, v, o] = half( (sum_{tap,c} W[o, tap, c] * xin[b, v@tap, c] + bias[(b,) o])
- *                    * output_scale + residual[b, v, o] )
+ * y[b, v, o] = half( (sum_{tap,c} W[o, tap, c] * xin[b, v@tap, c] + bias[(b,) o]
+ *                     + shift[b, o]) * output_scale + residual[b, v, o] )
  * xin = half(silu(x * affine[b, c, 0] + affine[b, c, 1])) when affine/silu are set
  * (rounded once, zero padding applied after it), else x. One rounding of the FP32
- * sum. act = LDX_ACT_GELU further stores half(gelu_erf(float(y))) (the dense->GELU
- * pair of mlx_model.py:549).
+ * sum. act = LDX_ACT_GELU / LDX_ACT_SILU further stores half(gelu_erf(float(y))) /
+ * half(silu(float(y))) (the dense -> GELU pair of mlx_model.py:549 and the
+ * dense -> SiLU pairs of the time embedding, mlx_model.py:434, 614). shift is the
+ * ResBlock's projected time embedding (fp16, batch pitch in elements), added with
+ * the bias (mlx_model.py:340-341).
  *
  * Geometry: ksize 3 (padding 1) with stride 1 or 2, or with upsample = 1 (conv of
  * the nearest 2x upsampling of x, weights from ldx_pack_upsample_weight); ksize 1
@@ -60,6 +63,7 @@ int ldx_abi_version(void);
  */
 #define LDX_ACT_NONE 0
 #define LDX_ACT_GELU 1
+#define LDX_ACT_SILU 2
 
 typedef struct ldx_conv3d_args {
   int32_t batch, in_d, in_h, in_w;   /* input (source) grid */
@@ -73,6 +77,7 @@ typedef struct ldx_conv3d_args {
   const void* weight;                /* packed fp16, ldx_pack_weight layout */
   const float* bias;                 /* fp32 (O) or (batch, O) if bias_batched; may be NULL */
   int32_t bias_batched;
+  const void* shift; int64_t shift_pitch;  /* fp16 (batch, O) with batch pitch, or NULL */
   const float* affine;               /* fp32 (batch, c0 + c1, 2) scale/offset pairs or NULL */
   int32_t silu;                      /* apply SiLU to the prepared input */
   const void* residual; int64_t residual_pitch;  /* fp16 NDHWC of the output grid or NULL */
@@ -191,7 +196,16 @@ int ldx_ddim_prepare(float* x, const float* cond, const float* mask, int64_t vox
                      int32_t channels, int32_t cond_channels, void* net_in,
                      int64_t net_pitch, void* stream);
 int ldx_ddim_update(float* x, const void* net_out, int64_t net_pitch, const float* noise,
-                    const float* coef, int64_t voxels, int32_t channels, void* stream);
+                    const float* coef, const int32_t* step, int64_t voxels, int32_t channels,
+                    void* stream);
+
+/* Device-side step indexing for a captured (graph-replayed) sampler step: with
+ * step != NULL, ldx_ddim_update reads coef + 4 * (*step) and noise + (*step) * voxels
+ * * channels (tables of all steps); ldx_ddim_timestep writes t_out[0..batch) =
+ * t_table[*step]; ldx_step_advance increments *step (one thread). */
+int ldx_ddim_timestep(const int32_t* step, const int32_t* t_table, int32_t batch,
+                      int32_t* t_out, void* stream);
+int ldx_step_advance(int32_t* step, void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,7 @@ LDX_EINVAL = -1
 LDX_EHIP = -2
 ACT_NONE = 0
 ACT_GELU = 1
+ACT_SILU = 2
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -37,6 +38,7 @@ class ConvArgs(ctypes.Structure):
         ("x1", c_vp), ("x1_pitch", c_i64),
         ("weight", c_vp),
         ("bias", c_vp), ("bias_batched", c_i32),
+        ("shift", c_vp), ("shift_pitch", c_i64),
         ("affine", c_vp), ("silu", c_i32),
         ("residual", c_vp), ("residual_pitch", c_i64),
         ("output_scale", c_f32), ("act", c_i32),
@@ -79,10 +81,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_copy_channels": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i64, c_i32, c_vp]),
     "ldx_upsample_nearest2": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "ldx_ddim_prepare": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
-    "ldx_ddim_update": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_vp, c_i64, c_i32, c_vp]),
+    "ldx_ddim_update": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp]),
+    "ldx_ddim_timestep": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp]),
+    "ldx_step_advance": (c_i32, [c_vp, c_vp]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def _load() -> ctypes.CDLL:

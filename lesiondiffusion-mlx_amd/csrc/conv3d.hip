@@ -44,6 +44,7 @@ struct ConvParams {
   const f16* x1; int64_t x1p;
   const f16* w;
   const float* bias; int bias_batched;
+  const f16* shift; int64_t shiftp;
   const float* affine; int silu;
   const f16* res; int64_t resp;
   float scale; int act;
@@ -52,6 +53,13 @@ struct ConvParams {
 
 __device__ __forceinline__ float gelu_erf(float v) {
   return v * (1.0f + erff(v * 0.70710678118654752f)) * 0.5f;
+}
+
+// Epilogue activation applied to the stored half value (a second rounding).
+__device__ __forceinline__ f16 post_act(f16 h, int act) {
+  if (act == LDX_ACT_GELU) return (f16)gelu_erf((float)h);
+  if (act == LDX_ACT_SILU) return (f16)silu_f((float)h);
+  return h;
 }
 
 // q = t / d for 0 <= t < 2^21 and small d, from a host-rounded reciprocal: (t + 0.5) / d
@@ -273,6 +281,7 @@ __global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
   // accumulator elements, output channels (ob)*32 + j*8 + 4*(lane/32) + r.
   const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
   const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
+  const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
 #pragma unroll
   for (int fv = 0; fv < FV; fv++) {
     if (!valid[fv]) continue;
@@ -311,12 +320,11 @@ __global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
           float v = acc[fo][fv][j * 4 + r];
           if (o < p.O) {
             if (bias) v += bias[o];
+            if (shb) v += (float)shb[o];
             v *= p.scale;
             if (rrow) v += (float)rrow[o];
           }
-          f16 hv = (f16)v;
-          if (p.act == LDX_ACT_GELU) hv = (f16)gelu_erf((float)hv);
-          outv[r] = hv;
+          outv[r] = post_act((f16)v, p.act);
         }
         if (p.yvec && o4 + 4 <= p.O) {
           *reinterpret_cast<f16x4*>(yrow + o4) = outv;
@@ -343,11 +351,10 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
     const int64_t vol = nvox / p.B;
     const int b = (int)(ov / vol);
     if (p.bias) v += p.bias[(p.bias_batched ? (int64_t)b * p.O : 0) + o];
+    if (p.shift) v += (float)p.shift[(int64_t)b * p.shiftp + o];
     v *= p.scale;
     if (p.res) v += (float)p.res[ov * p.resp + o];
-    f16 hv = (f16)v;
-    if (p.act == LDX_ACT_GELU) hv = (f16)gelu_erf((float)hv);
-    p.y[ov * p.yp + o] = hv;
+    p.y[ov * p.yp + o] = post_act((f16)v, p.act);
   }
 }
 
@@ -428,7 +435,9 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   if (a->x0_pitch < a->c0 || (a->c1 > 0 && a->x1_pitch < a->c1) || a->y_pitch < a->out_c)
     return fail("conv3d: pitch smaller than channel count");
   if (a->residual && a->residual_pitch < a->out_c) return fail("conv3d: residual pitch < out_c");
-  if (a->act != LDX_ACT_NONE && a->act != LDX_ACT_GELU) return fail("conv3d: unknown act %d", a->act);
+  if (a->act != LDX_ACT_NONE && a->act != LDX_ACT_GELU && a->act != LDX_ACT_SILU)
+    return fail("conv3d: unknown act %d", a->act);
+  if (a->shift && a->shift_pitch < a->out_c) return fail("conv3d: shift pitch < out_c");
 
   p = ConvParams{};
   p.B = a->batch; p.D = a->in_d; p.H = a->in_h; p.W = a->in_w;
@@ -450,6 +459,7 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   p.x1 = (const f16*)a->x1; p.x1p = a->x1_pitch;
   p.w = (const f16*)a->weight;
   p.bias = a->bias; p.bias_batched = a->bias_batched ? 1 : 0;
+  p.shift = (const f16*)a->shift; p.shiftp = a->shift_pitch;
   p.affine = a->affine; p.silu = a->silu ? 1 : 0;
   p.res = (const f16*)a->residual; p.resp = a->residual_pitch;
   p.scale = a->output_scale; p.act = a->act;

@@ -349,7 +349,10 @@ __global__ void ddim_prepare_kernel(float* __restrict__ x, const float* __restri
 
 __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict__ net, int64_t np,
                                    const float* __restrict__ noise, const float* __restrict__ coef,
-                                   int64_t V, int C) {
+                                   const int32_t* __restrict__ step, int64_t V, int C) {
+  const int si = step ? *step : 0;
+  coef += 4 * si;
+  noise += (int64_t)si * V * C;
   const float a = coef[0], prev = coef[1], sig = coef[2], s1m = coef[3];
   const float c_dir = sqrtf(1.0f - prev - sig * sig);
   const int64_t n = V * C;
@@ -368,7 +371,7 @@ __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict_
 using namespace ldx;
 
 extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
-extern "C" int ldx_abi_version(void) { return 2; }
+extern "C" int ldx_abi_version(void) { return 3; }
 
 extern "C" size_t ldx_packed_weight_elems(int32_t O, int32_t C, int32_t k, int32_t upsample) {
   if (O < 1 || C < 1 || (k != 1 && k != 3) || (upsample && k != 3)) return 0;
@@ -508,11 +511,35 @@ extern "C" int ldx_ddim_prepare(float* x, const float* cond, const float* mask, 
 }
 
 extern "C" int ldx_ddim_update(float* x, const void* net, int64_t np, const float* noise,
-                               const float* coef, int64_t V, int32_t C, void* stream) {
+                               const float* coef, const int32_t* step, int64_t V, int32_t C,
+                               void* stream) {
   if (!x || !net || !noise || !coef) return fail("ddim_update: null pointer");
   if (V < 1 || C < 1 || np < C) return fail("ddim_update: bad shape");
   const int64_t n = V * C;
   hipLaunchKernelGGL(ddim_update_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
-                     as_stream(stream), x, (const f16*)net, np, noise, coef, V, C);
+                     as_stream(stream), x, (const f16*)net, np, noise, coef, step, V, C);
   return check_launch("ddim_update");
+}
+
+__global__ void ddim_timestep_kernel(const int32_t* step, const int32_t* table, int B, int32_t* out) {
+  const int i = threadIdx.x;
+  if (i < B) out[i] = table[*step];
+}
+
+__global__ void step_advance_kernel(int32_t* step) {
+  if (threadIdx.x == 0) *step += 1;
+}
+
+extern "C" int ldx_ddim_timestep(const int32_t* step, const int32_t* table, int32_t B, int32_t* out,
+                                 void* stream) {
+  if (!step || !table || !out) return fail("ddim_timestep: null pointer");
+  if (B < 1 || B > 1024) return fail("ddim_timestep: batch %d out of range", B);
+  hipLaunchKernelGGL(ddim_timestep_kernel, dim3(1), dim3(1024), 0, as_stream(stream), step, table, B, out);
+  return check_launch("ddim_timestep");
+}
+
+extern "C" int ldx_step_advance(int32_t* step, void* stream) {
+  if (!step) return fail("step_advance: null pointer");
+  hipLaunchKernelGGL(step_advance_kernel, dim3(1), dim3(64), 0, as_stream(stream), step);
+  return check_launch("step_advance");
 }

@@ -19,7 +19,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from ._lib import ACT_GELU, ACT_NONE, AttnArgs, ConvArgs, check, lib
+from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, check, lib
 
 __all__ = [
     "PackedWeight", "pack_weight", "pack_upsample_weight", "nax_conv3d", "conv3d", "dense",
@@ -152,11 +152,14 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
                affine: torch.Tensor | None = None, silu: bool = False, stride: int = 1,
                upsample: bool = False, output_scale: float = 1.0,
                residual: torch.Tensor | None = None, x1: torch.Tensor | None = None,
-               act: str | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+               act: str | None = None, out: torch.Tensor | None = None,
+               shift: torch.Tensor | None = None) -> torch.Tensor:
     """Fused conv of NDHWC ``x`` (optionally ``concat([x, x1], channels)``) with a packed
-    weight: ``half((conv(prep(x)) + bias) * output_scale + residual)``, ``prep`` = the
-    per-(b, c) ``affine`` then SiLU, rounded to fp16 once (nax_conv3d,
-    _nax_conv.py:451-500). ``act="gelu"`` additionally stores ``half(gelu(y))``.
+    weight: ``half((conv(prep(x)) + bias + shift) * output_scale + residual)``, ``prep`` =
+    the per-(b, c) ``affine`` then SiLU, rounded to fp16 once (nax_conv3d,
+    _nax_conv.py:451-500). ``shift`` is an fp16 ``(B, O)`` per-batch term (a row slice of
+    a wider tensor is fine). ``act="gelu"`` / ``"silu"`` additionally stores
+    ``half(act(y))``.
 
     Returns NDHWC ``(B, D', H', W', O)`` fp16 (written into ``out`` when given, which may
     be a channel slice of a wider tensor).
@@ -214,7 +217,12 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     a.affine, a.silu = (aff.data_ptr() if aff is not None else None), int(bool(silu))
     a.residual, a.residual_pitch = (residual.data_ptr() if residual is not None else None), resp
     a.output_scale = float(output_scale)
-    a.act = {None: ACT_NONE, "gelu": ACT_GELU}[act]
+    a.act = {None: ACT_NONE, "gelu": ACT_GELU, "silu": ACT_SILU}[act]
+    if shift is not None:
+        _require_cuda(shift, "shift")
+        if shift.dim() != 2 or tuple(shift.shape) != (b, o) or shift.stride(1) != 1:
+            raise ValueError(f"shift must be (B, O) = {(b, o)} with contiguous channels")
+        a.shift, a.shift_pitch = shift.data_ptr(), shift.stride(0) if b > 1 else o
     a.y, a.y_pitch = out.data_ptr(), yp
     ws_bytes = lib.ldx_conv3d_workspace_bytes(ctypes.byref(a))
     ws = None
@@ -239,7 +247,7 @@ def conv3d(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
 
 def dense(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = None, *,
           residual: torch.Tensor | None = None, act: str | None = None,
-          out: torch.Tensor | None = None) -> torch.Tensor:
+          out: torch.Tensor | None = None, affine: torch.Tensor | None = None) -> torch.Tensor:
     """``half(x @ W^T + bias (+ residual))`` over the last axis of fp16 ``x`` with fp32
     accumulation and one rounding (SourceLayers.dense native path, mlx_model.py:204-217)."""
     if packed.ksize != 1:
@@ -249,7 +257,7 @@ def dense(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = Non
     x5 = x.reshape(1, 1, 1, rows, x.shape[-1])
     r5 = None if residual is None else residual.reshape(1, 1, 1, rows, packed.out_channels)
     o5 = None if out is None else out.reshape(1, 1, 1, rows, packed.out_channels)
-    y = nax_conv3d(x5, packed, bias, residual=r5, act=act, out=o5)
+    y = nax_conv3d(x5, packed, bias, residual=r5, act=act, out=o5, affine=affine)
     return y.reshape(*lead, packed.out_channels)
 
 

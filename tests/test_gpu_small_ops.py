@@ -117,8 +117,8 @@ def test_ddim_step_kernels_match_oracle(pkg, dev) -> None:
         coef = to_dev(np.array([c["alphas"][idx], c["previous"][idx], c["sigmas"][idx],
                                 c["sqrt_one_minus"][idx]], np.float32), dev)
         noise = to_dev(z["noise"][it].transpose(0, 2, 3, 4, 1).reshape(-1, 4).astype(np.float32), dev)
-        assert lib.ldx_ddim_update(x.data_ptr(), out.data_ptr(), 9, noise.data_ptr(), coef.data_ptr(), 8, 4,
-                                   None) == 0
+        assert lib.ldx_ddim_update(x.data_ptr(), out.data_ptr(), 9, noise.data_ptr(), coef.data_ptr(), None,
+                                   8, 4, None) == 0
         torch.cuda.synchronize()
         eps_n = eps.astype(np.float64).reshape(1, 2, 2, 2, 4).transpose(0, 4, 1, 2, 3)
         xs = osm.ddim_update(xm, eps_n, float(c["alphas"][idx]), float(c["previous"][idx]),
