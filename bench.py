@@ -128,6 +128,149 @@ def bench_attention(pkg, steps: int, warmup: int) -> dict:
     return out
 
 
+def _graph_replay_ms(fn, reps: int, warmup: int = 2) -> float:
+    """Average ms of ``fn`` (a whole forward) captured once as a HIP graph and replayed
+    ``reps`` times between HIP events."""
+    import torch
+
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def _half(w: dict) -> dict:
+    return {k: v.astype(np.float16) for k, v in w.items()}
+
+
+def bench_config3(pkg, reps: int) -> dict:
+    """3-D UNet ResBlock stack: 4-channel 32x40x40 latent, levels 64/128/256/256, two
+    ResBlocks each (1x1 skip on channel change), stride-2 conv between levels."""
+    import torch
+
+    cfg = pkg.unet.UnetConfig(64, 2, (), (1, 2, 4, 4), 32, True)
+    net = pkg.unet.LdmUnet(_half(pkg.unet.unet_state_dict(cfg, in_channels=4, out_channels=4, context_dim=None,
+                                                          seed=0)), cfg)
+    rng = np.random.default_rng(0)
+    x = torch.from_numpy(rng.standard_normal((1, 32, 40, 40, 4)).astype(np.float16)).cuda()
+    t = torch.tensor([500], dtype=torch.int32, device="cuda")
+    with pkg.ops.count_flops() as fc:
+        net.encoder_stack(x, t)
+    ms = _graph_replay_ms(lambda: net.encoder_stack(x, t), reps)
+    return {"ms": round(ms, 4), "conv_gflop": round(fc.conv / 1e9, 2), "tflops": round(fc.total / ms / 1e9, 1),
+            "frac_peak": round(fc.total / ms / 1e9 / PEAK_FP16_TFLOPS, 4),
+            "config": "config 3: encoder stack 4->64/128/256/256 at 32x40x40 .. 4x5x5, 2 ResBlocks per level, "
+                      "fp16, random init"}
+
+
+def bench_config4(pkg, reps: int) -> dict:
+    """VQ decoder at full resolution: 8x32x40x40 latent -> 1x128x160x160 volume, channels
+    256/128/64/32, two nearest-2x upsamplings, single-head mid attention over 51,200
+    tokens at head width 256."""
+    import torch
+
+    w, kw = pkg.vq.vq_decoder_state_dict(latent_channels=8, levels=[(3, 256, True), (2, 128, True), (1, 64, False),
+                                                                    (0, 32, False)],
+                                         mid_channels=256, mid_attention=True, seed=0)
+    dec = pkg.vq.VqDecoder(_half(w), **kw)
+    rng = np.random.default_rng(0)
+    z = torch.from_numpy(rng.standard_normal((1, 32, 40, 40, 8)).astype(np.float16)).cuda()
+    with pkg.ops.count_flops() as fc:
+        y = dec.decode(z)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (1, 128, 160, 160, 1)
+    del y
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    dec.decode(z)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        dec.decode(z)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / reps
+    return {"ms": round(ms, 3), "conv_gflop": round(fc.conv / 1e9, 1), "attention_gflop": round(fc.attention / 1e9, 1),
+            "tflops": round(fc.total / ms / 1e9, 1), "frac_peak": round(fc.total / ms / 1e9 / PEAK_FP16_TFLOPS, 4),
+            "config": "config 4: VQ decoder 8x32x40x40 -> 1x128x160x160, channels 256/128/64/32, mid attention "
+                      "51,200 tokens x 256, fp16, random init, eager launches"}
+
+
+def ldm_alphas_cumprod(n: int = 1000) -> np.ndarray:
+    """The LDM 'linear' schedule (sqrt-spaced betas 0.00085 .. 0.012), stored in fp16 as
+    the LINet checkpoint stores it."""
+    betas = np.linspace(0.00085 ** 0.5, 0.012 ** 0.5, n, dtype=np.float64) ** 2
+    return np.cumprod(1.0 - betas).astype(np.float16)
+
+
+def bench_config5(pkg, steps: int = 200) -> dict:
+    """One full conditioned LINet-style denoise step (UNet 9 -> 4 channels at 32x40x40,
+    levels 64/128/256/256, self + cross attention at the two lowest levels and the middle,
+    77x768 context), DDIM, ``steps`` steps replayed from one captured step graph."""
+    import torch
+
+    cfg = pkg.unet.UnetConfig(64, 2, (4, 8), (1, 2, 4, 4), 32, False)
+    net = pkg.unet.LdmUnet(_half(pkg.unet.unet_state_dict(cfg, in_channels=9, out_channels=4, context_dim=768,
+                                                          seed=0)), cfg)
+    rng = np.random.default_rng(0)
+    dev = torch.device("cuda")
+    ctx = torch.from_numpy(rng.standard_normal((1, 77, 768)).astype(np.float16)).to(dev)
+    cond = torch.from_numpy(rng.standard_normal((1, 32, 40, 40, 4)).astype(np.float32)).to(dev)
+    mask = np.zeros((1, 32, 40, 40), np.float32)
+    d0, h0, w0 = rng.integers(0, 32 - 6), rng.integers(0, 40 - 8), rng.integers(0, 40 - 8)
+    mask[0, d0:d0 + 6, h0:h0 + 8, w0:w0 + 8] = (rng.random((6, 8, 8)) < 0.05).astype(np.float32)
+    sampler = pkg.sampling.DdimSampler(ldm_alphas_cumprod(), steps)
+    prep = sampler.prepare(net.prepare_denoiser(ctx), cond, torch.from_numpy(mask).to(dev),
+                           masked_conditioning=True)
+    g = torch.Generator(device=dev).manual_seed(0)
+    init = torch.randn((1, 32, 40, 40, 4), generator=g, device=dev)
+    noise = torch.randn((prep.num_steps, 1, 32, 40, 40, 4), generator=g, device=dev)
+    prep.set_noise(init, noise)
+    with pkg.ops.count_flops() as fc:
+        prep.denoiser(prep.net_in, prep.t)
+    torch.cuda.synchronize()
+    prep.capture()
+    prep.set_noise(init, noise)
+    prep.run()  # warm replay
+    torch.cuda.synchronize()
+    prep.set_noise(init, noise)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    out = prep.run()
+    end.record()
+    torch.cuda.synchronize()
+    total = start.elapsed_time(end)
+    assert bool(torch.isfinite(out).all())
+    per = total / prep.num_steps
+    return {"ms_per_step": round(per, 4), "total_ms": round(total, 2), "steps": prep.num_steps,
+            "step_gflop": round(fc.total / 1e9, 1), "step_conv_gflop": round(fc.conv / 1e9, 1),
+            "step_attention_gflop": round(fc.attention / 1e9, 2),
+            "tflops": round(fc.total / per / 1e9, 1), "frac_peak": round(fc.total / per / 1e9 / PEAK_FP16_TFLOPS, 4),
+            "config": "config 5: LINet-style UNet 9->4 ch at 32x40x40, 64/128/256/256, 2 ResBlocks/level, "
+                      "self+cross attention at 8x10x20.. levels (heads of 32), 77x768 context, fp16 random init, "
+                      f"DDIM {prep.num_steps} steps, one HIP graph per step"}
+
+
 def cpu_baseline_conv(x, w, b, budget_s: float = 12.0) -> dict:
     """The float64 oracle conv (oracle/conv.py) on the host cores, on a bounded sample:
     repeated full config-1 convolutions until ``budget_s`` seconds have elapsed."""
@@ -196,6 +339,10 @@ def main() -> int:
             "config": "config 2: fp16, B=1, 8 heads x 64, 1600 queries; self 1600 keys, cross 77 keys "
                       "(context 77x768 projected by to_k/to_v)"},
     }
+    if not args.skip_model:
+        line["unet_block_stack"] = bench_config3(pkg, max(args.steps // 5, 5))
+        line["vq_decoder"] = bench_config4(pkg, 3)
+        line["denoise_step"] = bench_config5(pkg, 200)
     if not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline_conv(conv["x"], conv["w"], conv["b"])
     print(json.dumps(line))

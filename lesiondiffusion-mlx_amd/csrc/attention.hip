@@ -1,18 +1,23 @@
-// Flash attention on gfx950 MFMA (v_mfma_f32_16x16x32_f16), fp16 in/out, fp32
+// Flash attention on gfx950 MFMA (v_mfma_f32_32x32x16_f16), fp16 in/out, fp32
 // scores, online softmax and accumulation.
 //
-// Orientation: each wave computes S^T = K Q^T (rows = keys, columns = its 16*FQ
-// queries) so a lane's score registers -- four consecutive keys of one query -- are
-// already the B-operand layout of O^T = V^T P^T: probabilities never leave
-// registers, and every per-query quantity (running max, alpha, partial row sum)
-// is lane-local. Q^T fragments stay in registers for the whole key loop; K tiles
-// (row-major) and V^T tiles (transposed on the LDS store) stream through LDS, the
-// next tile's global loads in flight while the current one is computed.
+// Orientation: a wave computes S^T = K Q^T for a 32-key block and its 32 queries (rows
+// = keys, columns = queries), so the lane's score registers -- 16 of the block's keys
+// for one query -- are already the B operand of O^T = V^T P^T: probabilities never
+// leave registers, and the running max / rescale / partial row sum of a query are
+// lane-local (its other 16 keys sit in lane ^ 32, one swizzle away). Q^T stays in
+// registers; K (row-major) and V^T (transposed on the LDS store) stream through LDS
+// with the next block's global loads in flight during the current block.
+//
+// SPLIT = 1: a workgroup's 4 waves own 4 x 32 queries and share each K/V tile.
+// SPLIT = 4: the 4 waves own the same 32 queries and take interleaved key blocks with
+// private tiles; their (max, sum, O) states merge through LDS at the end -- four times
+// the waves for short sequences (1,600 tokens x 8 heads is only 400 query blocks).
 //
 // Reference semantics: flash_attention_half (src/lesiondiffusion_mlx/_attention_half.py:
 // 23-114): scores scaled by scale*log2(e) in fp32 (:70-72), exp2 online softmax
-// (:74-92), probabilities rounded to fp16 for the PV product (:86), output
-// half(o / l) (:105-113); plus the additive mask of mx.fast.scaled_dot_product_attention
+// (:74-92), probabilities rounded to fp16 for the PV product (:86), output half(o / l)
+// (:105-113); plus the additive mask of mx.fast.scaled_dot_product_attention
 // (mlx_model.py:843-847, 860-862).
 
 #include "common.h"
@@ -29,67 +34,67 @@ struct AttnParams {
   const float* mask; int64_t ms0, ms1, ms2, ms3;
 };
 
-template <int D, int FQ, int KB>
+__device__ __forceinline__ f32x16 mfma32x(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int D, int SPLIT>
 __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
-  constexpr int DK = D >= 32 ? D / 32 : 1;   // K-steps of the QK^T product
-  constexpr int DB = D / 16;                 // 16-row blocks of O^T
-  constexpr int KR = KB / 16;                // 16-key row blocks of S^T
-  constexpr int KJ = KB / 32;                // 32-key K-steps of the PV product
-  constexpr int KP = D + 8;                  // K tile pitch (halves)
-  constexpr int VP = KB + 8;                 // V^T tile pitch (halves)
-  constexpr int CPR = D / 8;                 // 16-byte chunks per key row
-  constexpr int NCH = KB * CPR;              // chunks per tile
-  constexpr int CPT = (NCH + 255) / 256;     // chunks per thread
-  __shared__ __attribute__((aligned(16))) f16 Ks[KB * KP];
-  __shared__ __attribute__((aligned(16))) f16 Vt[D * VP];
+  constexpr int KB = 32;                      // keys per block
+  constexpr int DK = D >= 16 ? D / 16 : 1;    // 16-wide k-steps of Q K^T
+  constexpr int DB = D >= 32 ? D / 32 : 1;    // 32-row blocks of O^T
+  constexpr int KP = D + 8;                   // K tile pitch (halves)
+  constexpr int VP = KB + 8;                  // V^T tile pitch (halves)
+  constexpr int CPR = D / 8;                  // 16-byte chunks per key row
+  constexpr int NCH = KB * CPR;               // chunks per tile
+  constexpr int TPT = SPLIT == 1 ? 256 : 64;  // threads loading one tile
+  constexpr int CPT = (NCH + TPT - 1) / TPT;  // chunks per loading thread
+  constexpr int TILE = KB * KP + D * VP;      // halves per (K, V^T) tile pair
+  constexpr int NT = SPLIT == 1 ? 1 : 4;      // tile pairs in LDS
+  constexpr int MERGE = SPLIT == 1 ? 0 : 4 * (D * 32 + 64);  // floats for the merge
+  constexpr int LDS_H = NT * TILE > MERGE * 2 ? NT * TILE : MERGE * 2;
+  __shared__ __attribute__((aligned(16))) f16 smem[LDS_H];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int g = lane >> 4, col = lane & 15;
+  const int hf = lane >> 5, col = lane & 31;
   const int h = blockIdx.y, b = blockIdx.z;
-  const int q0 = blockIdx.x * (64 * FQ) + wave * 16 * FQ;
+  const int q0 = SPLIT == 1 ? blockIdx.x * 128 + wave * 32 : blockIdx.x * 32;
+  const int tile_id = SPLIT == 1 ? 0 : wave;
+  f16* Ks = smem + tile_id * TILE;
+  f16* Vt = Ks + KB * KP;
+  const int ltid = SPLIT == 1 ? threadIdx.x : lane;  // loader index within the tile's threads
+
   const f16* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
   const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
   const f16* vb = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
 
-  // Q^T fragments: lane holds query q0+fq*16+col, dims dk*32 + 8g .. +7.
-  f16x8 qf[FQ][DK];
+  // Q^T fragments: lane holds query q0 + col, dims 16*dk + 8*hf .. +7.
+  const int qi = min(q0 + col, p.L - 1);
+  f16x8 qf[DK];
 #pragma unroll
-  for (int fq = 0; fq < FQ; fq++) {
-    const int qi = min(q0 + fq * 16 + col, p.L - 1);
-#pragma unroll
-    for (int dk = 0; dk < DK; dk++) {
-      const int d = dk * 32 + 8 * g;
-      f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (d < D) v = *reinterpret_cast<const f16x8*>(qb + (int64_t)qi * p.qs1 + d);
-      qf[fq][dk] = v;
-    }
+  for (int dk = 0; dk < DK; dk++) {
+    const int d = dk * 16 + 8 * hf;
+    f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (d < D) v = *reinterpret_cast<const f16x8*>(qb + (int64_t)qi * p.qs1 + d);
+    qf[dk] = v;
   }
+  const float* mrow = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi * p.ms2 : nullptr;
 
-  f32x4 o[DB][FQ];
+  f32x16 o[DB];
 #pragma unroll
   for (int i = 0; i < DB; i++)
 #pragma unroll
-    for (int j = 0; j < FQ; j++) o[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  float m[FQ], l[FQ];
-#pragma unroll
-  for (int j = 0; j < FQ; j++) { m[j] = -INFINITY; l[j] = 0.f; }
+    for (int e = 0; e < 16; e++) o[i][e] = 0.f;
+  float m = -INFINITY, l = 0.f;
 
-  const float* mrow[FQ];
-#pragma unroll
-  for (int fq = 0; fq < FQ; fq++) {
-    const int qi = min(q0 + fq * 16 + col, p.L - 1);
-    mrow[fq] = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi * p.ms2 : nullptr;
-  }
-
-  // Register staging of the next tile.
   f16x8 kst[CPT], vst[CPT];
   auto load_tile = [&](int kbase) {
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
-      const int ch = threadIdx.x + i * 256;
-      const int key = ch / CPR, dc = ch - key * CPR;
+      const int chn = ltid + i * TPT;
+      const int key = chn / CPR, dc = chn - key * CPR;
       f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
-      if (ch < NCH && kbase + key < p.LK) {
+      if (chn < NCH && kbase + key < p.LK) {
         kv = *reinterpret_cast<const f16x8*>(kb_ + (int64_t)(kbase + key) * p.ks1 + dc * 8);
         vv = *reinterpret_cast<const f16x8*>(vb + (int64_t)(kbase + key) * p.vs1 + dc * 8);
       }
@@ -99,9 +104,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   auto store_tile = [&]() {
 #pragma unroll
     for (int i = 0; i < CPT; i++) {
-      const int ch = threadIdx.x + i * 256;
-      if (ch < NCH) {
-        const int key = ch / CPR, dc = ch - key * CPR;
+      const int chn = ltid + i * TPT;
+      if (chn < NCH) {
+        const int key = chn / CPR, dc = chn - key * CPR;
         *reinterpret_cast<f16x8*>(Ks + key * KP + dc * 8) = kst[i];
 #pragma unroll
         for (int e = 0; e < 8; e++) Vt[(dc * 8 + e) * VP + key] = vst[i][e];
@@ -110,110 +115,154 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   };
 
   const int nblk = (p.LK + KB - 1) / KB;
-  load_tile(0);
-  for (int blk = 0; blk < nblk; blk++) {
+  const int nit = SPLIT == 1 ? nblk : (nblk + 3) / 4;   // uniform trip count per wave
+  auto blk_of = [&](int it) { return SPLIT == 1 ? it : it * 4 + wave; };
+  if (blk_of(0) < nblk) load_tile(blk_of(0) * KB);
+  for (int it = 0; it < nit; it++) {
+    const int blk = blk_of(it);
+    const bool live = blk < nblk;
     const int kbase = blk * KB;
     __syncthreads();
-    store_tile();
+    if (live) store_tile();
     __syncthreads();
-    if (blk + 1 < nblk) load_tile(kbase + KB);
+    if (it + 1 < nit && blk_of(it + 1) < nblk) load_tile(blk_of(it + 1) * KB);
+    if (!live) continue;
 
-    // S^T = K Q^T
-    f32x4 s[KR][FQ];
+    // S^T = K Q^T: rows = keys, columns = queries.
+    f32x16 s;
 #pragma unroll
-    for (int kr = 0; kr < KR; kr++)
+    for (int e = 0; e < 16; e++) s[e] = 0.f;
 #pragma unroll
-      for (int fq = 0; fq < FQ; fq++) s[kr][fq] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kr = 0; kr < KR; kr++) {
-#pragma unroll
-      for (int dk = 0; dk < DK; dk++) {
-        const int d = dk * 32 + 8 * g;
-        f16x8 kf = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (d < D) kf = *reinterpret_cast<const f16x8*>(Ks + (kr * 16 + col) * KP + d);
-#pragma unroll
-        for (int fq = 0; fq < FQ; fq++) s[kr][fq] = mfma16(kf, qf[fq][dk], s[kr][fq]);
-      }
+    for (int dk = 0; dk < DK; dk++) {
+      const int d = dk * 16 + 8 * hf;
+      f16x8 kf = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (d < D) kf = *reinterpret_cast<const f16x8*>(Ks + col * KP + d);
+      s = mfma32x(kf, qf[dk], s);
     }
-
-    // Online softmax per query column.
-    f16x8 pf[KJ][FQ];
+    // Lane holds keys kbase + (e/4)*8 + 4*hf + e%4 of query q0 + col.
+    float top = -INFINITY;
 #pragma unroll
-    for (int fq = 0; fq < FQ; fq++) {
-      float top = -INFINITY;
-#pragma unroll
-      for (int kr = 0; kr < KR; kr++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int key = kbase + kr * 16 + 4 * g + r;
-          float t = s[kr][fq][r] * p.c;
-          if (mrow[fq] && key < p.LK) t += mrow[fq][(int64_t)key * p.ms3] * 1.44269504088896341f;
-          if (key >= p.LK) t = -INFINITY;
-          s[kr][fq][r] = t;
-          top = fmaxf(top, t);
-        }
-      top = fmaxf(top, __shfl_xor(top, 16));
-      top = fmaxf(top, __shfl_xor(top, 32));
-      const float mn = fmaxf(m[fq], top);
-      // A row with every key so far removed keeps m = -inf: contribute nothing.
-      const float base = mn == -INFINITY ? 0.f : mn;
-      const float alpha = exp2f(m[fq] - base);
-      m[fq] = mn;
-      float sum = 0.f;
-#pragma unroll
-      for (int kr = 0; kr < KR; kr++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float e = exp2f(s[kr][fq][r] - base);
-          sum += e;
-          pf[kr >> 1][fq][(kr & 1) * 4 + r] = (f16)e;
-        }
-      l[fq] = l[fq] * alpha + sum;
-#pragma unroll
-      for (int db = 0; db < DB; db++) o[db][fq] *= alpha;
+    for (int e = 0; e < 16; e++) {
+      const int key = kbase + (e >> 2) * 8 + 4 * hf + (e & 3);
+      float t = s[e] * p.c;
+      if (key >= p.LK) t = -INFINITY;
+      else if (mrow) t += mrow[(int64_t)key * p.ms3] * 1.44269504088896341f;
+      s[e] = t;
+      top = fmaxf(top, t);
     }
-
-    // O^T += V^T P^T
+    top = fmaxf(top, __shfl_xor(top, 32));
+    const float mn = fmaxf(m, top);
+    // A query with every key so far removed keeps m = -inf and contributes nothing.
+    const float base = mn == -INFINITY ? 0.f : mn;
+    const float alpha = exp2f(m - base);
+    m = mn;
+    float sum = 0.f;
+    f16x8 pf[2];
 #pragma unroll
-    for (int kj = 0; kj < KJ; kj++) {
+    for (int e = 0; e < 16; e++) {
+      const float ev = exp2f(s[e] - base);
+      sum += ev;
+      pf[e >> 3][e & 7] = (f16)ev;
+    }
+    l = l * alpha + sum;
+    // Rescale only when some query's running max moved (wave-uniform test).
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int db = 0; db < DB; db++) o[db] *= alpha;
+    }
+    // O^T += V^T P^T over two 16-key k-steps; the k ordering matches pf's registers.
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
       for (int db = 0; db < DB; db++) {
-        const f16* vr = Vt + (db * 16 + col) * VP + kj * 32 + 4 * g;
-        const f16x4 lo = *reinterpret_cast<const f16x4*>(vr);
-        const f16x4 hi = *reinterpret_cast<const f16x4*>(vr + 16);
-        const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-        for (int fq = 0; fq < FQ; fq++) o[db][fq] = mfma16(vf, pf[kj][fq], o[db][fq]);
+        const int d = db * 32 + col;
+        f16x8 vf = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (d < D) {
+          const f16* vr = Vt + d * VP + ks * 16 + 4 * hf;
+          const f16x4 lo = *reinterpret_cast<const f16x4*>(vr);
+          const f16x4 hi = *reinterpret_cast<const f16x4*>(vr + 8);
+          vf = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        o[db] = mfma32x(vf, pf[ks], o[db]);
       }
     }
   }
+  l += __shfl_xor(l, 32);
 
-  // Normalise and store: lane holds dims db*16 + 4g + r of query q0+fq*16+col.
   f16* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
+  const int qo = q0 + col;
+  if constexpr (SPLIT == 1) {
+    if (qo < p.L) {
+      const float inv = l > 0.f ? 1.0f / l : 0.f;
+      f16* orow = ob + (int64_t)qo * p.os1;
 #pragma unroll
-  for (int fq = 0; fq < FQ; fq++) {
-    float tot = l[fq];
-    tot += __shfl_xor(tot, 16);
-    tot += __shfl_xor(tot, 32);
-    const int qi = q0 + fq * 16 + col;
-    if (qi >= p.L) continue;
-    const float inv = tot > 0.f ? 1.0f / tot : 0.f;
-    f16* orow = ob + (int64_t)qi * p.os1;
+      for (int db = 0; db < DB; db++)
 #pragma unroll
-    for (int db = 0; db < DB; db++) {
-      f16x4 out;
+        for (int j = 0; j < 4; j++) {
+          const int d = db * 32 + j * 8 + 4 * hf;
+          if (d < D) {
+            f16x4 out;
 #pragma unroll
-      for (int r = 0; r < 4; r++) out[r] = (f16)(o[db][fq][r] * inv);
-      *reinterpret_cast<f16x4*>(orow + db * 16 + 4 * g) = out;
+            for (int r = 0; r < 4; r++) out[r] = (f16)(o[db][j * 4 + r] * inv);
+            *reinterpret_cast<f16x4*>(orow + d) = out;
+          }
+        }
+    }
+  } else {
+    // Merge the four waves' states: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
+    float* mo = reinterpret_cast<float*>(smem);            // [4][D][32] partial O^T
+    float* ml = mo + 4 * D * 32;                            // [4][32] m, then [4][32] l
+    __syncthreads();
+#pragma unroll
+    for (int db = 0; db < DB; db++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int d = db * 32 + (e >> 2) * 8 + 4 * hf + (e & 3);
+        if (d < D) mo[(wave * D + d) * 32 + col] = o[db][e];
+      }
+    if (hf == 0) { ml[wave * 32 + col] = m; ml[128 + wave * 32 + col] = l; }
+    __syncthreads();
+    // Thread t finishes query t % 32 for dims (t / 32) * 8 .. + 8 (D up to 64 per pass).
+    for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += 256) {
+      const int qq = idx & 31, d4 = (idx >> 5) * 4;
+      float mw[4], M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < 4; w++) { mw[w] = ml[w * 32 + qq]; M = fmaxf(M, mw[w]); }
+      const float bse = M == -INFINITY ? 0.f : M;
+      float den = 0.f, f[4];
+#pragma unroll
+      for (int w = 0; w < 4; w++) { f[w] = exp2f(mw[w] - bse); den += f[w] * ml[128 + w * 32 + qq]; }
+      const float inv = den > 0.f ? 1.0f / den : 0.f;
+      const int qg = q0 + qq;
+      if (qg < p.L) {
+        f16x4 out;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          float acc = 0.f;
+#pragma unroll
+          for (int w = 0; w < 4; w++) acc += f[w] * mo[(w * D + d4 + r) * 32 + qq];
+          out[r] = (f16)(acc * inv);
+        }
+        *reinterpret_cast<f16x4*>(ob + (int64_t)qg * p.os1 + d4) = out;
+      }
     }
   }
 }
 
-template <int D, int FQ, int KB>
+template <int D, int SPLIT>
 static int launch_attn(const AttnParams& p, hipStream_t st) {
-  dim3 grid((unsigned)((p.L + 64 * FQ - 1) / (64 * FQ)), (unsigned)p.H, (unsigned)p.B);
-  hipLaunchKernelGGL((attention_kernel<D, FQ, KB>), grid, dim3(256), 0, st, p);
+  const int per = SPLIT == 1 ? 128 : 32;
+  dim3 grid((unsigned)((p.L + per - 1) / per), (unsigned)p.H, (unsigned)p.B);
+  hipLaunchKernelGGL((attention_kernel<D, SPLIT>), grid, dim3(256), 0, st, p);
   return check_launch("attention");
+}
+
+template <int D>
+static int launch_d(const AttnParams& p, hipStream_t st) {
+  // Key-split workgroups when 128-query workgroups would leave most CUs idle.
+  const int64_t wgs = (int64_t)((p.L + 127) / 128) * p.H * p.B;
+  if (D <= 128 && wgs < 512 && p.LK > 64) return launch_attn<D, D <= 128 ? 4 : 1>(p, st);
+  return launch_attn<D, 1>(p, st);
 }
 
 }  // namespace ldx
@@ -247,10 +296,10 @@ extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
   p.ms0 = a->mask_stride[0]; p.ms1 = a->mask_stride[1]; p.ms2 = a->mask_stride[2]; p.ms3 = a->mask_stride[3];
   hipStream_t st = as_stream(stream);
   switch (D) {
-    case 16: return launch_attn<16, 1, 64>(p, st);
-    case 32: return launch_attn<32, 1, 64>(p, st);
-    case 64: return launch_attn<64, 1, 64>(p, st);
-    case 128: return launch_attn<128, 1, 32>(p, st);
-    default: return launch_attn<256, 1, 32>(p, st);
+    case 16: return launch_d<16>(p, st);
+    case 32: return launch_d<32>(p, st);
+    case 64: return launch_d<64>(p, st);
+    case 128: return launch_d<128>(p, st);
+    default: return launch_d<256>(p, st);
   }
 }

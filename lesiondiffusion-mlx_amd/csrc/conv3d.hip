@@ -530,7 +530,7 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   const int nchunks = (p.C + t.CC - 1) / t.CC;
   p.split = 1;
   p.cps = nchunks;
-  if (wgs < 192 && nchunks > 1) {
+  if (wgs < 192 && nchunks > 1 && p.taps > 1 && p.C >= 128) {
     int want = (int)((512 + wgs - 1) / wgs);
     if (want > nchunks) want = nchunks;
     p.cps = (nchunks + want - 1) / want;

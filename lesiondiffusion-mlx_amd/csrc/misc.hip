@@ -137,57 +137,70 @@ template <int V>
 __global__ __launch_bounds__(256) void gn_partial_kernel(
     const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,
     int C, int G, int64_t S, int64_t chunk, float* __restrict__ partial, int nchunks) {
+  // Thread t owns channels [lane_c, lane_c + V) of voxels vsub, vsub + vpi, ... of the
+  // chunk and sums (x - K_c) and (x - K_c)^2 with K_c the channel's value at the chunk's
+  // first voxel (a shift that keeps the variance free of cancellation).
   __shared__ float s_sum[256 * V];
   __shared__ float s_sq[256 * V];
-  __shared__ float s_n[256];
+  __shared__ float c_n[2048], c_mean[2048], c_m2[2048];
   const int b = blockIdx.y;
   const int ch = blockIdx.x;
-  const int tpv = C / V;                // threads per voxel
-  const int vpi = 256 / tpv;            // voxels per iteration
+  const int tpv = C / V;
+  const int vpi = 256 / tpv;
   const int t = threadIdx.x;
-  const int lane_c = (t % tpv) * V;     // first channel of this thread
+  const int lane_c = (t % tpv) * V;
   const int vsub = t / tpv;
   const bool active = vsub < vpi;
-  float sum[V], sq[V];
-#pragma unroll
-  for (int e = 0; e < V; e++) { sum[e] = 0.f; sq[e] = 0.f; }
-  float n = 0.f;
   const int64_t v_begin = (int64_t)ch * chunk;
   const int64_t v_end = min(S, v_begin + chunk);
+  auto src_of = [&](int64_t v) {
+    const int64_t vi = (int64_t)b * S + v;
+    return lane_c < C0 ? x0 + vi * p0 + lane_c : x1 + vi * p1 + (lane_c - C0);
+  };
+  float k[V], sum[V], sq[V];
+  {
+    const f16* s0 = src_of(v_begin);
+#pragma unroll
+    for (int e = 0; e < V; e++) { k[e] = (float)s0[e]; sum[e] = 0.f; sq[e] = 0.f; }
+  }
   if (active) {
     for (int64_t v = v_begin + vsub; v < v_end; v += vpi) {
-      const int64_t vi = (int64_t)b * S + v;
-      const f16* src = lane_c < C0 ? x0 + vi * p0 + lane_c : x1 + vi * p1 + (lane_c - C0);
+      const f16* src = src_of(v);
       if constexpr (V == 8) {
         const f16x8 h = *reinterpret_cast<const f16x8*>(src);
 #pragma unroll
-        for (int e = 0; e < 8; e++) { const float f = (float)h[e]; sum[e] += f; sq[e] += f * f; }
+        for (int e = 0; e < 8; e++) { const float f = (float)h[e] - k[e]; sum[e] += f; sq[e] += f * f; }
       } else {
 #pragma unroll
-        for (int e = 0; e < V; e++) { const float f = (float)src[e]; sum[e] += f; sq[e] += f * f; }
+        for (int e = 0; e < V; e++) { const float f = (float)src[e] - k[e]; sum[e] += f; sq[e] += f * f; }
       }
-      n += 1.f;
     }
   }
 #pragma unroll
   for (int e = 0; e < V; e++) {
-    // per-thread per-channel mean and M2
-    const float mean = n > 0.f ? sum[e] / n : 0.f;
-    s_sum[t * V + e] = mean;
-    s_sq[t * V + e] = n > 0.f ? fmaxf(sq[e] - sum[e] * mean, 0.f) : 0.f;
+    s_sum[t * V + e] = active ? sum[e] : 0.f;
+    s_sq[t * V + e] = active ? sq[e] : 0.f;
   }
-  s_n[t] = active ? n : 0.f;
+  __syncthreads();
+  // Per channel: add the vpi thread partials (same shift), then (n, mean, M2).
+  const float n_c = (float)(v_end - v_begin);
+  for (int c = t; c < C; c += 256) {
+    const int tc = c / V, e = c % V;
+    float a = 0.f, q = 0.f;
+    for (int vs = 0; vs < vpi; vs++) { a += s_sum[(vs * tpv + tc) * V + e]; q += s_sq[(vs * tpv + tc) * V + e]; }
+    const f16* s0 = c < C0 ? x0 + ((int64_t)b * S + v_begin) * p0 + c
+                           : x1 + ((int64_t)b * S + v_begin) * p1 + (c - C0);
+    const float kc = (float)*s0;
+    const float m = a / n_c;
+    c_n[c] = n_c;
+    c_mean[c] = kc + m;
+    c_m2[c] = fmaxf(q - a * m, 0.f);
+  }
   __syncthreads();
   const int gs = C / G;
   for (int g = t; g < G; g += 256) {
     Moments m = {0.f, 0.f, 0.f};
-    for (int vs = 0; vs < vpi; vs++) {
-      for (int c = g * gs; c < (g + 1) * gs; c++) {
-        const int tt = vs * tpv + c / V;
-        const int e = c % V;
-        m = merge(m, Moments{s_n[tt], s_sum[tt * V + e], s_sq[tt * V + e]});
-      }
-    }
+    for (int c = g * gs; c < (g + 1) * gs; c++) m = merge(m, Moments{c_n[c], c_mean[c], c_m2[c]});
     float* out = partial + (((int64_t)b * nchunks + ch) * G + g) * 3;
     out[0] = m.n; out[1] = m.mean; out[2] = m.m2;
   }
@@ -226,10 +239,10 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(
 }
 
 static int64_t gn_chunk(int64_t S, int batch) {
-  // aim for >= ~512 workgroups in pass 1, chunks of 64..4096 voxels
-  int64_t per = (S * batch + 511) / 512;
+  // about 256 workgroups in pass 1 (one per CU), chunks of 64 .. 8192 voxels
+  int64_t per = (S * batch + 255) / 256;
   if (per < 64) per = 64;
-  if (per > 4096) per = 4096;
+  if (per > 8192) per = 8192;
   return per;
 }
 
@@ -423,6 +436,7 @@ extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, con
   const bool vec = C % 8 == 0 && c0 % 8 == 0 && p0 % 8 == 0 && (c1 <= 0 || p1 % 8 == 0) &&
                    (uintptr_t)x0 % 16 == 0 && (c1 <= 0 || (uintptr_t)x1 % 16 == 0) && C / 8 <= 256;
   if (!vec && C > 256) return fail("group_norm_affine: unaligned input with more than 256 channels");
+  if (C > 2048) return fail("group_norm_affine: more than 2048 channels");
   const int64_t chunk = gn_chunk(voxels, batch);
   const int64_t nchunks = (voxels + chunk - 1) / chunk;
   if (nchunks > 0x7fffffff || batch > 65535 || groups > 65535) return fail("group_norm_affine: too large");

@@ -24,8 +24,32 @@ from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, check, lib
 __all__ = [
     "PackedWeight", "pack_weight", "pack_upsample_weight", "nax_conv3d", "conv3d", "dense",
     "group_norm_affine", "layer_norm", "attention", "flash_attention", "timestep_embedding",
-    "silu", "upsample_nearest2", "resize_nearest", "output_extent",
+    "silu", "upsample_nearest2", "resize_nearest", "output_extent", "count_flops",
 ]
+
+
+class count_flops:
+    """Context manager tallying the algorithmic FLOPs (2 x real multiply-adds, no
+    padding; a folded upsample conv counts its 8 taps) of the convs, dense layers and
+    attention launched inside it -- for throughput figures."""
+
+    active: "count_flops | None" = None
+
+    def __init__(self) -> None:
+        self.conv = 0.0
+        self.dense = 0.0
+        self.attention = 0.0
+
+    @property
+    def total(self) -> float:
+        return self.conv + self.dense + self.attention
+
+    def __enter__(self) -> "count_flops":
+        count_flops.active = self
+        return self
+
+    def __exit__(self, *exc) -> None:
+        count_flops.active = None
 
 
 def _stream() -> ctypes.c_void_p:
@@ -224,6 +248,13 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
             raise ValueError(f"shift must be (B, O) = {(b, o)} with contiguous channels")
         a.shift, a.shift_pitch = shift.data_ptr(), shift.stride(0) if b > 1 else o
     a.y, a.y_pitch = out.data_ptr(), yp
+    if count_flops.active is not None:
+        taps = 8 if upsample else packed.ksize ** 3
+        flops = 2.0 * b * grid[0] * grid[1] * grid[2] * o * (c0 + c1) * taps
+        if packed.ksize == 1 and d == 1 and h == 1:
+            count_flops.active.dense += flops
+        else:
+            count_flops.active.conv += flops
     ws_bytes = lib.ldx_conv3d_workspace_bytes(ctypes.byref(a))
     ws = None
     if ws_bytes:
@@ -361,6 +392,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
     out = torch.empty((b, h, lq, d), dtype=torch.float16, device=q.device)
     m = _prepare_mask(mask, b, h, lq, lk, q.device)
     a = _attn_args(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2), scale, m)
+    if count_flops.active is not None:
+        count_flops.active.attention += 4.0 * b * h * lq * lk * d
     check(lib.ldx_attention(ctypes.byref(a), _stream()), "attention")
     return out
 
@@ -386,6 +419,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
     a = _attn_args(q.view(b, lq, heads, d) if q.is_contiguous() else q.unflatten(2, (heads, d)),
                    k.unflatten(2, (heads, d)), v.unflatten(2, (heads, d)), out.unflatten(2, (heads, d)),
                    scale, None)
+    if count_flops.active is not None:
+        count_flops.active.attention += 4.0 * b * heads * lq * lk * d
     check(lib.ldx_attention(ctypes.byref(a), _stream()), "attention")
     return out
 
