@@ -34,7 +34,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (3); bumped on any change to the structs below. */
+/* ABI version (4); bumped on any change to the structs below. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -145,7 +145,9 @@ int ldx_layer_norm(const void* x, int64_t x_pitch, int64_t rows, int32_t feature
  * (head_dim stride must be 1); both the projection layout (B, L, H*D) and
  * (B, H, L, D) are views of this. head_dim in {16, 32, 64, 128, 256}.
  * mask (optional) is additive fp32 with strides (batch, head, query, key), 0 for a
- * broadcast axis; -inf removes a key; a query row with every key removed gives 0. */
+ * broadcast axis; -inf removes a key; a query row with every key removed gives 0.
+ * workspace (ldx_attention_workspace_bytes) receives a key-contiguous copy of V
+ * made at the start of the call, so the kernel stages V^T tiles with wide stores. */
 typedef struct ldx_attention_args {
   int32_t batch, heads, q_len, kv_len, head_dim;
   const void* q; int64_t q_stride[3];   /* batch, len, head strides (elements) */
@@ -154,8 +156,10 @@ typedef struct ldx_attention_args {
   void* o; int64_t o_stride[3];
   float scale;
   const float* mask; int64_t mask_stride[4];
+  void* workspace; size_t workspace_bytes;   /* device scratch, required */
 } ldx_attention_args;
 
+size_t ldx_attention_workspace_bytes(const ldx_attention_args* args);
 int ldx_attention(const ldx_attention_args* args, void* stream);
 
 /* ------------------------------------------------------------ small ops ---------

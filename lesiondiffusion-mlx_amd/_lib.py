@@ -59,6 +59,7 @@ class AttnArgs(ctypes.Structure):
         ("o", c_vp), ("o_stride", c_i64 * 3),
         ("scale", c_f32),
         ("mask", c_vp), ("mask_stride", c_i64 * 4),
+        ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -75,6 +76,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_group_norm_affine": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
                                       c_vp, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "ldx_layer_norm": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),
+    "ldx_attention_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(AttnArgs)]),
     "ldx_attention": (c_i32, [ctypes.POINTER(AttnArgs), c_vp]),
     "ldx_timestep_embedding": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_silu": (c_i32, [c_vp, c_i64, c_vp, c_vp]),
@@ -86,7 +88,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_step_advance": (c_i32, [c_vp, c_vp]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 def _load() -> ctypes.CDLL:

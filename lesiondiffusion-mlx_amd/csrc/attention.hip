@@ -6,8 +6,10 @@
 // for one query -- are already the B operand of O^T = V^T P^T: probabilities never
 // leave registers, and the running max / rescale / partial row sum of a query are
 // lane-local (its other 16 keys sit in lane ^ 32, one swizzle away). Q^T stays in
-// registers; K (row-major) and V^T (transposed on the LDS store) stream through LDS
-// with the next block's global loads in flight during the current block.
+// registers; K (row-major) and V^T (transposed once per call by transpose_v_kernel)
+// stream through LDS with 16-byte stores, the next block's global loads in flight
+// during the current block. Masking and key bounds are applied only on blocks that
+// need them; row sums use v_dot2 on the fp16 probabilities the PV product consumes.
 //
 // SPLIT = 1: a workgroup's 4 waves own 4 x 32 queries and share each K/V tile.
 // SPLIT = 4: the 4 waves own the same 32 queries and take interleaved key blocks with
@@ -28,7 +30,7 @@ struct AttnParams {
   int B, H, L, LK;
   const f16* q; int64_t qs0, qs1, qs2;
   const f16* k; int64_t ks0, ks1, ks2;
-  const f16* v; int64_t vs0, vs1, vs2;
+  const f16* vt; int64_t vtp;  // V^T: row ((b * H + h) * D + d), keys contiguous, pitch vtp
   f16* o; int64_t os0, os1, os2;
   float c;  // scale * log2(e)
   const float* mask; int64_t ms0, ms1, ms2, ms3;
@@ -38,6 +40,29 @@ __device__ __forceinline__ f32x16 mfma32x(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// V (B, LK, H, D) with strides -> V^T rows ((b * H + h) * D + d) of `pitch` keys, the
+// keys in [LK, pitch) zero. 32 keys x 32 dims per 256-thread tile.
+__global__ __launch_bounds__(256) void transpose_v_kernel(const f16* __restrict__ v, int64_t s0, int64_t s1,
+                                                          int64_t s2, int LK, int H, int D, int64_t pitch,
+                                                          f16* __restrict__ vt) {
+  __shared__ f16 tile[32][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int k0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
+  const int bh = blockIdx.z, b = bh / H, h = bh % H;
+  const f16* src = v + (int64_t)b * s0 + (int64_t)h * s2;
+  for (int i = ty; i < 32; i += 8) {
+    const int key = k0 + i, d = d0 + tx;
+    tile[i][tx] = (key < LK && d < D) ? src[(int64_t)key * s1 + d] : (f16)0;
+  }
+  __syncthreads();
+  for (int i = ty; i < 32; i += 8) {
+    const int d = d0 + i, key = k0 + tx;
+    if (d < D && key < pitch) vt[((int64_t)bh * D + d) * pitch + key] = tile[tx][i];
+  }
+}
+
 template <int D, int SPLIT>
 __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   constexpr int KB = 32;                      // keys per block
@@ -45,10 +70,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   constexpr int DB = D >= 32 ? D / 32 : 1;    // 32-row blocks of O^T
   constexpr int KP = D + 8;                   // K tile pitch (halves)
   constexpr int VP = KB + 8;                  // V^T tile pitch (halves)
-  constexpr int CPR = D / 8;                  // 16-byte chunks per key row
-  constexpr int NCH = KB * CPR;               // chunks per tile
+  constexpr int KCH = KB * (D / 8);           // 16-byte chunks of a K tile
+  constexpr int VCH = D * (KB / 8);           // 16-byte chunks of a V^T tile
   constexpr int TPT = SPLIT == 1 ? 256 : 64;  // threads loading one tile
-  constexpr int CPT = (NCH + TPT - 1) / TPT;  // chunks per loading thread
+  constexpr int KPT = (KCH + TPT - 1) / TPT;
+  constexpr int VPT = (VCH + TPT - 1) / TPT;
   constexpr int TILE = KB * KP + D * VP;      // halves per (K, V^T) tile pair
   constexpr int NT = SPLIT == 1 ? 1 : 4;      // tile pairs in LDS
   constexpr int MERGE = SPLIT == 1 ? 0 : 4 * (D * 32 + 64);  // floats for the merge
@@ -62,11 +88,11 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   const int tile_id = SPLIT == 1 ? 0 : wave;
   f16* Ks = smem + tile_id * TILE;
   f16* Vt = Ks + KB * KP;
-  const int ltid = SPLIT == 1 ? threadIdx.x : lane;  // loader index within the tile's threads
+  const int ltid = SPLIT == 1 ? threadIdx.x : lane;
 
   const f16* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
   const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
-  const f16* vb = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+  const f16* vtb = p.vt + ((int64_t)b * p.H + h) * D * p.vtp;
 
   // Q^T fragments: lane holds query q0 + col, dims 16*dk + 8*hf .. +7.
   const int qi = min(q0 + col, p.L - 1);
@@ -87,30 +113,37 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     for (int e = 0; e < 16; e++) o[i][e] = 0.f;
   float m = -INFINITY, l = 0.f;
 
-  f16x8 kst[CPT], vst[CPT];
+  f16x8 kst[KPT], vst[VPT];
   auto load_tile = [&](int kbase) {
 #pragma unroll
-    for (int i = 0; i < CPT; i++) {
+    for (int i = 0; i < KPT; i++) {
       const int chn = ltid + i * TPT;
-      const int key = chn / CPR, dc = chn - key * CPR;
-      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0}, vv = kv;
-      if (chn < NCH && kbase + key < p.LK) {
+      const int key = chn / (D / 8), dc = chn % (D / 8);
+      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (chn < KCH && kbase + key < p.LK)
         kv = *reinterpret_cast<const f16x8*>(kb_ + (int64_t)(kbase + key) * p.ks1 + dc * 8);
-        vv = *reinterpret_cast<const f16x8*>(vb + (int64_t)(kbase + key) * p.vs1 + dc * 8);
-      }
-      kst[i] = kv; vst[i] = vv;
+      kst[i] = kv;
+    }
+#pragma unroll
+    for (int i = 0; i < VPT; i++) {
+      const int chn = ltid + i * TPT;
+      const int d = chn / (KB / 8), kc = chn % (KB / 8);
+      f16x8 vv = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (chn < VCH && kbase + kc * 8 < p.vtp)
+        vv = *reinterpret_cast<const f16x8*>(vtb + (int64_t)d * p.vtp + kbase + kc * 8);
+      vst[i] = vv;
     }
   };
   auto store_tile = [&]() {
 #pragma unroll
-    for (int i = 0; i < CPT; i++) {
+    for (int i = 0; i < KPT; i++) {
       const int chn = ltid + i * TPT;
-      if (chn < NCH) {
-        const int key = chn / CPR, dc = chn - key * CPR;
-        *reinterpret_cast<f16x8*>(Ks + key * KP + dc * 8) = kst[i];
+      if (chn < KCH) *reinterpret_cast<f16x8*>(Ks + (chn / (D / 8)) * KP + (chn % (D / 8)) * 8) = kst[i];
+    }
 #pragma unroll
-        for (int e = 0; e < 8; e++) Vt[(dc * 8 + e) * VP + key] = vst[i][e];
-      }
+    for (int i = 0; i < VPT; i++) {
+      const int chn = ltid + i * TPT;
+      if (chn < VCH) *reinterpret_cast<f16x8*>(Vt + (chn / (KB / 8)) * VP + (chn % (KB / 8)) * 8) = vst[i];
     }
   };
 
@@ -118,6 +151,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
   const int nit = SPLIT == 1 ? nblk : (nblk + 3) / 4;   // uniform trip count per wave
   auto blk_of = [&](int it) { return SPLIT == 1 ? it : it * 4 + wave; };
   if (blk_of(0) < nblk) load_tile(blk_of(0) * KB);
+  const f16x2 ones = {(f16)1, (f16)1};
   for (int it = 0; it < nit; it++) {
     const int blk = blk_of(it);
     const bool live = blk < nblk;
@@ -139,30 +173,46 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
       if (d < D) kf = *reinterpret_cast<const f16x8*>(Ks + col * KP + d);
       s = mfma32x(kf, qf[dk], s);
     }
-    // Lane holds keys kbase + (e/4)*8 + 4*hf + e%4 of query q0 + col.
-    float top = -INFINITY;
+    // Lane holds keys kbase + (e/4)*8 + 4*hf + e%4 of query q0 + col. Exponents are
+    // log2-scaled: t = s * scale * log2(e) (+ mask * log2(e)).
+    float mn, base;
+    if (kbase + KB <= p.LK && !mrow) {
+      float top = s[0];
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const int key = kbase + (e >> 2) * 8 + 4 * hf + (e & 3);
-      float t = s[e] * p.c;
-      if (key >= p.LK) t = -INFINITY;
-      else if (mrow) t += mrow[(int64_t)key * p.ms3] * 1.44269504088896341f;
-      s[e] = t;
-      top = fmaxf(top, t);
+      for (int e = 1; e < 16; e++) top = fmaxf(top, s[e]);
+      top = fmaxf(top, __shfl_xor(top, 32));
+      mn = fmaxf(m, top * p.c);
+      base = mn;
+#pragma unroll
+      for (int e = 0; e < 16; e++) s[e] = s[e] * p.c - base;
+    } else {
+      float top = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int key = kbase + (e >> 2) * 8 + 4 * hf + (e & 3);
+        float t = s[e] * p.c;
+        if (key >= p.LK) t = -INFINITY;
+        else if (mrow) t += mrow[(int64_t)key * p.ms3] * 1.44269504088896341f;
+        s[e] = t;
+        top = fmaxf(top, t);
+      }
+      top = fmaxf(top, __shfl_xor(top, 32));
+      mn = fmaxf(m, top);
+      // A query with every key so far removed keeps m = -inf and contributes nothing.
+      base = mn == -INFINITY ? 0.f : mn;
+#pragma unroll
+      for (int e = 0; e < 16; e++) s[e] -= base;
     }
-    top = fmaxf(top, __shfl_xor(top, 32));
-    const float mn = fmaxf(m, top);
-    // A query with every key so far removed keeps m = -inf and contributes nothing.
-    const float base = mn == -INFINITY ? 0.f : mn;
-    const float alpha = exp2f(m - base);
+    const float alpha = __builtin_amdgcn_exp2f(m - base);
     m = mn;
-    float sum = 0.f;
     f16x8 pf[2];
+    float sum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const float ev = exp2f(s[e] - base);
-      sum += ev;
-      pf[e >> 3][e & 7] = (f16)ev;
+    for (int e = 0; e < 16; e += 2) {
+      const f16x2 pr = {(f16)__builtin_amdgcn_exp2f(s[e]), (f16)__builtin_amdgcn_exp2f(s[e + 1])};
+      pf[e >> 3][e & 7] = pr[0];
+      pf[e >> 3][(e & 7) + 1] = pr[1];
+      sum = __builtin_amdgcn_fdot2(pr, ones, sum, false);
     }
     l = l * alpha + sum;
     // Rescale only when some query's running max moved (wave-uniform test).
@@ -269,7 +319,7 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
 
 using namespace ldx;
 
-extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
+static int check_attention_args(const ldx_attention_args* a) {
   if (!a) return fail("attention: null args");
   if (a->batch < 1 || a->heads < 1 || a->q_len < 1 || a->kv_len < 1)
     return fail("attention: empty shape (B %d H %d L %d LK %d)", a->batch, a->heads, a->q_len, a->kv_len);
@@ -277,24 +327,50 @@ extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
   if (D != 16 && D != 32 && D != 64 && D != 128 && D != 256)
     return fail("attention: head_dim %d not in {16, 32, 64, 128, 256}", D);
   if (!a->q || !a->k || !a->v || !a->o) return fail("attention: null tensor");
-  if (a->batch > 65535 || a->heads > 65535) return fail("attention: batch/heads too large");
+  if (a->batch > 65535 || a->heads > 65535 || (int64_t)a->batch * a->heads > 65535)
+    return fail("attention: batch x heads too large");
   const int64_t* ss[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
   const void* ps[4] = {a->q, a->k, a->v, a->o};
   for (int i = 0; i < 4; i++) {
     for (int j = 0; j < 3; j++)
-      if (ss[i][j] % 8 != 0) return fail("attention: strides must be multiples of 8 elements");
-    if ((uintptr_t)ps[i] % 16 != 0) return fail("attention: tensors must be 16-byte aligned");
+      if (ss[i][j] % 8 != 0 && i != 2) return fail("attention: strides must be multiples of 8 elements");
+    if ((uintptr_t)ps[i] % 16 != 0 && i != 2) return fail("attention: tensors must be 16-byte aligned");
   }
+  return LDX_OK;
+}
+
+static int64_t vt_pitch(const ldx_attention_args* a) { return ((int64_t)a->kv_len + 7) / 8 * 8; }
+
+extern "C" size_t ldx_attention_workspace_bytes(const ldx_attention_args* a) {
+  if (check_attention_args(a) != LDX_OK) return 0;
+  return (size_t)a->batch * a->heads * a->head_dim * vt_pitch(a) * sizeof(f16) + 256;
+}
+
+extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
+  int rc = check_attention_args(a);
+  if (rc != LDX_OK) return rc;
+  const size_t need = ldx_attention_workspace_bytes(a);
+  if (!a->workspace || a->workspace_bytes < need)
+    return fail("attention: workspace of %zu bytes required (got %zu)", need, a->workspace_bytes);
+  const int D = a->head_dim;
   AttnParams p{};
   p.B = a->batch; p.H = a->heads; p.L = a->q_len; p.LK = a->kv_len;
   p.q = (const f16*)a->q; p.qs0 = a->q_stride[0]; p.qs1 = a->q_stride[1]; p.qs2 = a->q_stride[2];
   p.k = (const f16*)a->k; p.ks0 = a->k_stride[0]; p.ks1 = a->k_stride[1]; p.ks2 = a->k_stride[2];
-  p.v = (const f16*)a->v; p.vs0 = a->v_stride[0]; p.vs1 = a->v_stride[1]; p.vs2 = a->v_stride[2];
   p.o = (f16*)a->o; p.os0 = a->o_stride[0]; p.os1 = a->o_stride[1]; p.os2 = a->o_stride[2];
   p.c = a->scale * 1.44269504088896341f;
   p.mask = a->mask;
   p.ms0 = a->mask_stride[0]; p.ms1 = a->mask_stride[1]; p.ms2 = a->mask_stride[2]; p.ms3 = a->mask_stride[3];
+  // 256-byte aligned V^T inside the workspace.
+  f16* vt = (f16*)(((uintptr_t)a->workspace + 255) & ~(uintptr_t)255);
+  p.vt = vt;
+  p.vtp = vt_pitch(a);
   hipStream_t st = as_stream(stream);
+  dim3 tg((unsigned)((p.vtp + 31) / 32), (unsigned)((D + 31) / 32), (unsigned)(p.B * p.H));
+  hipLaunchKernelGGL(transpose_v_kernel, tg, dim3(256), 0, st, (const f16*)a->v, a->v_stride[0],
+                     a->v_stride[1], a->v_stride[2], p.LK, p.H, D, p.vtp, vt);
+  rc = check_launch("attention: transpose V");
+  if (rc != LDX_OK) return rc;
   switch (D) {
     case 16: return launch_d<16>(p, st);
     case 32: return launch_d<32>(p, st);

@@ -358,6 +358,11 @@ def _attn_args(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, o4: torch.T
     if mask is not None:
         a.mask = mask.data_ptr()
         a.mask_stride[:] = [mask.stride(0), mask.stride(1), mask.stride(2), mask.stride(3)]
+    ws_bytes = lib.ldx_attention_workspace_bytes(ctypes.byref(a))
+    if ws_bytes:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q4.device)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+        a._keep = ws  # the buffer lives as long as the argument block
     return a
 
 
