@@ -32,6 +32,10 @@ sys.path.insert(0, str(REPO))
 METRIC = "conv3d & flash-attn TFLOP/s (% MFMA peak); ms per 3D-UNet denoise step"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+# HBM bytes per config-1 conv launch: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
+# this script with --copy-calibration, each divided by what the counter reports per byte
+# of a plain 512 MiB device copy (FETCH 0.5, WRITE 1.0); profiles/conv3d_config1.txt.
+CONV_CONFIG1_TRAFFIC_BYTES = 25.22e6
 
 
 def _graph_time(launch, steps: int, warmup: int) -> float:
@@ -271,7 +275,7 @@ def bench_config5(pkg, steps: int = 200) -> dict:
                       f"DDIM {prep.num_steps} steps, one HIP graph per step"}
 
 
-def cpu_baseline_conv(x, w, b, budget_s: float = 12.0) -> dict:
+def cpu_baseline_conv(x, w, b, budget_s: float = 15.0) -> dict:
     """The float64 oracle conv (oracle/conv.py) on the host cores, on a bounded sample:
     repeated full config-1 convolutions until ``budget_s`` seconds have elapsed."""
     from oracle import conv as ocv
@@ -285,12 +289,55 @@ def cpu_baseline_conv(x, w, b, budget_s: float = 12.0) -> dict:
         ocv.conv3d(xn, wn, bn)
         n += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or n >= 50:
+        if el >= budget_s:
             break
     flop = 2.0 * 51200 * 64 * 64 * 27
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": flop * n / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"{n} full config-1 convolutions (float64 NumPy oracle, per-tap BLAS products) in {el:.1f} s"}
+
+
+def cpu_torch_fp32(x, w, b, qkv) -> dict:
+    """torch CPU fp32 on the same seeded tensors (F.conv3d on channels_last_3d input,
+    F.scaled_dot_product_attention): median of 5 timed calls after one warm-up."""
+    import torch
+    import torch.nn.functional as F
+
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(cores)
+    xc = x.float().cpu().permute(0, 4, 1, 2, 3).contiguous(memory_format=torch.channels_last_3d)
+    wc, bc = w.float().cpu(), b.float().cpu()
+    q, k, v = (t.float().cpu() for t in qkv)
+
+    def med(fn):
+        fn()
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
+
+    with torch.no_grad():
+        tc = med(lambda: F.conv3d(xc, wc, bc, padding=1))
+        ta = med(lambda: F.scaled_dot_product_attention(q, k, v, scale=0.125))
+    return {"conv3d_tflops": round(2.0 * 51200 * 64 * 64 * 27 / tc / 1e12, 4), "conv3d_ms": round(tc * 1e3, 2),
+            "self_attention_tflops": round(4.0 * 8 * 1600 * 1600 * 64 / ta / 1e12, 4),
+            "self_attention_ms": round(ta * 1e3, 2), "cores": cores,
+            "note": "CPU baseline (torch, not MLX): the reference's mx.cpu path needs macOS arm64"}
+
+
+def copy_calibration(mib: int = 512, reps: int = 3) -> None:
+    """``reps`` plain device copies of ``mib`` MiB (larger than the 256 MiB last-level
+    cache): each reads and writes exactly ``mib`` MiB of HBM, so the counters these
+    launches report give the counter-to-byte factors."""
+    import torch
+
+    src = torch.ones(mib * 2 ** 20 // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
 
 
 def main() -> int:
@@ -300,6 +347,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-model", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 512 MiB device copy (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -313,6 +363,8 @@ def main() -> int:
     torch.cuda.synchronize()
     conv = bench_conv(pkg, args.steps, args.warmup)
     att = bench_attention(pkg, args.steps, args.warmup)
+    if args.copy_calibration:
+        copy_calibration()
     line = {
         "metric": METRIC,
         "value": round(conv["tflops"], 2),
@@ -330,7 +382,7 @@ def main() -> int:
                                "D x H x W = 32 x 40 x 40, seed 0", "global_batch": 1},
         "roofline": {"bound": "mfma", "achieved": round(conv["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(conv["tflops"] / PEAK_FP16_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": CONV_CONFIG1_TRAFFIC_BYTES},
         "attention": {
             "self_tflops": round(att["self"]["tflops"], 2), "self_ms": round(att["self"]["ms"], 5),
             "self_frac_peak": round(att["self"]["frac_peak"], 4),
@@ -345,6 +397,7 @@ def main() -> int:
         line["denoise_step"] = bench_config5(pkg, 200)
     if not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline_conv(conv["x"], conv["w"], conv["b"])
+        line["cpu_torch_fp32"] = cpu_torch_fp32(conv["x"], conv["w"], conv["b"], att["_tensors"])
     print(json.dumps(line))
     return 0
 

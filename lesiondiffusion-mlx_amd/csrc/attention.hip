@@ -42,6 +42,48 @@ __device__ __forceinline__ f32x16 mfma32x(f16x8 a, f16x8 b, f32x16 c) {
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor word 3): loads at
+// offsets past the extent return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// acc *= a with tied operands, so the branch that rescales leaves the accumulator in
+// the registers the other branch keeps it in (no copies across the loop). The compiler
+// does not see the asm's register reads and writes for MFMA hazards, so it waits out
+// the longest MFMA-result latency first (18 wait states for a 32x32 result read by
+// VALU) and the VALU-write-to-MFMA-read gap after.
+__device__ __forceinline__ void scale_in_place(f32x16& acc, float a) {
+  asm volatile(
+      "s_nop 7\n s_nop 7\n s_nop 3\n"
+      "v_mul_f32 %0, %16, %0\n v_mul_f32 %1, %16, %1\n v_mul_f32 %2, %16, %2\n v_mul_f32 %3, %16, %3\n"
+      "v_mul_f32 %4, %16, %4\n v_mul_f32 %5, %16, %5\n v_mul_f32 %6, %16, %6\n v_mul_f32 %7, %16, %7\n"
+      "v_mul_f32 %8, %16, %8\n v_mul_f32 %9, %16, %9\n v_mul_f32 %10, %16, %10\n v_mul_f32 %11, %16, %11\n"
+      "v_mul_f32 %12, %16, %12\n v_mul_f32 %13, %16, %13\n v_mul_f32 %14, %16, %14\n v_mul_f32 %15, %16, %15\n"
+      "s_nop 4"
+      : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]), "+v"(acc[4]), "+v"(acc[5]), "+v"(acc[6]),
+        "+v"(acc[7]), "+v"(acc[8]), "+v"(acc[9]), "+v"(acc[10]), "+v"(acc[11]), "+v"(acc[12]), "+v"(acc[13]),
+        "+v"(acc[14]), "+v"(acc[15])
+      : "v"(a));
+}
+
+// Max / sum of a value over lanes l and l ^ 32. v_permlane32_swap of v with itself
+// leaves each lane holding its own value and its partner's, one in each result.
+__device__ __forceinline__ float halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
 // V (B, LK, H, D) with strides -> V^T rows ((b * H + h) * D + d) of `pitch` keys, the
 // keys in [LK, pitch) zero. 32 keys x 32 dims per 256-thread tile.
 __global__ __launch_bounds__(256) void transpose_v_kernel(const f16* __restrict__ v, int64_t s0, int64_t s1,
@@ -63,31 +105,46 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const f16* __restrict_
   }
 }
 
+// The keys of a 32-key block are stored in LDS K-tile rows permuted by pi (bits 2 and 3
+// of the row swapped; pi is its own inverse). MFMA row r of S^T then holds key pi(r), so
+// a lane's score register e is key 16 * (e / 8) + 8 * hf + e % 8: the eight
+// probabilities of one PV k-step are eight consecutive keys, and the matching V^T
+// operand is one 16-byte read.
+__device__ __forceinline__ int key_row(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
+
+// Waves per SIMD >= 2 keeps the register budget at 256 VGPRs, so the MFMA accumulators
+// live in ordinary VGPRs (no accumulator-register copies around the softmax).
+template <int D>
+struct AttnOcc { static constexpr int waves = D <= 64 ? 2 : 1; };
+
 template <int D, int SPLIT>
-__global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOcc<D>::waves, 8)))
+void attention_kernel(AttnParams p) {
   constexpr int KB = 32;                      // keys per block
   constexpr int DK = D >= 16 ? D / 16 : 1;    // 16-wide k-steps of Q K^T
   constexpr int DB = D >= 32 ? D / 32 : 1;    // 32-row blocks of O^T
   constexpr int KP = D + 8;                   // K tile pitch (halves)
   constexpr int VP = KB + 8;                  // V^T tile pitch (halves)
-  constexpr int KCH = KB * (D / 8);           // 16-byte chunks of a K tile
+  constexpr int KG = D / 8;                   // 16-byte chunks per key row
+  constexpr int KCH = KB * KG;                // 16-byte chunks of a K tile
   constexpr int VCH = D * (KB / 8);           // 16-byte chunks of a V^T tile
   constexpr int TPT = SPLIT == 1 ? 256 : 64;  // threads loading one tile
   constexpr int KPT = (KCH + TPT - 1) / TPT;
   constexpr int VPT = (VCH + TPT - 1) / TPT;
+  constexpr bool KALL = KCH % TPT == 0, VALL = VCH % TPT == 0;
   constexpr int TILE = KB * KP + D * VP;      // halves per (K, V^T) tile pair
-  constexpr int NT = SPLIT == 1 ? 1 : 4;      // tile pairs in LDS
+  constexpr int NT = SPLIT == 1 ? 2 : 4;      // tile pairs in LDS
   constexpr int MERGE = SPLIT == 1 ? 0 : 4 * (D * 32 + 64);  // floats for the merge
   constexpr int LDS_H = NT * TILE > MERGE * 2 ? NT * TILE : MERGE * 2;
   __shared__ __attribute__((aligned(16))) f16 smem[LDS_H];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // The wave index is uniform; readfirstlane lets the compiler keep block indices,
+  // tile bases and loop conditions in scalar registers.
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hf = lane >> 5, col = lane & 31;
   const int h = blockIdx.y, b = blockIdx.z;
   const int q0 = SPLIT == 1 ? blockIdx.x * 128 + wave * 32 : blockIdx.x * 32;
-  const int tile_id = SPLIT == 1 ? 0 : wave;
-  f16* Ks = smem + tile_id * TILE;
-  f16* Vt = Ks + KB * KP;
+  f16* Ks = smem + (SPLIT == 1 ? 0 : wave) * TILE;  // SPLIT = 4: this wave's tile
   const int ltid = SPLIT == 1 ? threadIdx.x : lane;
 
   const f16* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
@@ -113,56 +170,76 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     for (int e = 0; e < 16; e++) o[i][e] = 0.f;
   float m = -INFINITY, l = 0.f;
 
+  // This thread's 16-byte chunks of a tile: K chunk i = key (chn / KG), dims
+  // (chn % KG) * 8, stored at LDS row key_row(key); V^T chunk i = dim row chn / 4, keys
+  // (chn % 4) * 8. Byte offsets from the tile base fit in 32 bits (the host bounds ks1
+  // and D * vtp).
+  unsigned koff[KPT], voff[VPT];
+  int kst_off[KPT], vst_off[VPT];
+#pragma unroll
+  for (int i = 0; i < KPT; i++) {
+    const int chn = ltid + i * TPT;
+    const int key = (chn / KG) & 31;
+    koff[i] = (unsigned)(key * p.ks1 + (chn % KG) * 8) * 2u;
+    kst_off[i] = key_row(key) * KP + (chn % KG) * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; i++) {
+    const int chn = ltid + i * TPT;
+    voff[i] = (unsigned)((chn >> 2) * p.vtp + (chn & 3) * 8) * 2u;
+    vst_off[i] = (chn >> 2) * VP + (chn & 3) * 8;
+  }
+
   f16x8 kst[KPT], vst[VPT];
+  // Tile loads through buffer resources whose extent ends at the last valid key:
+  // addresses need no per-lane arithmetic and rows past the key length read as zero.
+  // (V^T reads past a row's padded end wrap into the next row: finite values whose
+  // probabilities are zero.)
   auto load_tile = [&](int kbase) {
+    const int rows = min(KB, p.LK - kbase);
+    const auto kr = make_rsrc(kb_ + (int64_t)kbase * p.ks1, (unsigned)(((rows - 1) * p.ks1 + D) * 2));
+    const auto vr = make_rsrc(vtb + kbase, (unsigned)((D * p.vtp - kbase) * 2));
 #pragma unroll
-    for (int i = 0; i < KPT; i++) {
-      const int chn = ltid + i * TPT;
-      const int key = chn / (D / 8), dc = chn % (D / 8);
-      f16x8 kv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (chn < KCH && kbase + key < p.LK)
-        kv = *reinterpret_cast<const f16x8*>(kb_ + (int64_t)(kbase + key) * p.ks1 + dc * 8);
-      kst[i] = kv;
-    }
+    for (int i = 0; i < KPT; i++)
+      if (KALL || ltid + i * TPT < KCH) kst[i] = buffer_load16(kr, koff[i]);
 #pragma unroll
-    for (int i = 0; i < VPT; i++) {
-      const int chn = ltid + i * TPT;
-      const int d = chn / (KB / 8), kc = chn % (KB / 8);
-      f16x8 vv = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (chn < VCH && kbase + kc * 8 < p.vtp)
-        vv = *reinterpret_cast<const f16x8*>(vtb + (int64_t)d * p.vtp + kbase + kc * 8);
-      vst[i] = vv;
-    }
+    for (int i = 0; i < VPT; i++)
+      if (VALL || ltid + i * TPT < VCH) vst[i] = buffer_load16(vr, voff[i]);
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](f16* kd) {
+    f16* vd = kd + KB * KP;
 #pragma unroll
-    for (int i = 0; i < KPT; i++) {
-      const int chn = ltid + i * TPT;
-      if (chn < KCH) *reinterpret_cast<f16x8*>(Ks + (chn / (D / 8)) * KP + (chn % (D / 8)) * 8) = kst[i];
-    }
+    for (int i = 0; i < KPT; i++)
+      if (KALL || ltid + i * TPT < KCH) *reinterpret_cast<f16x8*>(kd + kst_off[i]) = kst[i];
 #pragma unroll
-    for (int i = 0; i < VPT; i++) {
-      const int chn = ltid + i * TPT;
-      if (chn < VCH) *reinterpret_cast<f16x8*>(Vt + (chn / (KB / 8)) * VP + (chn % (KB / 8)) * 8) = vst[i];
-    }
+    for (int i = 0; i < VPT; i++)
+      if (VALL || ltid + i * TPT < VCH) *reinterpret_cast<f16x8*>(vd + vst_off[i]) = vst[i];
   };
 
   const int nblk = (p.LK + KB - 1) / KB;
-  const int nit = SPLIT == 1 ? nblk : (nblk + 3) / 4;   // uniform trip count per wave
+  const int nit = SPLIT == 1 ? nblk : (nblk - wave + 3) / 4;   // this wave's blocks
   auto blk_of = [&](int it) { return SPLIT == 1 ? it : it * 4 + wave; };
-  if (blk_of(0) < nblk) load_tile(blk_of(0) * KB);
+  // Tile buffers: SPLIT = 1 double-buffers the shared tile (one barrier per block);
+  // SPLIT = 4 gives each wave one private tile, rewritten after the block's reads (LDS
+  // operations of one wave complete in program order).
+  auto tile_k = [&](int it) { return SPLIT == 1 ? smem + (it & 1) * TILE : Ks; };
+  if (nit > 0) {
+    load_tile(blk_of(0) * KB);
+    store_tile(tile_k(0));
+  }
+  if constexpr (SPLIT == 1) __syncthreads();
+  // All vector-memory loads so far (Q fragments, first tile) have landed; stating it
+  // keeps the loop's MFMAs from waiting on the in-flight prefetch of the next tile.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const f16x2 ones = {(f16)1, (f16)1};
   for (int it = 0; it < nit; it++) {
-    const int blk = blk_of(it);
-    const bool live = blk < nblk;
-    const int kbase = blk * KB;
-    __syncthreads();
-    if (live) store_tile();
-    __syncthreads();
-    if (it + 1 < nit && blk_of(it + 1) < nblk) load_tile(blk_of(it + 1) * KB);
-    if (!live) continue;
+    const int kbase = blk_of(it) * KB;
+    const bool more = it + 1 < nit;
+    if (more) load_tile(blk_of(it + 1) * KB);
+    const f16* Kc = tile_k(it);
+    const f16* Vc = Kc + KB * KP;
 
-    // S^T = K Q^T: rows = keys, columns = queries.
+    // S^T = K Q^T: rows = keys (permuted by key_row), columns = queries.
     f32x16 s;
 #pragma unroll
     for (int e = 0; e < 16; e++) s[e] = 0.f;
@@ -170,17 +247,18 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     for (int dk = 0; dk < DK; dk++) {
       const int d = dk * 16 + 8 * hf;
       f16x8 kf = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (d < D) kf = *reinterpret_cast<const f16x8*>(Ks + col * KP + d);
+      if (d < D) kf = *reinterpret_cast<const f16x8*>(Kc + col * KP + d);
       s = mfma32x(kf, qf[dk], s);
     }
-    // Lane holds keys kbase + (e/4)*8 + 4*hf + e%4 of query q0 + col. Exponents are
+    // Lane holds keys kbase + 16*(e/8) + 8*hf + e%8 of query q0 + col. Exponents are
     // log2-scaled: t = s * scale * log2(e) (+ mask * log2(e)).
     float mn, base;
     if (kbase + KB <= p.LK && !mrow) {
-      float top = s[0];
+      // med3(a, b, +inf) = max(a, b) without the operand canonicalisation fmaxf needs.
+      float top = __builtin_amdgcn_fmed3f(s[0], s[1], INFINITY);
 #pragma unroll
-      for (int e = 1; e < 16; e++) top = fmaxf(top, s[e]);
-      top = fmaxf(top, __shfl_xor(top, 32));
+      for (int e = 2; e < 16; e++) top = __builtin_amdgcn_fmed3f(top, s[e], INFINITY);
+      top = halves_max(top);
       mn = fmaxf(m, top * p.c);
       base = mn;
 #pragma unroll
@@ -189,14 +267,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
       float top = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        const int key = kbase + (e >> 2) * 8 + 4 * hf + (e & 3);
+        const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
         float t = s[e] * p.c;
         if (key >= p.LK) t = -INFINITY;
         else if (mrow) t += mrow[(int64_t)key * p.ms3] * 1.44269504088896341f;
         s[e] = t;
         top = fmaxf(top, t);
       }
-      top = fmaxf(top, __shfl_xor(top, 32));
+      top = halves_max(top);
       mn = fmaxf(m, top);
       // A query with every key so far removed keeps m = -inf and contributes nothing.
       base = mn == -INFINITY ? 0.f : mn;
@@ -218,26 +296,30 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
     // Rescale only when some query's running max moved (wave-uniform test).
     if (__ballot(alpha != 1.f)) {
 #pragma unroll
-      for (int db = 0; db < DB; db++) o[db] *= alpha;
+      for (int db = 0; db < DB; db++) scale_in_place(o[db], alpha);
     }
-    // O^T += V^T P^T over two 16-key k-steps; the k ordering matches pf's registers.
+    // O^T += V^T P^T over two 16-key k-steps: lane (hf, d) supplies keys 16*ks + 8*hf ..
+    // + 7 of dim d, the keys pf[ks] holds.
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
       for (int db = 0; db < DB; db++) {
         const int d = db * 32 + col;
         f16x8 vf = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (d < D) {
-          const f16* vr = Vt + d * VP + ks * 16 + 4 * hf;
-          const f16x4 lo = *reinterpret_cast<const f16x4*>(vr);
-          const f16x4 hi = *reinterpret_cast<const f16x4*>(vr + 8);
-          vf = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
+        if (d < D) vf = *reinterpret_cast<const f16x8*>(Vc + d * VP + ks * 16 + 8 * hf);
         o[db] = mfma32x(vf, pf[ks], o[db]);
       }
     }
+    if constexpr (SPLIT == 1) {
+      if (more) store_tile(tile_k(it + 1));
+      __syncthreads();
+    } else {
+      __builtin_amdgcn_wave_barrier();
+      if (more) store_tile(Ks);
+      __builtin_amdgcn_wave_barrier();
+    }
   }
-  l += __shfl_xor(l, 32);
+  l = halves_sum(l);
 
   f16* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
   const int qo = q0 + col;
@@ -272,7 +354,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnParams p) {
       }
     if (hf == 0) { ml[wave * 32 + col] = m; ml[128 + wave * 32 + col] = l; }
     __syncthreads();
-    // Thread t finishes query t % 32 for dims (t / 32) * 8 .. + 8 (D up to 64 per pass).
+    // Thread t finishes query t % 32 for dims (t / 32) * 4 .. + 4.
     for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += 256) {
       const int qq = idx & 31, d4 = (idx >> 5) * 4;
       float mw[4], M = -INFINITY;
@@ -336,6 +418,11 @@ static int check_attention_args(const ldx_attention_args* a) {
       if (ss[i][j] % 8 != 0 && i != 2) return fail("attention: strides must be multiples of 8 elements");
     if ((uintptr_t)ps[i] % 16 != 0 && i != 2) return fail("attention: tensors must be 16-byte aligned");
   }
+  // In-tile offsets are 32-bit: 32 key rows of K, D rows of the transposed V.
+  if (a->k_stride[1] < 0 || a->k_stride[1] > (1 << 25))
+    return fail("attention: key stride %lld out of range", (long long)a->k_stride[1]);
+  if ((int64_t)a->head_dim * (((int64_t)a->kv_len + 7) / 8 * 8) >= ((int64_t)1 << 31))
+    return fail("attention: kv_len %d too long for head_dim %d", a->kv_len, a->head_dim);
   return LDX_OK;
 }
 

@@ -1,18 +1,21 @@
-// Implicit-GEMM 3-D convolution on gfx950 MFMA (v_mfma_f32_16x16x32_f16).
+// Implicit-GEMM 3-D convolution on gfx950 MFMA (v_mfma_f32_32x32x16_f16).
 //
-// GEMM view: rows = output channels (A operand = packed weights, K-contiguous per
-// output channel), columns = output voxels (B operand = input channels of the
-// voxel's tap window, K-contiguous in NDHWC), K = taps x input channels.
+// GEMM view: rows = output channels (A operand = packed weights, fragment-major: one
+// 1 KB block per 32 output channels x 16 input channels, already in MFMA lane order),
+// columns = output voxels (B operand = input channels of the voxel's tap window,
+// K-contiguous in NDHWC), K = taps x input channels.
 //
-// A workgroup (4 waves) owns BO output channels x one brick of BV = TD*TH*TW
-// voxels of the "row grid" (output grid; source grid for the upsample fold). For
-// each chunk of CC input channels it stages the brick's halo -- the input voxels
-// every tap of every brick voxel reads -- into LDS once, applying the fused
-// GroupNorm affine + SiLU prologue and zero padding on the way. The tap loop then
-// reads B fragments from LDS at a per-lane base plus a workgroup-uniform tap offset
-// (no im2col buffer), while A fragments stream from L2 into registers one K-step
-// ahead. Epilogue: bias (per batch item optional), output scale, residual, one fp16
-// rounding, optional GELU, NDHWC store with a voxel pitch.
+// A workgroup (4 waves) owns BO output channels x one brick of BV = TD*TH*TW voxels
+// of the "row grid" (output grid; source grid for the upsample fold). For each chunk
+// of CC input channels it stages the brick's halo -- the input voxels every tap of
+// every brick voxel reads -- into LDS once, applying the fused GroupNorm affine + SiLU
+// prologue and zero padding on the way (no im2col buffer). The weight fragments of
+// one tap are staged through a two-slot LDS ring, the next tap's loaded into registers
+// while the current tap's MFMAs run. B fragments are read from the halo at a per-lane
+// base plus a workgroup-uniform tap offset. Epilogue: bias (per batch item optional),
+// fp16 shift, output scale, residual, one fp16 rounding, optional GELU / SiLU, NDHWC
+// store with a voxel pitch; or, split over channel chunks, fp32 partial planes that a
+// reduce kernel sums in a fixed order.
 //
 // Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619):
 // prologue _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421),
