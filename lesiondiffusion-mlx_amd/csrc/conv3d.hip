@@ -38,6 +38,7 @@ struct ConvParams {
   int HD, HH, HW;          // halo dims
   int ID0, IH0, IW0;       // halo origin offset: origin = brick_start * s - pad
   float rHW, rHH;          // 1 / HW, 1 / HH (host-rounded)
+  float rTW, rTH;          // 1 / TW, 1 / TH
   int RS;                  // halo row stride (halves): HW * (CC + 8) + row padding
   int NKC;                 // 16-channel K fragments of the packed weight
   int NOB;                 // 32-row output blocks of the packed weight
@@ -52,6 +53,7 @@ struct ConvParams {
   const f16* res; int64_t resp;
   float scale; int act;
   f16* y; int64_t yp; int yvec;
+  int ep_vec;              // 16-byte epilogue accesses: y, residual, shift, bias, partials aligned
 };
 
 __device__ __forceinline__ float gelu_erf(float v) {
@@ -72,7 +74,7 @@ __device__ __forceinline__ int fdiv(int t, float rcp) { return (int)(((float)t +
 // Stage the halo of one brick for channels [c0, c0 + CC) into LDS, applying the
 // affine + SiLU prologue and zero padding. Global loads are issued NB at a time before
 // any of them is consumed, so their latencies overlap.
-template <int CC, bool VEC>
+template <int CC, bool VEC, int NT>
 __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b, int c0,
                                           int gd0, int gh0, int gw0) {
   constexpr int PITCH = CC + 8;
@@ -80,8 +82,8 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
   const int64_t vol = (int64_t)p.D * p.H * p.W;
   const int64_t bvox = (int64_t)b * vol;
   if constexpr (VEC) {
-    constexpr int G = CC / 8;          // 16-byte channel groups per voxel (divides 256)
-    constexpr int VPI = 256 / G;       // voxels per pass of the workgroup
+    constexpr int G = CC / 8;          // 16-byte channel groups per voxel (divides NT)
+    constexpr int VPI = NT / G;        // voxels per pass of the workgroup
     constexpr int NB = 12;
     const int cg = threadIdx.x % G;
     const int c = c0 + cg * 8;
@@ -136,7 +138,7 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
       }
     }
   } else {
-    for (int idx = threadIdx.x; idx < hvox * CC; idx += blockDim.x) {
+    for (int idx = threadIdx.x; idx < hvox * CC; idx += NT) {
       const int vox = idx / CC, cc = idx - vox * CC;
       const int t = fdiv(vox, p.rHW);
       const int hw = vox - t * p.HW;
@@ -169,21 +171,69 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC>
-__global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
+// Weight ring: WRING slots, loads issued WPF = WRING - 1 stages ahead.
+constexpr int WRING = 4;
+constexpr int WPF = WRING - 1;
+
+// Byte offset of an LDS pointer within the workgroup's LDS (the low 32 bits of its
+// flat address).
+__device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned)(uintptr_t)p; }
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4). Issued as asm so that the compiler's wait insertion,
+// which cannot tell these writes from the halo, does not drain all of them before
+// every LDS read; completion is awaited explicitly with vmcnt_wait + a barrier.
+__device__ __forceinline__ void dma_b128(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory");
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding.
+// (s_waitcnt immediate for gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt
+// 11:8 left at their no-wait maxima.)
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// KSPL K-groups of 4 waves each: group g takes k-steps [g * KS / KSPL, (g + 1) * KS /
+// KSPL) of every tap (its own weight ring, the shared halo), so KSPL = 2 puts two waves
+// on every SIMD for the same output tile; the groups' partial sums meet in LDS at the
+// end (fixed order: group 0 + group 1).
+// Scheduling hint: spread NR LDS reads between NM MFMAs (one MFMA, then its share of
+// the reads) so the next tap's operands stream in while the current tap's MFMAs run.
+template <int NR, int NM, int I = 0>
+__device__ __forceinline__ void interleave_reads_mfma() {
+  if constexpr (I < NM) {
+    constexpr int per = (NR + NM - 1) / NM;
+    constexpr int left = NR - I * per;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+    if constexpr (left > 0) __builtin_amdgcn_sched_group_barrier(0x100, left < per ? left : per, 0);
+    interleave_reads_mfma<NR, NM, I + 1>();
+  }
+}
+
+template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, int KSPL>
+__global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
+  constexpr int NT = 256 * KSPL;
   constexpr int BO = WO * FO * 32;
   constexpr int PITCH = CC + 8;
   constexpr int KS = CC / 16;                 // MFMA k-steps per tap and chunk
+  constexpr int KSG = KS / KSPL;              // k-steps per tap of one K-group
+  static_assert(KSG * KSPL == KS && KSG >= 1, "K-groups must split the chunk's k-steps");
   constexpr int TAPS = KSZ * KSZ * KSZ;
-  constexpr int NFRAG = (BO / 32) * KS;       // 1 KB weight fragments per tap stage
-  constexpr int WSTAGE = NFRAG * 512;         // halves per stage
-  constexpr int WL = (NFRAG * 64 + 255) / 256;  // 16-byte loads per thread per stage
+  constexpr int NFRAG = (BO / 32) * KSG;      // 1 KB weight fragments per group stage
+  constexpr int WSTAGE = NFRAG * 512;         // halves per group stage
+  constexpr int LW = (NFRAG + 3) / 4;         // weight DMAs per wave per stage
   extern __shared__ __attribute__((aligned(16))) f16 smem[];
-  f16* wring = smem;                          // 2 stages of weights
-  f16* halo = smem + 2 * WSTAGE;
+  f16* halo = smem + KSPL * WRING * WSTAGE;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wo = wave / WV, wv = wave - wo * WV;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = wave >> 2, w4 = wave & 3;
+  const int wo = w4 / WV, wv = w4 - wo * WV;
+  f16* wring = smem + kg * WRING * WSTAGE;    // this K-group's weight ring
   const int sidx = blockIdx.z % p.split;
   const int z = blockIdx.z / p.split;
   const int b = p.upsample ? z >> 3 : z;
@@ -195,45 +245,49 @@ __global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
   const int d0 = bd_i * p.TD, h0 = bh_i * p.TH, w0 = bw_i * p.TW;
   const int s = p.stride;
   const int gd0 = d0 * s + p.ID0, gh0 = h0 * s + p.IH0, gw0 = w0 * s + p.IW0;
-  const int kq = 8 * (lane >> 5);
+  const int kq = 8 * (lane >> 5) + kg * KSG * 16;
 
   // Per-lane B-operand (voxel) bases in the halo.
   int lbase[FV];
-  int rv[FV][3];
-  bool valid[FV];
 #pragma unroll
   for (int fv = 0; fv < FV; fv++) {
     const int vloc = (wv * FV + fv) * 32 + (lane & 31);
     const int vw = vloc % p.TW, vt = vloc / p.TW, vh = vt % p.TH, vd = vt / p.TH;
-    rv[fv][0] = d0 + vd; rv[fv][1] = h0 + vh; rv[fv][2] = w0 + vw;
-    valid[fv] = rv[fv][0] < p.RD && rv[fv][1] < p.RH && rv[fv][2] < p.RW;
     const int hd = vd * s + pd, hh = vh * s + ph, hw = vw * s + pw;
     lbase[fv] = (hd * p.HH + hh) * p.RS + hw * PITCH + kq;
   }
   const int sd = p.HH * p.RS, sh = p.RS;
 
-  // Weight staging: thread t loads 16 bytes of fragment f = t/64 (+ 4 per extra load) of
-  // the stage -- (ob, kc) = (f / KS, f % KS) -- contiguous 1 KB per wave-wide load.
+  // Weight staging: stage st = (channel chunk, tap) of this workgroup's sequence goes to
+  // ring slot st % WRING of each K-group by direct global->LDS loads, WPF stages ahead of
+  // its use. Wave w4 of group g moves the group's fragments f = w4 + 4 i ((ob, k) =
+  // (f / KSG, f % KSG)): one 1 KB fragment is one 16-byte-per-lane load, already in MFMA
+  // lane order. A wave with fewer real fragments repeats one (same data to the same
+  // place), so every wave issues LW loads per stage and the vmcnt wait is uniform.
   const int ob0 = blockIdx.y * (BO / 32);
-  const f16* wsrc[WL];
-  bool wok[WL];
+  const int c_begin = sidx * p.cps * CC;
+  const int c_end = min(p.C, (sidx + 1) * p.cps * CC);
+  const int nst = (c_end - c_begin + CC - 1) / CC * TAPS;
+  const unsigned ring_lds = lds_offset(wring);
+  // This wave's fragment sources at (tap 0, chunk 0); a stage adds (tap * NKC + kc0) * 512.
+  const f16* wsrc[LW];
 #pragma unroll
-  for (int i = 0; i < WL; i++) {
-    const int e = tid + i * 256;
-    wok[i] = e < NFRAG * 64;
-    const int f = wok[i] ? e / 64 : 0, l = e % 64;
-    const int ob = ob0 + f / KS, kc = f % KS;
-    wsrc[i] = p.w + (((int64_t)parity * p.NOB + ob) * TAPS * p.NKC + kc) * 512 + l * 8;
+  for (int i = 0; i < LW; i++) {
+    const int f = (w4 + 4 * i) % NFRAG;
+    wsrc[i] = p.w + (((int64_t)parity * p.NOB + ob0 + f / KSG) * TAPS * p.NKC + kg * KSG + f % KSG) * 512 +
+              lane * 8;
   }
-  auto wload = [&](f16x8 (&r)[WL], int tap, int kc0) {
+  // Next stage to load: (ntap, nkc); it stops advancing at the last stage.
+  int ntap = 0, nkc = c_begin / 16, nleft = nst - 1;
+  auto issue_stage = [&](int slot) {
+    const int64_t off = ((int64_t)ntap * p.NKC + nkc) * 512;
 #pragma unroll
-    for (int i = 0; i < WL; i++)
-      if (wok[i]) r[i] = *reinterpret_cast<const f16x8*>(wsrc[i] + ((int64_t)tap * p.NKC + kc0) * 512);
-  };
-  auto wstore = [&](const f16x8 (&r)[WL], int slot) {
-#pragma unroll
-    for (int i = 0; i < WL; i++)
-      if (wok[i]) *reinterpret_cast<f16x8*>(wring + slot * WSTAGE + (tid + i * 256) * 8) = r[i];
+    for (int i = 0; i < LW; i++)
+      dma_b128(wsrc[i] + off, ring_lds + (unsigned)((slot * NFRAG + (w4 + 4 * i) % NFRAG) * 1024));
+    if (nleft > 0) {
+      nleft--;
+      if (++ntap == TAPS) { ntap = 0; nkc += KS; }
+    }
   };
 
   f32x16 acc[FO][FV];
@@ -244,100 +298,178 @@ __global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  const int c_end = min(p.C, (sidx + 1) * p.cps * CC);
-  for (int c0 = sidx * p.cps * CC; c0 < c_end; c0 += CC) {
-    const int kc0 = c0 / 16;
-    f16x8 r1[WL], r2[WL];
-    wload(r1, 0, kc0);
-    __syncthreads();  // previous chunk done with the LDS
-    wstore(r1, 0);
-    if (TAPS > 1) wload(r1, 1, kc0);
-    load_halo<CC, VEC>(p, halo, b, c0, gd0, gh0, gw0);
+  // Prologue: the first WPF stages (the last stage repeats past the end: repeats land in
+  // slots no stage uses before they are rewritten).
+#pragma unroll
+  for (int st = 0; st < WPF; st++) issue_stage(st);
+
+  // Operand fragments double-buffered in registers: while the MFMAs of tap t run, the
+  // A (weight ring) and B (halo) fragments of tap t + 1 are read from LDS.
+  f16x8 ra[2][FO][KSG], rb[2][FV][KSG];
+  auto load_frags = [&](int set, int stage, int tap) {
+    const int kd = tap / (KSZ * KSZ), kh = (tap / KSZ) % KSZ, kw = tap % KSZ;
+    const int toff = kd * sd + kh * sh + kw * PITCH;
+    const f16* wst = wring + (stage % WRING) * WSTAGE + lane * 8;
+#pragma unroll
+    for (int kk = 0; kk < KSG; kk++) {
+#pragma unroll
+      for (int fo = 0; fo < FO; fo++)
+        ra[set][fo][kk] = *reinterpret_cast<const f16x8*>(wst + ((wo * FO + fo) * KSG + kk) * 512);
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+        rb[set][fv][kk] = *reinterpret_cast<const f16x8*>(halo + lbase[fv] + toff + kk * 16);
+    }
+  };
+  auto mfma_frags = [&](int set) {
+#pragma unroll
+    for (int kk = 0; kk < KSG; kk++)
+#pragma unroll
+      for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+        for (int fv = 0; fv < FV; fv++) acc[fo][fv] = mfma32(ra[set][fo][kk], rb[set][fv][kk], acc[fo][fv]);
+  };
+
+  int st = 0;
+  for (int c0 = c_begin; c0 < c_end; c0 += CC) {
+    __syncthreads();  // previous chunk done with the halo
+    load_halo<CC, VEC, NT>(p, halo, b, c0, gd0, gh0, gw0);
+    // Every halo load -- and with them the weight stages issued so far -- has landed;
+    // saying so also clears the compiler's view of pending loads, which would otherwise
+    // drain the weight prefetch at every tap.
+    vmcnt_wait<0>();
     __syncthreads();
-    for (int tap = 0; tap < TAPS; tap++) {
-      if (tap + 2 < TAPS) wload(r2, tap + 2, kc0);
-      const int kd = tap / (KSZ * KSZ), kh = (tap / KSZ) % KSZ, kw = tap % KSZ;
-      const int toff = kd * sd + kh * sh + kw * PITCH;
-      const f16* wst = wring + (tap & 1) * WSTAGE + lane * 8;
+    load_frags(0, st, 0);
 #pragma unroll
-      for (int ks = 0; ks < KS; ks++) {
-        f16x8 a[FO], bf[FV];
-#pragma unroll
-        for (int fo = 0; fo < FO; fo++)
-          a[fo] = *reinterpret_cast<const f16x8*>(wst + ((wo * FO + fo) * KS + ks) * 512);
-#pragma unroll
-        for (int fv = 0; fv < FV; fv++)
-          bf[fv] = *reinterpret_cast<const f16x8*>(halo + lbase[fv] + toff + ks * 16);
-#pragma unroll
-        for (int fo = 0; fo < FO; fo++)
-#pragma unroll
-          for (int fv = 0; fv < FV; fv++) acc[fo][fv] = mfma32(a[fo], bf[fv], acc[fo][fv]);
-      }
-      if (tap + 1 < TAPS) wstore(r1, (tap + 1) & 1);
+    for (int tap = 0; tap < TAPS; tap++, st++) {
+      // Stage st + 1 has landed once only stage st + 2's loads may be pending; the
+      // barrier publishes every wave's part of it and retires stage st - 1 (read into
+      // registers two taps ago), whose slot the next load reuses.
+      vmcnt_wait<LW>();
       __syncthreads();
-#pragma unroll
-      for (int i = 0; i < WL; i++) r1[i] = r2[i];
+      issue_stage((st + WPF) % WRING);
+      if (tap + 1 < TAPS) load_frags((tap + 1) & 1, st + 1, tap + 1);
+      mfma_frags(tap & 1);
+      if (tap + 1 < TAPS) interleave_reads_mfma<(FO + FV) * KSG, FO * FV * KSG>();
     }
   }
+  // Drain the trailing (repeated) weight loads before the LDS is reused.
+  vmcnt_wait<0>();
+  __syncthreads();  // every wave is done with the halo and the weight rings
 
-  // Epilogue: lane holds voxel lane%32 of each column block and, per group j of four
-  // accumulator elements, output channels (ob)*32 + j*8 + 4*(lane/32) + r.
+  constexpr int EPW = FO * 32 + 4;   // epilogue staging pitch (floats)
+  constexpr int RED = 4 * FO * FV * 1024;  // floats of the K-group reduction buffer
+  if constexpr (KSPL == 2) {
+    // Group 1 hands its partial sums to group 0 (same wave slot, lane-major layout).
+    float* red = reinterpret_cast<float*>(smem) + w4 * (FO * FV * 1024);
+    if (kg == 1) {
+#pragma unroll
+      for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+        for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; e4++) {
+            const f32x4 q = {acc[fo][fv][e4 * 4], acc[fo][fv][e4 * 4 + 1], acc[fo][fv][e4 * 4 + 2],
+                             acc[fo][fv][e4 * 4 + 3]};
+            *reinterpret_cast<f32x4*>(red + ((fo * FV + fv) * 4 + e4) * 256 + lane * 4) = q;
+          }
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+          const f32x4 q = *reinterpret_cast<const f32x4*>(red + ((fo * FV + fv) * 4 + e4) * 256 + lane * 4);
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[fo][fv][e4 * 4 + r] += q[r];
+        }
+  }
+
+  // Epilogue through LDS: each wave stages one 32-voxel column block at a time (its
+  // FO * 32 channels in fp32, voxel-major), then each lane finishes 8 channels of one
+  // voxel -- bias, shift, scale, residual, one rounding, activation -- and writes them
+  // as one 16-byte store, the lanes of a voxel covering its channels contiguously.
+  constexpr int G8 = FO * 4;         // 8-channel groups per voxel
+  float* stg = reinterpret_cast<float*>(smem) + (KSPL == 2 ? RED : 0) + w4 * 32 * EPW;
+  const int col = lane & 31, hf = lane >> 5;
+  const int obase = (ob0 + wo * FO) * 32;
   const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
   const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
   const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
 #pragma unroll
   for (int fv = 0; fv < FV; fv++) {
-    if (!valid[fv]) continue;
-    int64_t ov;
-    if (p.upsample)
-      ov = ((int64_t)(2 * rv[fv][0] + pd) * p.OH + (2 * rv[fv][1] + ph)) * p.OW + 2 * rv[fv][2] + pw;
-    else
-      ov = ((int64_t)rv[fv][0] * p.OH + rv[fv][1]) * p.OW + rv[fv][2];
-    ov += (int64_t)b * ovol;
-    f16* yrow = p.y + ov * p.yp;
-    const f16* rrow = p.res ? p.res + ov * p.resp : nullptr;
-    if (p.split > 1) {
-      // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
-      float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov) * p.O;
+    // Lane (hf, col) holds voxel col, channels fo * 32 + j * 8 + 4 * hf + r.
 #pragma unroll
-      for (int fo = 0; fo < FO; fo++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int o4 = (ob0 + wo * FO + fo) * 32 + j * 8 + 4 * (lane >> 5);
-#pragma unroll
-          for (int r = 0; r < 4; r++)
-            if (o4 + r < p.O) prow[o4 + r] = acc[fo][fv][j * 4 + r];
-        }
-      continue;
-    }
-#pragma unroll
-    for (int fo = 0; fo < FO; fo++) {
+    for (int fo = 0; fo < FO; fo++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const int o4 = (ob0 + wo * FO + fo) * 32 + j * 8 + 4 * (lane >> 5);
-        if (o4 >= p.O) continue;
-        f16x4 outv;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int o = o4 + r;
-          float v = acc[fo][fv][j * 4 + r];
-          if (o < p.O) {
-            if (bias) v += bias[o];
-            if (shb) v += (float)shb[o];
-            v *= p.scale;
-            if (rrow) v += (float)rrow[o];
-          }
-          outv[r] = post_act((f16)v, p.act);
-        }
-        if (p.yvec && o4 + 4 <= p.O) {
-          *reinterpret_cast<f16x4*>(yrow + o4) = outv;
+        const f32x4 q = {acc[fo][fv][j * 4], acc[fo][fv][j * 4 + 1], acc[fo][fv][j * 4 + 2], acc[fo][fv][j * 4 + 3]};
+        *reinterpret_cast<f32x4*>(stg + col * EPW + fo * 32 + j * 8 + 4 * hf) = q;
+      }
+    __builtin_amdgcn_wave_barrier();  // (LDS operations of a wave complete in order)
+    for (int idx = lane; idx < 32 * G8; idx += 64) {
+      const int v = idx / G8, g = idx - v * G8;
+      const int o = obase + g * 8;
+      const int vloc = (wv * FV + fv) * 32 + v;
+      const int vt = fdiv(vloc, p.rTW), vw = vloc - vt * p.TW;
+      const int vd = fdiv(vt, p.rTH), vh = vt - vd * p.TH;
+      const int rd = d0 + vd, rh = h0 + vh, rw = w0 + vw;
+      if (o >= p.O || vd >= p.TD || rd >= p.RD || rh >= p.RH || rw >= p.RW) continue;
+      int64_t ov;
+      if (p.upsample)
+        ov = ((int64_t)(2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
+      else
+        ov = ((int64_t)rd * p.OH + rh) * p.OW + rw;
+      ov += (int64_t)b * ovol;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
+      float r8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const int n = min(8, p.O - o);
+      if (p.split > 1) {
+        // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
+        float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov) * p.O + o;
+        if (n == 8 && p.ep_vec) {
+          *reinterpret_cast<f32x4*>(prow) = lo;
+          *reinterpret_cast<f32x4*>(prow + 4) = hi;
         } else {
+          for (int r = 0; r < n; r++) prow[r] = r8[r];
+        }
+        continue;
+      }
+      f16* yrow = p.y + ov * p.yp + o;
+      const f16* rrow = p.res ? p.res + ov * p.resp + o : nullptr;
+      if (n == 8 && p.ep_vec) {
+        f16x8 sh8 = {0, 0, 0, 0, 0, 0, 0, 0}, re8 = {0, 0, 0, 0, 0, 0, 0, 0};
+        if (shb) sh8 = *reinterpret_cast<const f16x8*>(shb + o);
+        if (rrow) re8 = *reinterpret_cast<const f16x8*>(rrow);
+        f32x4 b0 = {0.f, 0.f, 0.f, 0.f}, b1 = {0.f, 0.f, 0.f, 0.f};
+        if (bias) {
+          b0 = *reinterpret_cast<const f32x4*>(bias + o);
+          b1 = *reinterpret_cast<const f32x4*>(bias + o + 4);
+        }
+        f16x8 out;
 #pragma unroll
-          for (int r = 0; r < 4; r++)
-            if (o4 + r < p.O) yrow[o4 + r] = outv[r];
+        for (int r = 0; r < 8; r++) {
+          float t = r8[r] + (r < 4 ? b0[r] : b1[r - 4]);
+          t += (float)sh8[r];
+          t = t * p.scale + (float)re8[r];
+          out[r] = post_act((f16)t, p.act);
+        }
+        *reinterpret_cast<f16x8*>(yrow) = out;
+      } else {
+        for (int r = 0; r < n; r++) {
+          float t = r8[r];
+          if (bias) t += bias[o + r];
+          if (shb) t += (float)shb[o + r];
+          t *= p.scale;
+          if (rrow) t += (float)rrow[r];
+          yrow[r] = post_act((f16)t, p.act);
         }
       }
     }
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
@@ -365,9 +497,16 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
 
 struct Tile {
   int WO, WV, FO, FV, CC;
+  int KSPL = 1;  // K-groups of 4 waves
   int BO() const { return WO * FO * 32; }
   int BV() const { return WV * FV * 32; }
 };
+
+// Tiles instantiated with two K-groups (the dispatch list in ldx_conv3d).
+static bool kspl2_tile(const Tile& t) {
+  return (t.WO == 1 && t.WV == 4 && ((t.FO == 2 && (t.FV == 2 || t.FV == 1)) || (t.FO == 1 && t.FV == 2))) ||
+         (t.WO == 2 && t.WV == 2 && ((t.FO == 2 && t.FV == 2) || (t.FO == 1 && t.FV == 1)));
+}
 
 static void pick_brick(const ConvParams& p, int BV, int s, int ks, int& TD, int& TH, int& TW) {
   // Minimise launched voxel slots (partial-brick waste), then the halo volume.
@@ -388,33 +527,41 @@ static void pick_brick(const ConvParams& p, int BV, int s, int ks, int& TD, int&
     }
 }
 
-template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC>
+template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, int KSPL>
 static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t lds) {
   constexpr int BO = WO * FO * 32;
-  lds += (size_t)2 * (BO / 32) * (CC / 16) * 512 * sizeof(f16);  // weight double buffer
+  lds += (size_t)WRING * (BO / 32) * (CC / 16) * 512 * sizeof(f16);  // weight rings (all groups)
+  // End phase: K-group partial sums, then the epilogue staging.
+  const size_t tail = (size_t)(KSPL == 2 ? 4 * FO * FV * 1024 : 0) * sizeof(float) +
+                      (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
+  if (lds < tail) lds = tail;
+  if (lds > 160 * 1024) return fail("conv3d: %zu bytes of LDS needed", lds);
   dim3 grid((unsigned)(p.NBD * p.NBH * p.NBW), (unsigned)((p.O + BO - 1) / BO), (unsigned)grid_z);
-  auto kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, VEC>;
+  auto kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, VEC, KSPL>;
   if (lds > 65536) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
       return check_launch("conv3d: set LDS size");
   }
-  hipLaunchKernelGGL(kern, grid, dim3(256), lds, stream, p);
+  hipLaunchKernelGGL(kern, grid, dim3(256 * KSPL), lds, stream, p);
   return check_launch("conv3d");
 }
 
-template <int WO, int WV, int FO, int FV, int KSZ>
+template <int WO, int WV, int FO, int FV, int KSZ, int KSPL>
 static int dispatch_cc(ConvParams& p, int cc, bool vec, int grid_z, hipStream_t stream, size_t lds) {
-  if (!vec) return launch<WO, WV, FO, FV, 32, KSZ, false>(p, grid_z, stream, lds);
-  if (cc == 64) return launch<WO, WV, FO, FV, 64, KSZ, true>(p, grid_z, stream, lds);
-  return launch<WO, WV, FO, FV, 32, KSZ, true>(p, grid_z, stream, lds);
+  if (!vec) {
+    if constexpr (KSPL == 1) return launch<WO, WV, FO, FV, 32, KSZ, false, 1>(p, grid_z, stream, lds);
+    return fail("conv3d: K-groups need 16-byte channel groups");
+  }
+  if (cc == 64) return launch<WO, WV, FO, FV, 64, KSZ, true, KSPL>(p, grid_z, stream, lds);
+  return launch<WO, WV, FO, FV, 32, KSZ, true, KSPL>(p, grid_z, stream, lds);
 }
 
-template <int WO, int WV, int FO, int FV>
+template <int WO, int WV, int FO, int FV, int KSPL>
 static int dispatch_k(ConvParams& p, int cc, bool vec, int grid_z, hipStream_t stream, size_t lds) {
-  if (p.taps == 27) return dispatch_cc<WO, WV, FO, FV, 3>(p, cc, vec, grid_z, stream, lds);
-  if (p.taps == 8) return dispatch_cc<WO, WV, FO, FV, 2>(p, cc, vec, grid_z, stream, lds);
-  return dispatch_cc<WO, WV, FO, FV, 1>(p, cc, vec, grid_z, stream, lds);
+  if (p.taps == 27) return dispatch_cc<WO, WV, FO, FV, 3, KSPL>(p, cc, vec, grid_z, stream, lds);
+  if (p.taps == 8) return dispatch_cc<WO, WV, FO, FV, 2, KSPL>(p, cc, vec, grid_z, stream, lds);
+  return dispatch_cc<WO, WV, FO, FV, 1, KSPL>(p, cc, vec, grid_z, stream, lds);
 }
 
 }  // namespace ldx
@@ -468,6 +615,11 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   p.scale = a->output_scale; p.act = a->act;
   p.y = (f16*)a->y; p.yp = a->y_pitch;
   p.yvec = (p.yp % 4 == 0) && ((uintptr_t)a->y % 8 == 0);
+  p.ep_vec = p.yp % 8 == 0 && (uintptr_t)a->y % 16 == 0 &&
+             (!a->residual || (p.resp % 8 == 0 && (uintptr_t)a->residual % 16 == 0)) &&
+             (!a->shift || (p.shiftp % 8 == 0 && (uintptr_t)a->shift % 16 == 0)) &&
+             (!a->bias || ((uintptr_t)a->bias % 16 == 0 && (!a->bias_batched || p.O % 4 == 0))) &&
+             p.O % 4 == 0 && (!a->workspace || (uintptr_t)a->workspace % 16 == 0);
 
   vec = (p.C0 % 8 == 0) && (p.x0p % 8 == 0) && (p.C1 == 0 || (p.C1 % 8 == 0 && p.x1p % 8 == 0)) &&
         ((uintptr_t)a->x0 % 16 == 0) && (p.C1 == 0 || (uintptr_t)a->x1 % 16 == 0);
@@ -484,8 +636,10 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   bool forced = false;
   if (const char* env = getenv("LDX_CONV_TILE")) {
     Tile o{};
-    if (sscanf(env, "%d,%d,%d,%d,%d", &o.WO, &o.WV, &o.FO, &o.FV, &o.CC) == 5 && o.WO * o.WV == 4 &&
-        (o.CC == 32 || (o.CC == 64 && p.C % 64 == 0 && vec))) {
+    const int got = sscanf(env, "%d,%d,%d,%d,%d,%d", &o.WO, &o.WV, &o.FO, &o.FV, &o.CC, &o.KSPL);
+    if (got == 5) o.KSPL = 1;
+    if (got >= 5 && o.WO * o.WV == 4 && (o.CC == 32 || (o.CC == 64 && p.C % 64 == 0 && vec)) &&
+        (o.KSPL == 1 || (o.KSPL == 2 && vec))) {
       t = o;
       forced = true;
     }
@@ -512,16 +666,18 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
       p.RS = (base_units + pad_units) * 8;
     }
     lds = (size_t)p.HD * p.HH * p.RS * sizeof(f16);
-    const size_t wbytes = (size_t)2 * (t.BO() / 32) * (t.CC / 16) * 1024;
+    const size_t wbytes = (size_t)WRING * (t.BO() / 32) * (t.CC / 16) * 1024;
     if (lds + wbytes <= (forced ? 160u * 1024 : 80u * 1024) || (t.CC == 32 && t.FV == 1)) break;
     if (t.CC == 64) t.CC = 32;
     else t.FV = 1;
+    if (!kspl2_tile(t)) t.KSPL = 1;
   }
-  if (lds + (size_t)2 * (t.BO() / 32) * (t.CC / 16) * 1024 > 160 * 1024)
+  if (lds + (size_t)WRING * (t.BO() / 32) * (t.CC / 16) * 1024 > 160 * 1024)
     return fail("conv3d: halo of %zu bytes exceeds LDS", lds);
   p.NBD = (p.RD + TD - 1) / TD; p.NBH = (p.RH + TH - 1) / TH; p.NBW = (p.RW + TW - 1) / TW;
   p.ID0 = ks == 1 ? 0 : -1; p.IH0 = p.ID0; p.IW0 = p.ID0;
   p.rHW = 1.0f / (float)p.HW; p.rHH = 1.0f / (float)p.HH;
+  p.rTW = 1.0f / (float)TW; p.rTH = 1.0f / (float)TH;
   p.NOB = (p.O + 127) / 128 * 4; p.NKC = (p.C + 63) / 64 * 4;
   if ((int64_t)p.HD * p.HH * p.HW >= (1 << 20)) return fail("conv3d: halo too large");
   const int64_t bricks = (int64_t)p.NBD * p.NBH * p.NBW;
@@ -572,16 +728,23 @@ extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
   const int grid_z = p.B * (p.upsample ? 8 : 1) * p.split;
   hipStream_t st = as_stream(stream);
 
-#define LDX_TILE(WO_, WV_, FO_, FV_) \
-  if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_) rc = dispatch_k<WO_, WV_, FO_, FV_>(p, t.CC, vec, grid_z, st, lds); else
-  LDX_TILE(1, 4, 1, 2)
-  LDX_TILE(1, 4, 1, 1)
-  LDX_TILE(1, 4, 2, 2)
-  LDX_TILE(1, 4, 2, 1)
-  LDX_TILE(2, 2, 2, 2)
-  LDX_TILE(2, 2, 1, 2)
-  LDX_TILE(2, 2, 2, 1)
-  LDX_TILE(2, 2, 1, 1)
+#define LDX_TILE(WO_, WV_, FO_, FV_, KSPL_)                                             \
+  if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_ && t.KSPL == KSPL_) \
+    rc = dispatch_k<WO_, WV_, FO_, FV_, KSPL_>(p, t.CC, vec, grid_z, st, lds);     \
+  else
+  LDX_TILE(1, 4, 1, 2, 1)
+  LDX_TILE(1, 4, 1, 1, 1)
+  LDX_TILE(1, 4, 2, 2, 1)
+  LDX_TILE(1, 4, 2, 1, 1)
+  LDX_TILE(2, 2, 2, 2, 1)
+  LDX_TILE(2, 2, 1, 2, 1)
+  LDX_TILE(2, 2, 2, 1, 1)
+  LDX_TILE(2, 2, 1, 1, 1)
+  LDX_TILE(1, 4, 2, 2, 2)
+  LDX_TILE(1, 4, 2, 1, 2)
+  LDX_TILE(1, 4, 1, 2, 2)
+  LDX_TILE(2, 2, 2, 2, 2)
+  LDX_TILE(2, 2, 1, 1, 2)
   return fail("conv3d: no kernel for tile");
 #undef LDX_TILE
   if (rc != LDX_OK || p.split == 1) return rc;
