@@ -24,6 +24,7 @@
 #include "common.h"
 
 #include <cstdlib>
+#include <type_traits>
 
 namespace ldx {
 
@@ -66,10 +67,26 @@ __device__ __forceinline__ f16 post_act(f16 h, int act) {
   if (act == LDX_ACT_SILU) return (f16)silu_f((float)h);
   return h;
 }
+template <int ACT>
+__device__ __forceinline__ f16 post_act_t(f16 h) {
+  if constexpr (ACT == LDX_ACT_GELU) return (f16)gelu_erf((float)h);
+  else if constexpr (ACT == LDX_ACT_SILU) return (f16)silu_f((float)h);
+  else return h;
+}
 
 // q = t / d for 0 <= t < 2^21 and small d, from a host-rounded reciprocal: (t + 0.5) / d
 // lies at least 0.5 / d from an integer, far beyond the float error of the product.
 __device__ __forceinline__ int fdiv(int t, float rcp) { return (int)(((float)t + 0.5f) * rcp); }
+
+// Raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor word 3): loads at
+// offsets past the extent return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
 
 // Stage the halo of one brick for channels [c0, c0 + CC) into LDS, applying the
 // affine + SiLU prologue and zero padding. Global loads are issued NB at a time before
@@ -88,9 +105,6 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
     const int cg = threadIdx.x % G;
     const int c = c0 + cg * 8;
     const bool cval = c < p.C;
-    const bool from0 = c < p.C0;
-    const f16* src_base = from0 ? p.x0 + c : p.x1 + (c - p.C0);
-    const int64_t pitch = from0 ? p.x0p : p.x1p;
     float sc[8], of[8];
     const bool aff = p.affine != nullptr;
     if (aff && cval) {
@@ -101,7 +115,17 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
 #pragma unroll
       for (int e = 0; e < 8; e++) { sc[e] = 1.f; of[e] = 0.f; }
     }
+    const bool xf = aff || p.silu;
     const int silu = p.silu;
+    // Source of this chunk: all of it in x0, or all in x1 (the host sends chunks that
+    // straddle the split, or a batch item past 2 GiB, down the generic path). Reads go
+    // through a buffer resource over the batch item, so padding voxels and channels
+    // past C read as zero without a branch.
+    const bool in0 = c0 < p.C0;
+    const f16* base = in0 ? p.x0 + bvox * p.x0p : p.x1 + bvox * p.x1p;
+    const int64_t pitch = in0 ? p.x0p : p.x1p;
+    const auto rs = make_rsrc(base, (unsigned)(vol * pitch * 2));
+    const unsigned cofs = (unsigned)((in0 ? c : c - p.C0) * 2);
     for (int v0 = threadIdx.x / G; v0 < hvox; v0 += VPI * NB) {
       f16x8 val[NB];
       bool ok[NB];
@@ -114,23 +138,21 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
         const int hh = t - hd * p.HH;
         const int id = gd0 + hd, ih = gh0 + hh, iw = gw0 + hw;
         ok[j] = vox < hvox && cval && id >= 0 && id < p.D && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
-        val[j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-        if (ok[j]) {
-          const int64_t vi = bvox + ((int64_t)id * p.H + ih) * p.W + iw;
-          val[j] = *reinterpret_cast<const f16x8*>(src_base + vi * pitch);
-        }
+        const unsigned off = ok[j] ? (unsigned)(((id * p.H + ih) * p.W + iw) * (unsigned)pitch * 2u) + cofs
+                                   : 0xfffffff0u;
+        val[j] = buffer_load16(rs, off);
       }
 #pragma unroll
       for (int j = 0; j < NB; j++) {
         const int vox = v0 + j * VPI;
         if (vox >= hvox) break;
         f16x8 v = val[j];
-        if (ok[j] && (aff || silu)) {
+        if (xf) {
 #pragma unroll
           for (int e = 0; e < 8; e++) {
             float yv = (float)v[e] * sc[e] + of[e];
             if (silu) yv = silu_f(yv);
-            v[e] = (f16)yv;
+            v[e] = ok[j] ? (f16)yv : (f16)0;
           }
         }
         const int t2 = fdiv(vox, p.rHW);
@@ -234,13 +256,24 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   const int kg = wave >> 2, w4 = wave & 3;
   const int wo = w4 / WV, wv = w4 - wo * WV;
   f16* wring = smem + kg * WRING * WSTAGE;    // this K-group's weight ring
-  const int sidx = blockIdx.z % p.split;
-  const int z = blockIdx.z / p.split;
+  // Workgroup -> (output block, brick, z) with the output blocks of a brick adjacent and
+  // the bricks each XCD receives (workgroups are dealt to the 8 XCDs round-robin)
+  // contiguous, so neighbouring halos meet in the same L2.
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+  }
+  const int nob = (p.O + BO - 1) / BO, nbr = p.NBD * p.NBH * p.NBW;
+  const int oblk = wg % nob;
+  const int brick = (wg / nob) % nbr;
+  const int zz = wg / nob / nbr;
+  const int sidx = zz % p.split;
+  const int z = zz / p.split;
   const int b = p.upsample ? z >> 3 : z;
   const int parity = p.upsample ? z & 7 : 0;
   const int pd = parity >> 2, ph = (parity >> 1) & 1, pw = parity & 1;
 
-  const int brick = blockIdx.x;
   const int bw_i = brick % p.NBW, bt = brick / p.NBW, bh_i = bt % p.NBH, bd_i = bt / p.NBH;
   const int d0 = bd_i * p.TD, h0 = bh_i * p.TH, w0 = bw_i * p.TW;
   const int s = p.stride;
@@ -264,7 +297,7 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   // (f / KSG, f % KSG)): one 1 KB fragment is one 16-byte-per-lane load, already in MFMA
   // lane order. A wave with fewer real fragments repeats one (same data to the same
   // place), so every wave issues LW loads per stage and the vmcnt wait is uniform.
-  const int ob0 = blockIdx.y * (BO / 32);
+  const int ob0 = oblk * (BO / 32);
   const int c_begin = sidx * p.cps * CC;
   const int c_end = min(p.C, (sidx + 1) * p.cps * CC);
   const int nst = (c_end - c_begin + CC - 1) / CC * TAPS;
@@ -388,16 +421,44 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   }
 
   // Epilogue through LDS: each wave stages one 32-voxel column block at a time (its
-  // FO * 32 channels in fp32, voxel-major), then each lane finishes 8 channels of one
-  // voxel -- bias, shift, scale, residual, one rounding, activation -- and writes them
-  // as one 16-byte store, the lanes of a voxel covering its channels contiguously.
-  constexpr int G8 = FO * 4;         // 8-channel groups per voxel
+  // FO * 32 channels in fp32, voxel-major), then each lane finishes 8 channels of
+  // 32 * G8 / 64 voxels -- bias, shift, scale, residual, one rounding, activation -- and
+  // writes each as one 16-byte store, the lanes of a voxel covering its channels
+  // contiguously. A lane's channel group is the same for every voxel it finishes, so
+  // its bias and shift are loaded once; the residual rows are all requested before the
+  // first is used.
+  constexpr int G8 = FO * 4;         // 8-channel groups per voxel (divides 64)
+  constexpr int NI = 32 * G8 / 64;   // voxels per lane per column block
   float* stg = reinterpret_cast<float*>(smem) + (KSPL == 2 ? RED : 0) + w4 * 32 * EPW;
   const int col = lane & 31, hf = lane >> 5;
-  const int obase = (ob0 + wo * FO) * 32;
+  const int g = lane % G8;
+  const int o = (ob0 + wo * FO) * 32 + g * 8;
+  const int nch = min(8, p.O - o);   // channels of this lane's group (<= 0: none)
+  const bool vec8 = nch == 8 && p.ep_vec;
   const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
   const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
   const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
+  float add8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // bias + shift
+  if (nch > 0) {
+    if (vec8) {
+      if (bias) {
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + o);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + o + 4);
+#pragma unroll
+        for (int r = 0; r < 4; r++) { add8[r] = b0[r]; add8[r + 4] = b1[r]; }
+      }
+      if (shb) {
+        const f16x8 s8 = *reinterpret_cast<const f16x8*>(shb + o);
+#pragma unroll
+        for (int r = 0; r < 8; r++) add8[r] += (float)s8[r];
+      }
+    } else {
+      for (int r = 0; r < nch; r++) add8[r] = (bias ? bias[o + r] : 0.f) + (shb ? (float)shb[o + r] : 0.f);
+    }
+  }
+  // One copy of the store loop per activation: no per-element branch on it.
+  auto finish = [&](auto act_c) {
+  constexpr int ACT = decltype(act_c)::value;
 #pragma unroll
   for (int fv = 0; fv < FV; fv++) {
     // Lane (hf, col) holds voxel col, channels fo * 32 + j * 8 + 4 * hf + r.
@@ -409,68 +470,64 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
         *reinterpret_cast<f32x4*>(stg + col * EPW + fo * 32 + j * 8 + 4 * hf) = q;
       }
     __builtin_amdgcn_wave_barrier();  // (LDS operations of a wave complete in order)
-    for (int idx = lane; idx < 32 * G8; idx += 64) {
-      const int v = idx / G8, g = idx - v * G8;
-      const int o = obase + g * 8;
+    int64_t ov[NI];
+    bool ok[NI];
+    f16x8 re8[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int v = lane / G8 + i * (64 / G8);
       const int vloc = (wv * FV + fv) * 32 + v;
       const int vt = fdiv(vloc, p.rTW), vw = vloc - vt * p.TW;
       const int vd = fdiv(vt, p.rTH), vh = vt - vd * p.TH;
       const int rd = d0 + vd, rh = h0 + vh, rw = w0 + vw;
-      if (o >= p.O || vd >= p.TD || rd >= p.RD || rh >= p.RH || rw >= p.RW) continue;
-      int64_t ov;
+      ok[i] = nch > 0 && vd < p.TD && rd < p.RD && rh < p.RH && rw < p.RW;
       if (p.upsample)
-        ov = ((int64_t)(2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
+        ov[i] = ((int64_t)(2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
       else
-        ov = ((int64_t)rd * p.OH + rh) * p.OW + rw;
-      ov += (int64_t)b * ovol;
+        ov[i] = ((int64_t)rd * p.OH + rh) * p.OW + rw;
+      ov[i] += (int64_t)b * ovol;
+      re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (ok[i] && p.res && vec8 && p.split == 1) re8[i] = *reinterpret_cast<const f16x8*>(p.res + ov[i] * p.resp + o);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      if (!ok[i]) continue;
+      const int v = lane / G8 + i * (64 / G8);
       const f32x4 lo = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
       const f32x4 hi = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
-      float r8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      const int n = min(8, p.O - o);
+      const float r8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       if (p.split > 1) {
         // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
-        float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov) * p.O + o;
-        if (n == 8 && p.ep_vec) {
+        float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov[i]) * p.O + o;
+        if (vec8) {
           *reinterpret_cast<f32x4*>(prow) = lo;
           *reinterpret_cast<f32x4*>(prow + 4) = hi;
         } else {
-          for (int r = 0; r < n; r++) prow[r] = r8[r];
+          for (int r = 0; r < nch; r++) prow[r] = r8[r];
         }
         continue;
       }
-      f16* yrow = p.y + ov * p.yp + o;
-      const f16* rrow = p.res ? p.res + ov * p.resp + o : nullptr;
-      if (n == 8 && p.ep_vec) {
-        f16x8 sh8 = {0, 0, 0, 0, 0, 0, 0, 0}, re8 = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (shb) sh8 = *reinterpret_cast<const f16x8*>(shb + o);
-        if (rrow) re8 = *reinterpret_cast<const f16x8*>(rrow);
-        f32x4 b0 = {0.f, 0.f, 0.f, 0.f}, b1 = {0.f, 0.f, 0.f, 0.f};
-        if (bias) {
-          b0 = *reinterpret_cast<const f32x4*>(bias + o);
-          b1 = *reinterpret_cast<const f32x4*>(bias + o + 4);
-        }
+      f16* yrow = p.y + ov[i] * p.yp + o;
+      if (vec8) {
         f16x8 out;
 #pragma unroll
-        for (int r = 0; r < 8; r++) {
-          float t = r8[r] + (r < 4 ? b0[r] : b1[r - 4]);
-          t += (float)sh8[r];
-          t = t * p.scale + (float)re8[r];
-          out[r] = post_act((f16)t, p.act);
-        }
+        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + add8[r]) * p.scale + (float)re8[i][r]));
         *reinterpret_cast<f16x8*>(yrow) = out;
       } else {
-        for (int r = 0; r < n; r++) {
-          float t = r8[r];
-          if (bias) t += bias[o + r];
-          if (shb) t += (float)shb[o + r];
-          t *= p.scale;
+        const f16* rrow = p.res ? p.res + ov[i] * p.resp + o : nullptr;
+        for (int r = 0; r < nch; r++) {
+          float t = (r8[r] + add8[r]) * p.scale;
           if (rrow) t += (float)rrow[r];
-          yrow[r] = post_act((f16)t, p.act);
+          yrow[r] = post_act_t<ACT>((f16)t);
         }
       }
     }
     __builtin_amdgcn_wave_barrier();
   }
+  };
+  if (p.act == LDX_ACT_GELU) finish(std::integral_constant<int, LDX_ACT_GELU>());
+  else if (p.act == LDX_ACT_SILU) finish(std::integral_constant<int, LDX_ACT_SILU>());
+  else finish(std::integral_constant<int, LDX_ACT_NONE>());
 }
 
 // Split-K finish: sum the fp32 partial planes in split order, then the same epilogue
@@ -485,9 +542,9 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
     for (int s2 = 0; s2 < p.split; s2++) v += p.part[(int64_t)s2 * n + i];
     const int64_t vol = nvox / p.B;
     const int b = (int)(ov / vol);
-    if (p.bias) v += p.bias[(p.bias_batched ? (int64_t)b * p.O : 0) + o];
-    if (p.shift) v += (float)p.shift[(int64_t)b * p.shiftp + o];
-    v *= p.scale;
+    float add = p.bias ? p.bias[(p.bias_batched ? (int64_t)b * p.O : 0) + o] : 0.f;
+    if (p.shift) add += (float)p.shift[(int64_t)b * p.shiftp + o];
+    v = (v + add) * p.scale;
     if (p.res) v += (float)p.res[ov * p.resp + o];
     p.y[ov * p.yp + o] = post_act((f16)v, p.act);
   }
@@ -536,7 +593,9 @@ static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t lds) {
                       (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
   if (lds < tail) lds = tail;
   if (lds > 160 * 1024) return fail("conv3d: %zu bytes of LDS needed", lds);
-  dim3 grid((unsigned)(p.NBD * p.NBH * p.NBW), (unsigned)((p.O + BO - 1) / BO), (unsigned)grid_z);
+  const int64_t nwg = (int64_t)p.NBD * p.NBH * p.NBW * ((p.O + BO - 1) / BO) * grid_z;
+  if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
+  dim3 grid((unsigned)nwg);
   auto kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, VEC, KSPL>;
   if (lds > 65536) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -621,8 +680,11 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
              (!a->bias || ((uintptr_t)a->bias % 16 == 0 && (!a->bias_batched || p.O % 4 == 0))) &&
              p.O % 4 == 0 && (!a->workspace || (uintptr_t)a->workspace % 16 == 0);
 
+  // 16-byte halo reads through a buffer resource per batch item (byte offsets < 2 GiB).
+  const int64_t in_vol = (int64_t)p.D * p.H * p.W;
   vec = (p.C0 % 8 == 0) && (p.x0p % 8 == 0) && (p.C1 == 0 || (p.C1 % 8 == 0 && p.x1p % 8 == 0)) &&
-        ((uintptr_t)a->x0 % 16 == 0) && (p.C1 == 0 || (uintptr_t)a->x1 % 16 == 0);
+        ((uintptr_t)a->x0 % 16 == 0) && (p.C1 == 0 || (uintptr_t)a->x1 % 16 == 0) &&
+        in_vol * p.x0p * 2 < ((int64_t)1 << 31) && (p.C1 == 0 || in_vol * p.x1p * 2 < ((int64_t)1 << 31));
 
   // Tiles: (waves over O) x (waves over voxels), 32x32 MFMA blocks per wave; chosen
   // from measured sweeps on MI355X: 64x64 wave tiles when the volume fills the GPU,
@@ -645,6 +707,12 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
     }
   }
 
+  // A channel chunk of the vectorised halo path comes from x0 or from x1, never both.
+  if (vec && p.C1 > 0 && p.C0 % t.CC != 0) {
+    if (p.C0 % 32 == 0) t.CC = 32;
+    else vec = false;
+  }
+  if (!vec) t.KSPL = 1;
   const int ks = a->ksize;
   const int s = p.stride;
   int TD = 1, TH = 1, TW = 1;
