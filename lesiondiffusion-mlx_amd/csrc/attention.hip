@@ -24,6 +24,9 @@
 
 #include "common.h"
 
+#include <cstdlib>
+#include <type_traits>
+
 namespace ldx {
 
 struct AttnParams {
@@ -50,8 +53,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, un
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 
-__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned soff = 0) {
+  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
 }
 
 // acc *= a with tied operands, so the branch that rescales leaves the accumulator in
@@ -113,13 +116,21 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const f16* __restrict_
 __device__ __forceinline__ int key_row(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
 
 // Waves per SIMD >= 2 keeps the register budget at 256 VGPRs, so the MFMA accumulators
-// live in ordinary VGPRs (no accumulator-register copies around the softmax).
-template <int D>
-struct AttnOcc { static constexpr int waves = D <= 64 ? 2 : 1; };
-
+// live in ordinary VGPRs (no accumulator-register copies around the softmax); the
+// eight-wave key split asks for four (128 VGPRs) so that two of its workgroups share a
+// CU.
 template <int D, int SPLIT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(AttnOcc<D>::waves, 8)))
+struct AttnOcc { static constexpr int waves = SPLIT == 8 ? 4 : (D <= 64 ? 2 : 1); };
+
+// SPLIT = 1: a workgroup's 4 waves own 4 x 32 queries and share each K/V tile (double-
+// buffered in LDS, one barrier per tile). SPLIT = 4 or 8: SPLIT waves own the same 32
+// queries and take interleaved key blocks with private tiles; their (max, sum, O)
+// states merge through LDS at the end.
+template <int D, int SPLIT>
+__global__ __launch_bounds__(SPLIT == 1 ? 256 : 64 * SPLIT)
+__attribute__((amdgpu_waves_per_eu(AttnOcc<D, SPLIT>::waves, 8)))
 void attention_kernel(AttnParams p) {
+  constexpr int NT = SPLIT == 1 ? 256 : 64 * SPLIT;
   constexpr int KB = 32;                      // keys per block
   constexpr int DK = D >= 16 ? D / 16 : 1;    // 16-wide k-steps of Q K^T
   constexpr int DB = D >= 32 ? D / 32 : 1;    // 32-row blocks of O^T
@@ -133,9 +144,9 @@ void attention_kernel(AttnParams p) {
   constexpr int VPT = (VCH + TPT - 1) / TPT;
   constexpr bool KALL = KCH % TPT == 0, VALL = VCH % TPT == 0;
   constexpr int TILE = KB * KP + D * VP;      // halves per (K, V^T) tile pair
-  constexpr int NT = SPLIT == 1 ? 2 : 4;      // tile pairs in LDS
-  constexpr int MERGE = SPLIT == 1 ? 0 : 4 * (D * 32 + 64);  // floats for the merge
-  constexpr int LDS_H = NT * TILE > MERGE * 2 ? NT * TILE : MERGE * 2;
+  constexpr int NTILE = SPLIT == 1 ? 2 : SPLIT;
+  constexpr int MERGE = SPLIT == 1 ? 0 : SPLIT * (D * 32 + 64);  // floats for the merge
+  constexpr int LDS_H = NTILE * TILE > MERGE * 2 ? NTILE * TILE : MERGE * 2;
   __shared__ __attribute__((aligned(16))) f16 smem[LDS_H];
 
   // The wave index is uniform; readfirstlane lets the compiler keep block indices,
@@ -144,7 +155,7 @@ void attention_kernel(AttnParams p) {
   const int hf = lane >> 5, col = lane & 31;
   const int h = blockIdx.y, b = blockIdx.z;
   const int q0 = SPLIT == 1 ? blockIdx.x * 128 + wave * 32 : blockIdx.x * 32;
-  f16* Ks = smem + (SPLIT == 1 ? 0 : wave) * TILE;  // SPLIT = 4: this wave's tile
+  f16* Ks = smem + (SPLIT == 1 ? 0 : wave) * TILE;  // SPLIT > 1: this wave's tile
   const int ltid = SPLIT == 1 ? threadIdx.x : lane;
 
   const f16* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
@@ -170,72 +181,80 @@ void attention_kernel(AttnParams p) {
     for (int e = 0; e < 16; e++) o[i][e] = 0.f;
   float m = -INFINITY, l = 0.f;
 
-  // This thread's 16-byte chunks of a tile: K chunk i = key (chn / KG), dims
-  // (chn % KG) * 8, stored at LDS row key_row(key); V^T chunk i = dim row chn / 4, keys
-  // (chn % 4) * 8. Byte offsets from the tile base fit in 32 bits (the host bounds ks1
-  // and D * vtp).
-  unsigned koff[KPT], voff[VPT];
-  int kst_off[KPT], vst_off[VPT];
-#pragma unroll
-  for (int i = 0; i < KPT; i++) {
-    const int chn = ltid + i * TPT;
-    const int key = (chn / KG) & 31;
-    koff[i] = (unsigned)(key * p.ks1 + (chn % KG) * 8) * 2u;
-    kst_off[i] = key_row(key) * KP + (chn % KG) * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < VPT; i++) {
-    const int chn = ltid + i * TPT;
-    voff[i] = (unsigned)((chn >> 2) * p.vtp + (chn & 3) * 8) * 2u;
-    vst_off[i] = (chn >> 2) * VP + (chn & 3) * 8;
-  }
+  // This thread's 16-byte chunks of a tile: K chunk i = key k0 + i * KST, dims
+  // (ltid % KG) * 8, stored at LDS row key_row(key); V^T chunk i = dim row
+  // ltid / 4 + i * TPT / 4, keys (ltid % 4) * 8. Only the i = 0 offsets live in registers:
+  // the others add a uniform byte stride (global side) or a constant (LDS side, since
+  // key_row acts bitwise on the disjoint bits of k0 and i * KST). Byte offsets from the
+  // tile base fit in 32 bits (the host bounds ks1 and D * vtp).
+  constexpr int KST = TPT / KG;               // keys between a thread's K chunks
+  const int k0 = ltid / KG, dc = ltid % KG;
+  const unsigned koff0 = (unsigned)(k0 * p.ks1 + dc * 8) * 2u;
+  const unsigned kstep = (unsigned)(KST * p.ks1) * 2u;
+  const int kst0 = key_row(k0) * KP + dc * 8;
+  const unsigned voff0 = (unsigned)((ltid >> 2) * p.vtp + (ltid & 3) * 8) * 2u;
+  const unsigned vstep = (unsigned)((TPT / 4) * p.vtp) * 2u;
+  const int vst0 = (ltid >> 2) * VP + (ltid & 3) * 8;
 
-  f16x8 kst[KPT], vst[VPT];
+  // PF register sets of tile chunks. PF = 2: the tile two blocks ahead loads while the
+  // next one is stored and the current one is multiplied. PF = 1 (eight-wave key split,
+  // where the register budget must allow four waves per SIMD): the next tile loads
+  // while the current one is multiplied.
+  constexpr int PF = (SPLIT == 8 || D >= 128) ? 1 : 2;
+  f16x8 kst[PF][KPT], vst[PF][VPT];
   // Tile loads through buffer resources whose extent ends at the last valid key:
   // addresses need no per-lane arithmetic and rows past the key length read as zero.
   // (V^T reads past a row's padded end wrap into the next row: finite values whose
   // probabilities are zero.)
-  auto load_tile = [&](int kbase) {
+  auto load_tile = [&](auto set_c, int kbase) {
+    constexpr int S = decltype(set_c)::value;
     const int rows = min(KB, p.LK - kbase);
     const auto kr = make_rsrc(kb_ + (int64_t)kbase * p.ks1, (unsigned)(((rows - 1) * p.ks1 + D) * 2));
     const auto vr = make_rsrc(vtb + kbase, (unsigned)((D * p.vtp - kbase) * 2));
 #pragma unroll
     for (int i = 0; i < KPT; i++)
-      if (KALL || ltid + i * TPT < KCH) kst[i] = buffer_load16(kr, koff[i]);
+      if (KALL || ltid + i * TPT < KCH) kst[S][i] = buffer_load16(kr, koff0, i * kstep);
 #pragma unroll
     for (int i = 0; i < VPT; i++)
-      if (VALL || ltid + i * TPT < VCH) vst[i] = buffer_load16(vr, voff[i]);
+      if (VALL || ltid + i * TPT < VCH) vst[S][i] = buffer_load16(vr, voff0, i * vstep);
   };
-  auto store_tile = [&](f16* kd) {
+  auto store_tile = [&](auto set_c, f16* kd) {
+    constexpr int S = decltype(set_c)::value;
     f16* vd = kd + KB * KP;
 #pragma unroll
     for (int i = 0; i < KPT; i++)
-      if (KALL || ltid + i * TPT < KCH) *reinterpret_cast<f16x8*>(kd + kst_off[i]) = kst[i];
+      if (KALL || ltid + i * TPT < KCH)
+        *reinterpret_cast<f16x8*>(kd + kst0 + key_row((i * KST) & 31) * KP) = kst[S][i];
 #pragma unroll
     for (int i = 0; i < VPT; i++)
-      if (VALL || ltid + i * TPT < VCH) *reinterpret_cast<f16x8*>(vd + vst_off[i]) = vst[i];
+      if (VALL || ltid + i * TPT < VCH) *reinterpret_cast<f16x8*>(vd + vst0 + i * (TPT / 4) * VP) = vst[S][i];
   };
 
   const int nblk = (p.LK + KB - 1) / KB;
-  const int nit = SPLIT == 1 ? nblk : (nblk - wave + 3) / 4;   // this wave's blocks
-  auto blk_of = [&](int it) { return SPLIT == 1 ? it : it * 4 + wave; };
-  // Tile buffers: SPLIT = 1 double-buffers the shared tile (one barrier per block);
-  // SPLIT = 4 gives each wave one private tile, rewritten after the block's reads (LDS
-  // operations of one wave complete in program order).
+  const int nit = SPLIT == 1 ? nblk : (nblk - wave + SPLIT - 1) / SPLIT;   // this wave's blocks
+  auto blk_of = [&](int it) { return SPLIT == 1 ? it : it * SPLIT + wave; };
   auto tile_k = [&](int it) { return SPLIT == 1 ? smem + (it & 1) * TILE : Ks; };
-  if (nit > 0) {
-    load_tile(blk_of(0) * KB);
-    store_tile(tile_k(0));
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  if (nit > 0) load_tile(S0(), blk_of(0) * KB);
+  if (nit > 0) store_tile(S0(), tile_k(0));
+  if constexpr (PF == 2) {
+    if (nit > 1) load_tile(S1(), blk_of(1) * KB);
   }
   if constexpr (SPLIT == 1) __syncthreads();
-  // All vector-memory loads so far (Q fragments, first tile) have landed; stating it
-  // keeps the loop's MFMAs from waiting on the in-flight prefetch of the next tile.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   const f16x2 ones = {(f16)1, (f16)1};
-  for (int it = 0; it < nit; it++) {
+
+  // One key block: block it is in LDS, block it + 1 in register set NEXT (stored after
+  // the multiply), block it + 2 is loaded into the other set.
+  auto block = [&](int it, auto next_c) {
+    constexpr int NX = PF == 2 ? decltype(next_c)::value : 0;
+    using NXC = std::integral_constant<int, NX>;
     const int kbase = blk_of(it) * KB;
-    const bool more = it + 1 < nit;
-    if (more) load_tile(blk_of(it + 1) * KB);
+    if constexpr (PF == 2) {
+      if (it + 2 < nit) load_tile(std::integral_constant<int, 1 - NX>(), blk_of(it + 2) * KB);
+    } else {
+      if (it + 1 < nit) load_tile(NXC(), blk_of(it + 1) * KB);
+    }
     const f16* Kc = tile_k(it);
     const f16* Vc = Kc + KB * KP;
 
@@ -311,13 +330,23 @@ void attention_kernel(AttnParams p) {
       }
     }
     if constexpr (SPLIT == 1) {
-      if (more) store_tile(tile_k(it + 1));
+      if (it + 1 < nit) store_tile(NXC(), tile_k(it + 1));
       __syncthreads();
     } else {
+      // Wave-private tile: LDS operations of one wave complete in order, so only the
+      // compiler must keep the stores after this block's reads.
       __builtin_amdgcn_wave_barrier();
-      if (more) store_tile(Ks);
+      if (it + 1 < nit) store_tile(NXC(), Ks);
       __builtin_amdgcn_wave_barrier();
     }
+  };
+  // Wait once for every vector-memory load so far (Q fragments, the first tiles): the
+  // compiler then sees nothing outstanding that the loop's MFMAs read, and no longer
+  // drains the tile prefetch in front of them.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  for (int it = 0; it < nit; it += 2) {
+    block(it, S1());
+    if (it + 1 < nit) block(it + 1, S0());
   }
   l = halves_sum(l);
 
@@ -341,9 +370,9 @@ void attention_kernel(AttnParams p) {
         }
     }
   } else {
-    // Merge the four waves' states: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
-    float* mo = reinterpret_cast<float*>(smem);            // [4][D][32] partial O^T
-    float* ml = mo + 4 * D * 32;                            // [4][32] m, then [4][32] l
+    // Merge the waves' states: O = sum_w 2^(m_w - M) O_w / sum_w 2^(m_w - M) l_w.
+    float* mo = reinterpret_cast<float*>(smem);            // [SPLIT][D][32] partial O^T
+    float* ml = mo + SPLIT * D * 32;                        // [SPLIT][32] m, then [SPLIT][32] l
     __syncthreads();
 #pragma unroll
     for (int db = 0; db < DB; db++)
@@ -352,18 +381,18 @@ void attention_kernel(AttnParams p) {
         const int d = db * 32 + (e >> 2) * 8 + 4 * hf + (e & 3);
         if (d < D) mo[(wave * D + d) * 32 + col] = o[db][e];
       }
-    if (hf == 0) { ml[wave * 32 + col] = m; ml[128 + wave * 32 + col] = l; }
+    if (hf == 0) { ml[wave * 32 + col] = m; ml[SPLIT * 32 + wave * 32 + col] = l; }
     __syncthreads();
     // Thread t finishes query t % 32 for dims (t / 32) * 4 .. + 4.
-    for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += 256) {
+    for (int idx = threadIdx.x; idx < 32 * (D / 4); idx += NT) {
       const int qq = idx & 31, d4 = (idx >> 5) * 4;
-      float mw[4], M = -INFINITY;
+      float mw[SPLIT], M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < 4; w++) { mw[w] = ml[w * 32 + qq]; M = fmaxf(M, mw[w]); }
+      for (int w = 0; w < SPLIT; w++) { mw[w] = ml[w * 32 + qq]; M = fmaxf(M, mw[w]); }
       const float bse = M == -INFINITY ? 0.f : M;
-      float den = 0.f, f[4];
+      float den = 0.f, f[SPLIT];
 #pragma unroll
-      for (int w = 0; w < 4; w++) { f[w] = exp2f(mw[w] - bse); den += f[w] * ml[128 + w * 32 + qq]; }
+      for (int w = 0; w < SPLIT; w++) { f[w] = exp2f(mw[w] - bse); den += f[w] * ml[SPLIT * 32 + w * 32 + qq]; }
       const float inv = den > 0.f ? 1.0f / den : 0.f;
       const int qg = q0 + qq;
       if (qg < p.L) {
@@ -372,7 +401,7 @@ void attention_kernel(AttnParams p) {
         for (int r = 0; r < 4; r++) {
           float acc = 0.f;
 #pragma unroll
-          for (int w = 0; w < 4; w++) acc += f[w] * mo[(w * D + d4 + r) * 32 + qq];
+          for (int w = 0; w < SPLIT; w++) acc += f[w] * mo[(w * D + d4 + r) * 32 + qq];
           out[r] = (f16)(acc * inv);
         }
         *reinterpret_cast<f16x4*>(ob + (int64_t)qg * p.os1 + d4) = out;
@@ -385,15 +414,24 @@ template <int D, int SPLIT>
 static int launch_attn(const AttnParams& p, hipStream_t st) {
   const int per = SPLIT == 1 ? 128 : 32;
   dim3 grid((unsigned)((p.L + per - 1) / per), (unsigned)p.H, (unsigned)p.B);
-  hipLaunchKernelGGL((attention_kernel<D, SPLIT>), grid, dim3(256), 0, st, p);
+  hipLaunchKernelGGL((attention_kernel<D, SPLIT>), grid, dim3(SPLIT == 1 ? 256 : 64 * SPLIT), 0, st, p);
   return check_launch("attention");
 }
 
 template <int D>
 static int launch_d(const AttnParams& p, hipStream_t st) {
-  // Key-split workgroups when 128-query workgroups would leave most CUs idle.
+  // Key-split workgroups when 128-query workgroups would leave most CUs idle: eight
+  // waves per 32 queries for long key sequences (head width <= 64), else four.
   const int64_t wgs = (int64_t)((p.L + 127) / 128) * p.H * p.B;
-  if (D <= 128 && wgs < 512 && p.LK > 64) return launch_attn<D, D <= 128 ? 4 : 1>(p, st);
+  int split = 1;
+  if (const char* env = getenv("LDX_ATTN_SPLIT")) split = atoi(env);
+  else if (D <= 128 && wgs < 512 && p.LK > 64) split = (D <= 64 && p.LK >= 512) ? 8 : 4;
+  if constexpr (D <= 64) {
+    if (split == 8) return launch_attn<D, 8>(p, st);
+  }
+  if constexpr (D <= 128) {
+    if (split == 4 || split == 8) return launch_attn<D, 4>(p, st);
+  }
   return launch_attn<D, 1>(p, st);
 }
 
