@@ -5,16 +5,17 @@
 // = keys, columns = queries), so the lane's score registers -- 16 of the block's keys
 // for one query -- are already the B operand of O^T = V^T P^T: probabilities never
 // leave registers, and the running max / rescale / partial row sum of a query are
-// lane-local (its other 16 keys sit in lane ^ 32, one swizzle away). Q^T stays in
-// registers; K (row-major) and V^T (transposed once per call by transpose_v_kernel)
-// stream through LDS with 16-byte stores, the next block's global loads in flight
-// during the current block. Masking and key bounds are applied only on blocks that
+// lane-local (its other 16 keys sit in lane ^ 32, one lane swap away). Q^T stays in
+// registers. K and V tiles (rows = keys, as they lie in memory) stream through LDS with
+// 16-byte stores, loaded one or two blocks ahead through buffer resources; the V^T
+// operand is read back with gfx950's transposing LDS read (ds_read_b64_tr_b16), so V is
+// never transposed in memory. Masking and key bounds are applied only on blocks that
 // need them; row sums use v_dot2 on the fp16 probabilities the PV product consumes.
 //
 // SPLIT = 1: a workgroup's 4 waves own 4 x 32 queries and share each K/V tile.
-// SPLIT = 4: the 4 waves own the same 32 queries and take interleaved key blocks with
-// private tiles; their (max, sum, O) states merge through LDS at the end -- four times
-// the waves for short sequences (1,600 tokens x 8 heads is only 400 query blocks).
+// SPLIT = 4 / 8: the waves own the same 32 queries and take interleaved key blocks with
+// private tiles; their (max, sum, O) states merge through LDS at the end -- more waves
+// for short sequences (1,600 tokens x 8 heads is only 400 query blocks).
 //
 // Reference semantics: flash_attention_half (src/lesiondiffusion_mlx/_attention_half.py:
 // 23-114): scores scaled by scale*log2(e) in fp32 (:70-72), exp2 online softmax
@@ -33,7 +34,7 @@ struct AttnParams {
   int B, H, L, LK;
   const f16* q; int64_t qs0, qs1, qs2;
   const f16* k; int64_t ks0, ks1, ks2;
-  const f16* vt; int64_t vtp;  // V^T: row ((b * H + h) * D + d), keys contiguous, pitch vtp
+  const f16* v; int64_t vs0, vs1, vs2;
   f16* o; int64_t os0, os1, os2;
   float c;  // scale * log2(e)
   const float* mask; int64_t ms0, ms1, ms2, ms3;
@@ -87,25 +88,14 @@ __device__ __forceinline__ float halves_sum(float v) {
   return __int_as_float(r[0]) + __int_as_float(r[1]);
 }
 
-// V (B, LK, H, D) with strides -> V^T rows ((b * H + h) * D + d) of `pitch` keys, the
-// keys in [LK, pitch) zero. 32 keys x 32 dims per 256-thread tile.
-__global__ __launch_bounds__(256) void transpose_v_kernel(const f16* __restrict__ v, int64_t s0, int64_t s1,
-                                                          int64_t s2, int LK, int H, int D, int64_t pitch,
-                                                          f16* __restrict__ vt) {
-  __shared__ f16 tile[32][33];
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-  const int k0 = blockIdx.x * 32, d0 = blockIdx.y * 32;
-  const int bh = blockIdx.z, b = bh / H, h = bh % H;
-  const f16* src = v + (int64_t)b * s0 + (int64_t)h * s2;
-  for (int i = ty; i < 32; i += 8) {
-    const int key = k0 + i, d = d0 + tx;
-    tile[i][tx] = (key < LK && d < D) ? src[(int64_t)key * s1 + d] : (f16)0;
-  }
-  __syncthreads();
-  for (int i = ty; i < 32; i += 8) {
-    const int d = d0 + i, key = k0 + tx;
-    if (d < D && key < pitch) vt[((int64_t)bh * D + d) * pitch + key] = tile[tx][i];
-  }
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Pointer into this workgroup's LDS as the address-space-3 pointer that the transposing
+// read takes.
+__device__ __forceinline__ lds_s16x4* lds_v4(const f16* p) {
+  return (lds_s16x4*)((__attribute__((address_space(3))) char*)(p));
 }
 
 // The keys of a 32-key block are stored in LDS K-tile rows permuted by pi (bits 2 and 3
@@ -135,19 +125,18 @@ void attention_kernel(AttnParams p) {
   constexpr int DK = D >= 16 ? D / 16 : 1;    // 16-wide k-steps of Q K^T
   constexpr int DB = D >= 32 ? D / 32 : 1;    // 32-row blocks of O^T
   constexpr int KP = D + 8;                   // K tile pitch (halves)
-  constexpr int VP = KB + 8;                  // V^T tile pitch (halves)
   constexpr int KG = D / 8;                   // 16-byte chunks per key row
   constexpr int KCH = KB * KG;                // 16-byte chunks of a K tile
-  constexpr int VCH = D * (KB / 8);           // 16-byte chunks of a V^T tile
   constexpr int TPT = SPLIT == 1 ? 256 : 64;  // threads loading one tile
   constexpr int KPT = (KCH + TPT - 1) / TPT;
-  constexpr int VPT = (VCH + TPT - 1) / TPT;
-  constexpr bool KALL = KCH % TPT == 0, VALL = VCH % TPT == 0;
-  constexpr int TILE = KB * KP + D * VP;      // halves per (K, V^T) tile pair
+  constexpr bool KALL = KCH % TPT == 0;
+  constexpr int TILE = 2 * KB * KP;           // halves per (K, V) tile pair, rows = keys
   constexpr int NTILE = SPLIT == 1 ? 2 : SPLIT;
   constexpr int MERGE = SPLIT == 1 ? 0 : SPLIT * (D * 32 + 64);  // floats for the merge
   constexpr int LDS_H = NTILE * TILE > MERGE * 2 ? NTILE * TILE : MERGE * 2;
-  __shared__ __attribute__((aligned(16))) f16 smem[LDS_H];
+  // (+64 halves: for D = 16 the transposing V reads of the unused O^T rows 16..31 run
+  // up to 8 halves past the last tile.)
+  __shared__ __attribute__((aligned(16))) f16 smem[LDS_H + 64];
 
   // The wave index is uniform; readfirstlane lets the compiler keep block indices,
   // tile bases and loop conditions in scalar registers.
@@ -160,7 +149,7 @@ void attention_kernel(AttnParams p) {
 
   const f16* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
   const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
-  const f16* vtb = p.vt + ((int64_t)b * p.H + h) * D * p.vtp;
+  const f16* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
 
   // Q^T fragments: lane holds query q0 + col, dims 16*dk + 8*hf .. +7.
   const int qi = min(q0 + col, p.L - 1);
@@ -181,27 +170,32 @@ void attention_kernel(AttnParams p) {
     for (int e = 0; e < 16; e++) o[i][e] = 0.f;
   float m = -INFINITY, l = 0.f;
 
-  // This thread's 16-byte chunks of a tile: K chunk i = key k0 + i * KST, dims
-  // (ltid % KG) * 8, stored at LDS row key_row(key); V^T chunk i = dim row
-  // ltid / 4 + i * TPT / 4, keys (ltid % 4) * 8. Only the i = 0 offsets live in registers:
-  // the others add a uniform byte stride (global side) or a constant (LDS side, since
-  // key_row acts bitwise on the disjoint bits of k0 and i * KST). Byte offsets from the
-  // tile base fit in 32 bits (the host bounds ks1 and D * vtp).
-  constexpr int KST = TPT / KG;               // keys between a thread's K chunks
+  // This thread's 16-byte chunks of a tile: chunk i = key k0 + i * KST, dims
+  // (ltid % KG) * 8, of K (stored at LDS row key_row(key)) and of V (stored at row key).
+  // Only the i = 0 offsets live in registers: the others add a uniform byte stride
+  // (global side) or a constant (LDS side, since key_row acts bitwise on the disjoint
+  // bits of k0 and i * KST). Byte offsets from the tile base fit in 32 bits (the host
+  // bounds the key strides).
+  constexpr int KST = TPT / KG;               // keys between a thread's chunks
   const int k0 = ltid / KG, dc = ltid % KG;
   const unsigned koff0 = (unsigned)(k0 * p.ks1 + dc * 8) * 2u;
   const unsigned kstep = (unsigned)(KST * p.ks1) * 2u;
+  const unsigned voff0 = (unsigned)(k0 * p.vs1 + dc * 8) * 2u;
+  const unsigned vstep = (unsigned)(KST * p.vs1) * 2u;
   const int kst0 = key_row(k0) * KP + dc * 8;
-  const unsigned voff0 = (unsigned)((ltid >> 2) * p.vtp + (ltid & 3) * 8) * 2u;
-  const unsigned vstep = (unsigned)((TPT / 4) * p.vtp) * 2u;
-  const int vst0 = (ltid >> 2) * VP + (ltid & 3) * 8;
+  const int vst0 = k0 * KP + dc * 8;
+  // V^T operand of a PV k-step through transposing LDS reads: in each 16-lane group g,
+  // lane i addresses row 8 * (g / 2) + i / 4 (+ 4 for the second half, + 16 per k-step)
+  // at dims 16 * (g % 2) + 4 * (i % 4) (+ 32 per block of O^T rows), and receives dim
+  // 16 * (g % 2) + i of that row group's four keys.
+  const int vtr0 = (8 * (lane >> 5) + ((lane & 15) >> 2)) * KP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
   // PF register sets of tile chunks. PF = 2: the tile two blocks ahead loads while the
   // next one is stored and the current one is multiplied. PF = 1 (eight-wave key split,
   // where the register budget must allow four waves per SIMD): the next tile loads
   // while the current one is multiplied.
   constexpr int PF = (SPLIT == 8 || D >= 128) ? 1 : 2;
-  f16x8 kst[PF][KPT], vst[PF][VPT];
+  f16x8 kst[PF][KPT], vst[PF][KPT];
   // Tile loads through buffer resources whose extent ends at the last valid key:
   // addresses need no per-lane arithmetic and rows past the key length read as zero.
   // (V^T reads past a row's padded end wrap into the next row: finite values whose
@@ -210,13 +204,13 @@ void attention_kernel(AttnParams p) {
     constexpr int S = decltype(set_c)::value;
     const int rows = min(KB, p.LK - kbase);
     const auto kr = make_rsrc(kb_ + (int64_t)kbase * p.ks1, (unsigned)(((rows - 1) * p.ks1 + D) * 2));
-    const auto vr = make_rsrc(vtb + kbase, (unsigned)((D * p.vtp - kbase) * 2));
+    const auto vr = make_rsrc(vb_ + (int64_t)kbase * p.vs1, (unsigned)(((rows - 1) * p.vs1 + D) * 2));
 #pragma unroll
     for (int i = 0; i < KPT; i++)
       if (KALL || ltid + i * TPT < KCH) kst[S][i] = buffer_load16(kr, koff0, i * kstep);
 #pragma unroll
-    for (int i = 0; i < VPT; i++)
-      if (VALL || ltid + i * TPT < VCH) vst[S][i] = buffer_load16(vr, voff0, i * vstep);
+    for (int i = 0; i < KPT; i++)
+      if (KALL || ltid + i * TPT < KCH) vst[S][i] = buffer_load16(vr, voff0, i * vstep);
   };
   auto store_tile = [&](auto set_c, f16* kd) {
     constexpr int S = decltype(set_c)::value;
@@ -226,8 +220,8 @@ void attention_kernel(AttnParams p) {
       if (KALL || ltid + i * TPT < KCH)
         *reinterpret_cast<f16x8*>(kd + kst0 + key_row((i * KST) & 31) * KP) = kst[S][i];
 #pragma unroll
-    for (int i = 0; i < VPT; i++)
-      if (VALL || ltid + i * TPT < VCH) *reinterpret_cast<f16x8*>(vd + vst0 + i * (TPT / 4) * VP) = vst[S][i];
+    for (int i = 0; i < KPT; i++)
+      if (KALL || ltid + i * TPT < KCH) *reinterpret_cast<f16x8*>(vd + vst0 + ((i * KST) & 31) * KP) = vst[S][i];
   };
 
   const int nblk = (p.LK + KB - 1) / KB;
@@ -323,9 +317,10 @@ void attention_kernel(AttnParams p) {
     for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
       for (int db = 0; db < DB; db++) {
-        const int d = db * 32 + col;
-        f16x8 vf = {0, 0, 0, 0, 0, 0, 0, 0};
-        if (d < D) vf = *reinterpret_cast<const f16x8*>(Vc + d * VP + ks * 16 + 8 * hf);
+        const f16* va = Vc + vtr0 + ks * 16 * KP + db * 32;
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(va));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(va + 4 * KP));
+        const f16x8 vf = __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
         o[db] = mfma32x(vf, pf[ks], o[db]);
       }
     }
@@ -453,49 +448,37 @@ static int check_attention_args(const ldx_attention_args* a) {
   const void* ps[4] = {a->q, a->k, a->v, a->o};
   for (int i = 0; i < 4; i++) {
     for (int j = 0; j < 3; j++)
-      if (ss[i][j] % 8 != 0 && i != 2) return fail("attention: strides must be multiples of 8 elements");
-    if ((uintptr_t)ps[i] % 16 != 0 && i != 2) return fail("attention: tensors must be 16-byte aligned");
+      if (ss[i][j] % 8 != 0) return fail("attention: strides must be multiples of 8 elements");
+    if ((uintptr_t)ps[i] % 16 != 0) return fail("attention: tensors must be 16-byte aligned");
   }
-  // In-tile offsets are 32-bit: 32 key rows of K, D rows of the transposed V.
-  if (a->k_stride[1] < 0 || a->k_stride[1] > (1 << 25))
-    return fail("attention: key stride %lld out of range", (long long)a->k_stride[1]);
-  if ((int64_t)a->head_dim * (((int64_t)a->kv_len + 7) / 8 * 8) >= ((int64_t)1 << 31))
-    return fail("attention: kv_len %d too long for head_dim %d", a->kv_len, a->head_dim);
+  // In-tile offsets are 32-bit: 32 key rows of K and of V.
+  for (int i = 1; i < 3; i++)
+    if (ss[i][1] < 0 || ss[i][1] > (1 << 25))
+      return fail("attention: key stride %lld out of range", (long long)ss[i][1]);
   return LDX_OK;
 }
 
-static int64_t vt_pitch(const ldx_attention_args* a) { return ((int64_t)a->kv_len + 7) / 8 * 8; }
-
+// No scratch memory is needed (V is transposed by the LDS reads); the workspace fields
+// of the argument struct are accepted and ignored.
 extern "C" size_t ldx_attention_workspace_bytes(const ldx_attention_args* a) {
-  if (check_attention_args(a) != LDX_OK) return 0;
-  return (size_t)a->batch * a->heads * a->head_dim * vt_pitch(a) * sizeof(f16) + 256;
+  (void)a;
+  return 0;
 }
 
 extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
   int rc = check_attention_args(a);
   if (rc != LDX_OK) return rc;
-  const size_t need = ldx_attention_workspace_bytes(a);
-  if (!a->workspace || a->workspace_bytes < need)
-    return fail("attention: workspace of %zu bytes required (got %zu)", need, a->workspace_bytes);
   const int D = a->head_dim;
   AttnParams p{};
   p.B = a->batch; p.H = a->heads; p.L = a->q_len; p.LK = a->kv_len;
   p.q = (const f16*)a->q; p.qs0 = a->q_stride[0]; p.qs1 = a->q_stride[1]; p.qs2 = a->q_stride[2];
   p.k = (const f16*)a->k; p.ks0 = a->k_stride[0]; p.ks1 = a->k_stride[1]; p.ks2 = a->k_stride[2];
+  p.v = (const f16*)a->v; p.vs0 = a->v_stride[0]; p.vs1 = a->v_stride[1]; p.vs2 = a->v_stride[2];
   p.o = (f16*)a->o; p.os0 = a->o_stride[0]; p.os1 = a->o_stride[1]; p.os2 = a->o_stride[2];
   p.c = a->scale * 1.44269504088896341f;
   p.mask = a->mask;
   p.ms0 = a->mask_stride[0]; p.ms1 = a->mask_stride[1]; p.ms2 = a->mask_stride[2]; p.ms3 = a->mask_stride[3];
-  // 256-byte aligned V^T inside the workspace.
-  f16* vt = (f16*)(((uintptr_t)a->workspace + 255) & ~(uintptr_t)255);
-  p.vt = vt;
-  p.vtp = vt_pitch(a);
   hipStream_t st = as_stream(stream);
-  dim3 tg((unsigned)((p.vtp + 31) / 32), (unsigned)((D + 31) / 32), (unsigned)(p.B * p.H));
-  hipLaunchKernelGGL(transpose_v_kernel, tg, dim3(256), 0, st, (const f16*)a->v, a->v_stride[0],
-                     a->v_stride[1], a->v_stride[2], p.LK, p.H, D, p.vtp, vt);
-  rc = check_launch("attention: transpose V");
-  if (rc != LDX_OK) return rc;
   switch (D) {
     case 16: return launch_d<16>(p, st);
     case 32: return launch_d<32>(p, st);
