@@ -48,15 +48,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-// Raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor word 3): loads at
-// offsets past the extent return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned soff = 0) {
-  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
-}
 
 // acc *= a with tied operands, so the branch that rescales leaves the accumulator in
 // the registers the other branch keeps it in (no copies across the loop). The compiler

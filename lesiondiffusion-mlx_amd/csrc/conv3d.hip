@@ -78,15 +78,6 @@ __device__ __forceinline__ f16 post_act_t(f16 h) {
 // lies at least 0.5 / d from an integer, far beyond the float error of the product.
 __device__ __forceinline__ int fdiv(int t, float rcp) { return (int)(((float)t + 0.5f) * rcp); }
 
-// Raw buffer resource over `bytes` bytes from `base` (gfx9 descriptor word 3): loads at
-// offsets past the extent return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, unsigned bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-
-__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-}
 
 // Stage the halo of one brick for channels [c0, c0 + CC) into LDS, applying the
 // affine + SiLU prologue and zero padding. Global loads are issued NB at a time before
@@ -217,6 +208,123 @@ template <int N>
 __device__ __forceinline__ void vmcnt_wait() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Epilogue of one wave's FO x FV block of 32 x 32 accumulator tiles, through its LDS
+// staging area `stg` (32 x (FO * 32 + 4) floats): voxels of the brick at (d0, h0, w0)
+// (slot (wv * FV + fv) * 32 + v), output channels from 32 * ob_first.
+template <int FO, int FV>
+__device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x16 (&acc)[FO][FV], float* stg, int lane,
+                                              int wv, int ob_first, int b, int sidx, int pd, int ph, int pw,
+                                              int d0, int h0, int w0) {
+  constexpr int EPW = FO * 32 + 4;   // staging pitch (floats): conflict-free both ways
+  // Epilogue through LDS: each wave stages one 32-voxel column block at a time (its
+  // FO * 32 channels in fp32, voxel-major), then each lane finishes 8 channels of
+  // 32 * G8 / 64 voxels -- bias, shift, scale, residual, one rounding, activation -- and
+  // writes each as one 16-byte store, the lanes of a voxel covering its channels
+  // contiguously. A lane's channel group is the same for every voxel it finishes, so
+  // its bias and shift are loaded once; the residual rows are all requested before the
+  // first is used.
+  constexpr int G8 = FO * 4;         // 8-channel groups per voxel (divides 64)
+  constexpr int NI = 32 * G8 / 64;   // voxels per lane per column block
+  const int col = lane & 31, hf = lane >> 5;
+  const int g = lane % G8;
+  const int o = ob_first * 32 + g * 8;
+  const int nch = min(8, p.O - o);   // channels of this lane's group (<= 0: none)
+  const bool vec8 = nch == 8 && p.ep_vec;
+  const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
+  const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
+  const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
+  float add8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // bias + shift
+  if (nch > 0) {
+    if (vec8) {
+      if (bias) {
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + o);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + o + 4);
+#pragma unroll
+        for (int r = 0; r < 4; r++) { add8[r] = b0[r]; add8[r + 4] = b1[r]; }
+      }
+      if (shb) {
+        const f16x8 s8 = *reinterpret_cast<const f16x8*>(shb + o);
+#pragma unroll
+        for (int r = 0; r < 8; r++) add8[r] += (float)s8[r];
+      }
+    } else {
+      for (int r = 0; r < nch; r++) add8[r] = (bias ? bias[o + r] : 0.f) + (shb ? (float)shb[o + r] : 0.f);
+    }
+  }
+  // One copy of the store loop per activation: no per-element branch on it.
+  auto finish = [&](auto act_c) {
+  constexpr int ACT = decltype(act_c)::value;
+#pragma unroll
+  for (int fv = 0; fv < FV; fv++) {
+    // Lane (hf, col) holds voxel col, channels fo * 32 + j * 8 + 4 * hf + r.
+#pragma unroll
+    for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const f32x4 q = {acc[fo][fv][j * 4], acc[fo][fv][j * 4 + 1], acc[fo][fv][j * 4 + 2], acc[fo][fv][j * 4 + 3]};
+        *reinterpret_cast<f32x4*>(stg + col * EPW + fo * 32 + j * 8 + 4 * hf) = q;
+      }
+    __builtin_amdgcn_wave_barrier();  // (LDS operations of a wave complete in order)
+    int64_t ov[NI];
+    bool ok[NI];
+    f16x8 re8[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int v = lane / G8 + i * (64 / G8);
+      const int vloc = (wv * FV + fv) * 32 + v;
+      const int vt = fdiv(vloc, p.rTW), vw = vloc - vt * p.TW;
+      const int vd = fdiv(vt, p.rTH), vh = vt - vd * p.TH;
+      const int rd = d0 + vd, rh = h0 + vh, rw = w0 + vw;
+      ok[i] = nch > 0 && vd < p.TD && rd < p.RD && rh < p.RH && rw < p.RW;
+      if (p.upsample)
+        ov[i] = ((int64_t)(2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
+      else
+        ov[i] = ((int64_t)rd * p.OH + rh) * p.OW + rw;
+      ov[i] += (int64_t)b * ovol;
+      re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      if (ok[i] && p.res && vec8 && p.split == 1) re8[i] = *reinterpret_cast<const f16x8*>(p.res + ov[i] * p.resp + o);
+    }
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      if (!ok[i]) continue;
+      const int v = lane / G8 + i * (64 / G8);
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
+      const float r8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      if (p.split > 1) {
+        // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
+        float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov[i]) * p.O + o;
+        if (vec8) {
+          *reinterpret_cast<f32x4*>(prow) = lo;
+          *reinterpret_cast<f32x4*>(prow + 4) = hi;
+        } else {
+          for (int r = 0; r < nch; r++) prow[r] = r8[r];
+        }
+        continue;
+      }
+      f16* yrow = p.y + ov[i] * p.yp + o;
+      if (vec8) {
+        f16x8 out;
+#pragma unroll
+        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + add8[r]) * p.scale + (float)re8[i][r]));
+        *reinterpret_cast<f16x8*>(yrow) = out;
+      } else {
+        const f16* rrow = p.res ? p.res + ov[i] * p.resp + o : nullptr;
+        for (int r = 0; r < nch; r++) {
+          float t = (r8[r] + add8[r]) * p.scale;
+          if (rrow) t += (float)rrow[r];
+          yrow[r] = post_act_t<ACT>((f16)t);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  };
+  if (p.act == LDX_ACT_GELU) finish(std::integral_constant<int, LDX_ACT_GELU>());
+  else if (p.act == LDX_ACT_SILU) finish(std::integral_constant<int, LDX_ACT_SILU>());
+  else finish(std::integral_constant<int, LDX_ACT_NONE>());
 }
 
 // KSPL K-groups of 4 waves each: group g takes k-steps [g * KS / KSPL, (g + 1) * KS /
@@ -420,114 +528,122 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
         }
   }
 
-  // Epilogue through LDS: each wave stages one 32-voxel column block at a time (its
-  // FO * 32 channels in fp32, voxel-major), then each lane finishes 8 channels of
-  // 32 * G8 / 64 voxels -- bias, shift, scale, residual, one rounding, activation -- and
-  // writes each as one 16-byte store, the lanes of a voxel covering its channels
-  // contiguously. A lane's channel group is the same for every voxel it finishes, so
-  // its bias and shift are loaded once; the residual rows are all requested before the
-  // first is used.
-  constexpr int G8 = FO * 4;         // 8-channel groups per voxel (divides 64)
-  constexpr int NI = 32 * G8 / 64;   // voxels per lane per column block
-  float* stg = reinterpret_cast<float*>(smem) + (KSPL == 2 ? RED : 0) + w4 * 32 * EPW;
-  const int col = lane & 31, hf = lane >> 5;
-  const int g = lane % G8;
-  const int o = (ob0 + wo * FO) * 32 + g * 8;
-  const int nch = min(8, p.O - o);   // channels of this lane's group (<= 0: none)
-  const bool vec8 = nch == 8 && p.ep_vec;
-  const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
-  const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
-  const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
-  float add8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // bias + shift
-  if (nch > 0) {
-    if (vec8) {
-      if (bias) {
-        const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + o);
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + o + 4);
-#pragma unroll
-        for (int r = 0; r < 4; r++) { add8[r] = b0[r]; add8[r + 4] = b1[r]; }
-      }
-      if (shb) {
-        const f16x8 s8 = *reinterpret_cast<const f16x8*>(shb + o);
-#pragma unroll
-        for (int r = 0; r < 8; r++) add8[r] += (float)s8[r];
-      }
-    } else {
-      for (int r = 0; r < nch; r++) add8[r] = (bias ? bias[o + r] : 0.f) + (shb ? (float)shb[o + r] : 0.f);
-    }
+  conv_epilogue<FO, FV>(p, acc, reinterpret_cast<float*>(smem) + (KSPL == 2 ? RED : 0) + w4 * 32 * EPW, lane, wv,
+                        ob0 + wo * FO, b, sidx, pd, ph, pw, d0, h0, w0);
+}
+
+// Pointwise conv / dense layer: a GEMM whose operands both come straight from global
+// memory in MFMA lane order -- A is one 1 KB packed-weight fragment per 16-byte-per-lane
+// load, B is 16 bytes of one voxel row per lane -- PD k-steps in flight in registers, no
+// LDS in the main loop (a 1 x 1 x 1 tap has no halo to share). The optional per-(b, c)
+// affine + SiLU prologue is applied to B in registers. The host presents the volume
+// flattened (D = H = 1, W = voxels) so the conv epilogue maps voxel slots directly.
+template <int WO, int WV, int FO, int FV>
+__global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
+  constexpr int BO = WO * FO * 32, BV = WV * FV * 32;
+  constexpr int PD = 4;                       // k-steps of operands in flight
+  constexpr int EPW = FO * 32 + 4;
+  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wo = wave / WV, wv = wave - wo * WV;
+  const int hf = lane >> 5;
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
   }
-  // One copy of the store loop per activation: no per-element branch on it.
-  auto finish = [&](auto act_c) {
-  constexpr int ACT = decltype(act_c)::value;
+  const int nob = (p.O + BO - 1) / BO, nvb = p.NBW;
+  const int oblk = wg % nob, vb = (wg / nob) % nvb, b = wg / nob / nvb;
+  const int NV = p.W;                          // voxels per batch item
+  const int ob0 = oblk * (BO / 32) + wo * FO;  // first 32-row output block of this wave
+  const int nk = (p.C + 15) / 16;              // k-steps
+  const int nk0 = p.C1 > 0 ? p.C0 / 16 : nk;   // k-steps read from x0 (C0 % 16 == 0 with x1)
+
+  // B rows: voxel (vb * BV + (wv * FV + fv) * 32 + lane % 32), clamped into the volume
+  // (slots past it compute on the last voxel and are not stored).
+  const int64_t bvox = (int64_t)b * NV;
+  const auto r0 = make_rsrc(p.x0 + bvox * p.x0p, (unsigned)((int64_t)NV * p.x0p * 2));
+  const auto r1 = p.C1 > 0 ? make_rsrc(p.x1 + bvox * p.x1p, (unsigned)((int64_t)NV * p.x1p * 2)) : r0;
+  unsigned boff0[FV], boff1[FV];
 #pragma unroll
   for (int fv = 0; fv < FV; fv++) {
-    // Lane (hf, col) holds voxel col, channels fo * 32 + j * 8 + 4 * hf + r.
+    const int v = min(vb * BV + (wv * FV + fv) * 32 + (lane & 31), NV - 1);
+    boff0[fv] = (unsigned)(v * p.x0p * 2 + hf * 16);
+    boff1[fv] = (unsigned)(v * p.x1p * 2 + hf * 16);
+  }
+  const auto rw = make_rsrc(p.w, (unsigned)((size_t)p.NOB * p.NKC * 1024));
+  const unsigned aoff = (unsigned)lane * 16u;
+  const float* aff = p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr;
+
+  f16x8 ra[PD][FO], rb[PD][FV];
+  auto load = [&](int set, int kc) {
 #pragma unroll
     for (int fo = 0; fo < FO; fo++)
+      ra[set][fo] = buffer_load16(rw, aoff, (unsigned)((ob0 + fo) * p.NKC + kc) * 1024u);
+    const bool in0 = kc < nk0;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const f32x4 q = {acc[fo][fv][j * 4], acc[fo][fv][j * 4 + 1], acc[fo][fv][j * 4 + 2], acc[fo][fv][j * 4 + 3]};
-        *reinterpret_cast<f32x4*>(stg + col * EPW + fo * 32 + j * 8 + 4 * hf) = q;
-      }
-    __builtin_amdgcn_wave_barrier();  // (LDS operations of a wave complete in order)
-    int64_t ov[NI];
-    bool ok[NI];
-    f16x8 re8[NI];
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-      const int v = lane / G8 + i * (64 / G8);
-      const int vloc = (wv * FV + fv) * 32 + v;
-      const int vt = fdiv(vloc, p.rTW), vw = vloc - vt * p.TW;
-      const int vd = fdiv(vt, p.rTH), vh = vt - vd * p.TH;
-      const int rd = d0 + vd, rh = h0 + vh, rw = w0 + vw;
-      ok[i] = nch > 0 && vd < p.TD && rd < p.RD && rh < p.RH && rw < p.RW;
-      if (p.upsample)
-        ov[i] = ((int64_t)(2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
-      else
-        ov[i] = ((int64_t)rd * p.OH + rh) * p.OW + rw;
-      ov[i] += (int64_t)b * ovol;
-      re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (ok[i] && p.res && vec8 && p.split == 1) re8[i] = *reinterpret_cast<const f16x8*>(p.res + ov[i] * p.resp + o);
-    }
-#pragma unroll
-    for (int i = 0; i < NI; i++) {
-      if (!ok[i]) continue;
-      const int v = lane / G8 + i * (64 / G8);
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
-      const float r8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      if (p.split > 1) {
-        // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
-        float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov[i]) * p.O + o;
-        if (vec8) {
-          *reinterpret_cast<f32x4*>(prow) = lo;
-          *reinterpret_cast<f32x4*>(prow + 4) = hi;
-        } else {
-          for (int r = 0; r < nch; r++) prow[r] = r8[r];
-        }
-        continue;
-      }
-      f16* yrow = p.y + ov[i] * p.yp + o;
-      if (vec8) {
-        f16x8 out;
-#pragma unroll
-        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + add8[r]) * p.scale + (float)re8[i][r]));
-        *reinterpret_cast<f16x8*>(yrow) = out;
-      } else {
-        const f16* rrow = p.res ? p.res + ov[i] * p.resp + o : nullptr;
-        for (int r = 0; r < nch; r++) {
-          float t = (r8[r] + add8[r]) * p.scale;
-          if (rrow) t += (float)rrow[r];
-          yrow[r] = post_act_t<ACT>((f16)t);
-        }
-      }
-    }
-    __builtin_amdgcn_wave_barrier();
-  }
+    for (int fv = 0; fv < FV; fv++)
+      rb[set][fv] = in0 ? buffer_load16(r0, boff0[fv], (unsigned)kc * 32u)
+                        : buffer_load16(r1, boff1[fv], (unsigned)(kc - nk0) * 32u);
   };
-  if (p.act == LDX_ACT_GELU) finish(std::integral_constant<int, LDX_ACT_GELU>());
-  else if (p.act == LDX_ACT_SILU) finish(std::integral_constant<int, LDX_ACT_SILU>());
-  else finish(std::integral_constant<int, LDX_ACT_NONE>());
+  auto prep = [&](int set, int kc) {
+    // Channels past C (C % 16 != 0) meet zero weights; zero them so stray values cannot
+    // turn into NaN. Then the optional affine + SiLU, one fp16 rounding.
+    const int c = kc * 16 + hf * 8;
+    if (c + 8 > p.C) {
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          if (c + e >= p.C) rb[set][fv][e] = (f16)0;
+    }
+    if (aff || p.silu) {
+      float sc[8], of[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const bool ok = aff && c + e < p.C;
+        sc[e] = ok ? aff[(c + e) * 2] : 1.f;
+        of[e] = ok ? aff[(c + e) * 2 + 1] : 0.f;
+      }
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          float y = (float)rb[set][fv][e] * sc[e] + of[e];
+          if (p.silu) y = silu_f(y);
+          rb[set][fv][e] = c + e < p.C ? (f16)y : (f16)0;
+        }
+    }
+  };
+
+  f32x16 acc[FO][FV];
+#pragma unroll
+  for (int i = 0; i < FO; i++)
+#pragma unroll
+    for (int j = 0; j < FV; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+#pragma unroll
+  for (int j = 0; j < PD - 1; j++)
+    if (j < nk) load(j, j);
+  for (int kc0 = 0; kc0 < nk; kc0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; j++) {
+      const int kc = kc0 + j;
+      if (kc < nk) {
+        if (kc + PD - 1 < nk) load((j + PD - 1) % PD, kc + PD - 1);
+        prep(j, kc);
+#pragma unroll
+        for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+          for (int fv = 0; fv < FV; fv++) acc[fo][fv] = mfma32(ra[j][fo], rb[j][fv], acc[fo][fv]);
+      }
+    }
+  }
+  conv_epilogue<FO, FV>(p, acc, reinterpret_cast<float*>(smem) + wave * 32 * EPW, lane, wv, ob0, b, 0, 0, 0,
+                        0, 0, 0, vb * BV);
 }
 
 // Split-K finish: sum the fp32 partial planes in split order, then the same epilogue
@@ -769,6 +885,12 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   return LDX_OK;
 }
 
+// Pointwise convs with 16-byte-aligned channel groups run as a direct-load GEMM over
+// the flattened volume (dense_kernel).
+static bool use_dense(const ldx_conv3d_args* a, bool vec) {
+  return a->ksize == 1 && vec && (a->c1 == 0 || a->c0 % 16 == 0);
+}
+
 extern "C" size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* a) {
   ConvParams p;
   Tile t;
@@ -776,7 +898,45 @@ extern "C" size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* a) {
   bool vec;
   int64_t ws = 0;
   if (plan_conv(a, p, t, lds, vec, ws) != LDX_OK) return 0;
+  if (use_dense(a, vec)) return 0;
   return (size_t)ws;
+}
+
+template <int WO, int WV, int FO, int FV>
+static int launch_dense(ConvParams p, hipStream_t st) {
+  constexpr int BO = WO * FO * 32, BV = WV * FV * 32;
+  const int NV = p.D * p.H * p.W;
+  p.D = 1; p.H = 1; p.W = NV;
+  p.RD = 1; p.RH = 1; p.RW = NV;
+  p.OD = 1; p.OH = 1; p.OW = NV;
+  p.TD = 1; p.TH = 1; p.TW = BV;
+  p.rTW = 1.0f / (float)BV; p.rTH = 1.0f;
+  p.NBD = 1; p.NBH = 1; p.NBW = (NV + BV - 1) / BV;
+  p.split = 1;
+  p.part = nullptr;
+  const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
+  if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
+  const size_t lds = (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
+  hipLaunchKernelGGL((dense_kernel<WO, WV, FO, FV>), dim3((unsigned)nwg), dim3(256), lds, st, p);
+  return check_launch("conv3d: pointwise");
+}
+
+static int run_dense(const ConvParams& p, hipStream_t st) {
+  const int64_t nv = (int64_t)p.B * p.D * p.H * p.W;
+  int wo = 2, wv = 2, fo = 1, fv = 1;
+  if (p.O <= 32) { wo = 1; wv = 4; fo = 1; fv = 1; }
+  else if (p.O <= 64) { wo = 1; wv = 4; fo = 2; fv = 1; }
+  else if ((nv + 127) / 128 * ((p.O + 127) / 128) >= 256) { fo = 2; fv = 2; }
+  // LDX_DENSE_TILE="WO,WV,FO,FV" overrides the choice (tuning sweeps).
+  if (const char* env = getenv("LDX_DENSE_TILE")) {
+    int a0, a1, a2, a3;
+    if (sscanf(env, "%d,%d,%d,%d", &a0, &a1, &a2, &a3) == 4) { wo = a0; wv = a1; fo = a2; fv = a3; }
+  }
+  if (wo == 1 && wv == 4 && fo == 1 && fv == 1) return launch_dense<1, 4, 1, 1>(p, st);
+  if (wo == 1 && wv == 4 && fo == 2 && fv == 1) return launch_dense<1, 4, 2, 1>(p, st);
+  if (wo == 2 && wv == 2 && fo == 2 && fv == 2) return launch_dense<2, 2, 2, 2>(p, st);
+  if (wo == 1 && wv == 4 && fo == 1 && fv == 2) return launch_dense<1, 4, 1, 2>(p, st);
+  return launch_dense<2, 2, 1, 1>(p, st);
 }
 
 extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
@@ -787,6 +947,7 @@ extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
   int64_t ws = 0;
   int rc = plan_conv(a, p, t, lds, vec, ws);
   if (rc != LDX_OK) return rc;
+  if (use_dense(a, vec)) return run_dense(p, as_stream(stream));
   if (p.split > 1 && (!a->workspace || a->workspace_bytes < (size_t)ws)) {
     // No (or too small a) workspace: one pass over all channels.
     p.split = 1;
