@@ -646,6 +646,144 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
                         0, 0, 0, vb * BV);
 }
 
+// Pointwise conv / dense layer for few output tiles: the 4 waves of a workgroup share
+// one FO x FV block of 32 x 32 output tiles and split its k-steps four ways (a short
+// dependent chain per wave, all of its operands requested up front), then add their
+// partial sums through LDS in a fixed order (waves 1, 2, 3 into wave 0), which finishes
+// the epilogue.
+template <int FO, int FV>
+__global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
+  constexpr int BO = FO * 32, BV = FV * 32;
+  constexpr int PD = 8;                       // k-steps of operands in flight per wave
+  constexpr int EPW = FO * 32 + 4;
+  constexpr int PART = FO * FV * 1024;        // floats of one wave's partial block
+  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hf = lane >> 5;
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+  }
+  const int nob = (p.O + BO - 1) / BO, nvb = p.NBW;
+  const int oblk = wg % nob, vb = (wg / nob) % nvb, b = wg / nob / nvb;
+  const int NV = p.W;
+  const int ob0 = oblk * FO;
+  const int nk = (p.C + 15) / 16;
+  const int nk0 = p.C1 > 0 ? p.C0 / 16 : nk;
+  const int kb = wave * nk / 4, ke = (wave + 1) * nk / 4;   // this wave's k-steps
+
+  const int64_t bvox = (int64_t)b * NV;
+  const auto r0 = make_rsrc(p.x0 + bvox * p.x0p, (unsigned)((int64_t)NV * p.x0p * 2));
+  const auto r1 = p.C1 > 0 ? make_rsrc(p.x1 + bvox * p.x1p, (unsigned)((int64_t)NV * p.x1p * 2)) : r0;
+  unsigned boff0[FV], boff1[FV];
+#pragma unroll
+  for (int fv = 0; fv < FV; fv++) {
+    const int v = min(vb * BV + fv * 32 + (lane & 31), NV - 1);
+    boff0[fv] = (unsigned)(v * p.x0p * 2 + hf * 16);
+    boff1[fv] = (unsigned)(v * p.x1p * 2 + hf * 16);
+  }
+  const auto rw = make_rsrc(p.w, (unsigned)((size_t)p.NOB * p.NKC * 1024));
+  const unsigned aoff = (unsigned)lane * 16u;
+  const float* aff = p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr;
+
+  f16x8 ra[PD][FO], rb[PD][FV];
+  auto load = [&](int set, int kc) {
+#pragma unroll
+    for (int fo = 0; fo < FO; fo++)
+      ra[set][fo] = buffer_load16(rw, aoff, (unsigned)((ob0 + fo) * p.NKC + kc) * 1024u);
+    const bool in0 = kc < nk0;
+#pragma unroll
+    for (int fv = 0; fv < FV; fv++)
+      rb[set][fv] = in0 ? buffer_load16(r0, boff0[fv], (unsigned)kc * 32u)
+                        : buffer_load16(r1, boff1[fv], (unsigned)(kc - nk0) * 32u);
+  };
+  auto prep = [&](int set, int kc) {
+    const int c = kc * 16 + hf * 8;
+    if (c + 8 > p.C) {
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          if (c + e >= p.C) rb[set][fv][e] = (f16)0;
+    }
+    if (aff || p.silu) {
+      float sc[8], of[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        const bool ok = aff && c + e < p.C;
+        sc[e] = ok ? aff[(c + e) * 2] : 1.f;
+        of[e] = ok ? aff[(c + e) * 2 + 1] : 0.f;
+      }
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          float y = (float)rb[set][fv][e] * sc[e] + of[e];
+          if (p.silu) y = silu_f(y);
+          rb[set][fv][e] = c + e < p.C ? (f16)y : (f16)0;
+        }
+    }
+  };
+
+  f32x16 acc[FO][FV];
+#pragma unroll
+  for (int i = 0; i < FO; i++)
+#pragma unroll
+    for (int j = 0; j < FV; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+#pragma unroll
+  for (int j = 0; j < PD - 1; j++)
+    if (kb + j < ke) load(j, kb + j);
+  for (int kc0 = kb; kc0 < ke; kc0 += PD) {
+#pragma unroll
+    for (int j = 0; j < PD; j++) {
+      const int kc = kc0 + j;
+      if (kc < ke) {
+        if (kc + PD - 1 < ke) load((j + PD - 1) % PD, kc + PD - 1);
+        prep(j, kc);
+#pragma unroll
+        for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+          for (int fv = 0; fv < FV; fv++) acc[fo][fv] = mfma32(ra[j][fo], rb[j][fv], acc[fo][fv]);
+      }
+    }
+  }
+
+  // Partial sums of waves 1..3 -> LDS (lane-major), then wave 0 adds them in order.
+  float* red = reinterpret_cast<float*>(smem);
+  if (wave > 0) {
+#pragma unroll
+    for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+          const f32x4 q = {acc[fo][fv][e4 * 4], acc[fo][fv][e4 * 4 + 1], acc[fo][fv][e4 * 4 + 2],
+                           acc[fo][fv][e4 * 4 + 3]};
+          *reinterpret_cast<f32x4*>(red + (wave - 1) * PART + ((fo * FV + fv) * 4 + e4) * 256 + lane * 4) = q;
+        }
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; w++)
+#pragma unroll
+    for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+      for (int fv = 0; fv < FV; fv++)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+          const f32x4 q = *reinterpret_cast<const f32x4*>(red + w * PART + ((fo * FV + fv) * 4 + e4) * 256 + lane * 4);
+#pragma unroll
+          for (int r = 0; r < 4; r++) acc[fo][fv][e4 * 4 + r] += q[r];
+        }
+  conv_epilogue<FO, FV>(p, acc, red + 3 * PART, lane, 0, ob0, b, 0, 0, 0, 0, 0, 0, vb * BV);
+}
+
 // Split-K finish: sum the fp32 partial planes in split order, then the same epilogue
 // as the single-pass kernel (bias, scale, residual, one rounding, optional GELU).
 __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t nvox) {
@@ -921,8 +1059,40 @@ static int launch_dense(ConvParams p, hipStream_t st) {
   return check_launch("conv3d: pointwise");
 }
 
+template <int FO, int FV>
+static int launch_dense_ksplit(ConvParams p, hipStream_t st) {
+  constexpr int BO = FO * 32, BV = FV * 32;
+  const int NV = p.D * p.H * p.W;
+  p.D = 1; p.H = 1; p.W = NV;
+  p.RD = 1; p.RH = 1; p.RW = NV;
+  p.OD = 1; p.OH = 1; p.OW = NV;
+  p.TD = 1; p.TH = 1; p.TW = BV;
+  p.rTW = 1.0f / (float)BV; p.rTH = 1.0f;
+  p.NBD = 1; p.NBH = 1; p.NBW = (NV + BV - 1) / BV;
+  p.split = 1;
+  p.part = nullptr;
+  const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
+  if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
+  const size_t lds = (size_t)(3 * FO * FV * 1024 + 32 * (FO * 32 + 4)) * sizeof(float);
+  hipLaunchKernelGGL((dense_ksplit_kernel<FO, FV>), dim3((unsigned)nwg), dim3(256), lds, st, p);
+  return check_launch("conv3d: pointwise (k-split)");
+}
+
 static int run_dense(const ConvParams& p, hipStream_t st) {
   const int64_t nv = (int64_t)p.B * p.D * p.H * p.W;
+  // Few 64 x 128 output tiles and a long reduction (>= 16 k-steps): one 32 x 32 tile per
+  // workgroup with its k-steps split over the 4 waves (measured on MI355X: 800 x 1024 ->
+  // 256 in 6.7 us instead of 13.9 us).
+  const int64_t tiles64 = (nv + 127) / 128 * ((p.O + 63) / 64);
+  const char* ks_env = getenv("LDX_DENSE_KSPLIT");
+  if (ks_env ? atoi(ks_env) != 0 : (tiles64 < 256 && p.C >= 256)) {
+    int fo = 1, fv = 1;
+    if (const char* env = getenv("LDX_DENSE_KS_TILE")) sscanf(env, "%d,%d", &fo, &fv);
+    if (fo == 1 && fv == 1) return launch_dense_ksplit<1, 1>(p, st);
+    if (fo == 1 && fv == 2) return launch_dense_ksplit<1, 2>(p, st);
+    if (fo == 2 && fv == 1) return launch_dense_ksplit<2, 1>(p, st);
+    return launch_dense_ksplit<2, 2>(p, st);
+  }
   int wo = 2, wv = 2, fo = 1, fv = 1;
   if (p.O <= 32) { wo = 1; wv = 4; fo = 1; fv = 1; }
   else if (p.O <= 64) { wo = 1; wv = 4; fo = 2; fv = 1; }
