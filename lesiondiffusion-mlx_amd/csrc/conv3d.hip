@@ -10,12 +10,14 @@
 // of CC input channels it stages the brick's halo -- the input voxels every tap of
 // every brick voxel reads -- into LDS once, applying the fused GroupNorm affine + SiLU
 // prologue and zero padding on the way (no im2col buffer). The weight fragments of
-// one tap are staged through a two-slot LDS ring, the next tap's loaded into registers
-// while the current tap's MFMAs run. B fragments are read from the halo at a per-lane
-// base plus a workgroup-uniform tap offset. Epilogue: bias (per batch item optional),
-// fp16 shift, output scale, residual, one fp16 rounding, optional GELU / SiLU, NDHWC
-// store with a voxel pitch; or, split over channel chunks, fp32 partial planes that a
-// reduce kernel sums in a fixed order.
+// each tap arrive in a 4-slot LDS ring by direct global->LDS loads issued three taps
+// ahead; the next tap's A and B fragments are read into registers while the current
+// tap's MFMAs run. B fragments are read from the halo at a per-lane base plus a
+// workgroup-uniform tap offset. Epilogue: bias (per batch item optional), fp16 shift,
+// output scale, residual, one fp16 rounding, optional GELU / SiLU, NDHWC store with a
+// voxel pitch; or, split over channel chunks, fp32 partial planes that a reduce kernel
+// sums in a fixed order. Pointwise convs (and dense layers) run as a direct-load GEMM
+// over the flattened volume instead (dense_kernel, dense_ksplit_kernel).
 //
 // Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619):
 // prologue _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421),
