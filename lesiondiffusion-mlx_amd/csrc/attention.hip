@@ -133,8 +133,18 @@ void attention_kernel(AttnParams p) {
   // tile bases and loop conditions in scalar registers.
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hf = lane >> 5, col = lane & 31;
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int q0 = SPLIT == 1 ? blockIdx.x * 128 + wave * 32 : blockIdx.x * 32;
+  // Workgroup -> (query block, head, batch item), query blocks fastest, with the range of
+  // workgroups each XCD receives (they are dealt to the 8 XCDs round-robin) contiguous:
+  // the query blocks of one head then share its K and V in one L2.
+  constexpr int QPW = SPLIT == 1 ? 128 : 32;   // queries per workgroup
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+  }
+  const int nqb = (p.L + QPW - 1) / QPW;
+  const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
+  const int q0 = SPLIT == 1 ? qblk * 128 + wave * 32 : qblk * 32;
   f16* Ks = smem + (SPLIT == 1 ? 0 : wave) * TILE;  // SPLIT > 1: this wave's tile
   const int ltid = SPLIT == 1 ? threadIdx.x : lane;
 
@@ -399,7 +409,9 @@ void attention_kernel(AttnParams p) {
 template <int D, int SPLIT>
 static int launch_attn(const AttnParams& p, hipStream_t st) {
   const int per = SPLIT == 1 ? 128 : 32;
-  dim3 grid((unsigned)((p.L + per - 1) / per), (unsigned)p.H, (unsigned)p.B);
+  const int64_t n = (int64_t)((p.L + per - 1) / per) * p.H * p.B;
+  if (n > 0x7fffffff) return fail("attention: grid too large");
+  dim3 grid((unsigned)n);
   hipLaunchKernelGGL((attention_kernel<D, SPLIT>), grid, dim3(SPLIT == 1 ? 256 : 64 * SPLIT), 0, st, p);
   return check_launch("attention");
 }

@@ -25,6 +25,7 @@
 
 #include "common.h"
 
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -57,6 +58,9 @@ struct ConvParams {
   float scale; int act;
   f16* y; int64_t yp; int yvec;
   int ep_vec;              // 16-byte epilogue accesses: y, residual, shift, bias, partials aligned
+  int nh;                  // planned halo: register slots per thread (0: generic staging loop)
+  int aff_off;             // planned halo with affine: LDS offset (halves) of the (C, 2) affine
+  int stg_off;             // > 0: LDS offset (floats) of the epilogue staging, past the halo
 };
 
 __device__ __forceinline__ float gelu_erf(float v) {
@@ -212,49 +216,70 @@ __device__ __forceinline__ void vmcnt_wait() {
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
 }
 
+// Per-lane epilogue constants. In the epilogue each lane finishes one group of 8 output
+// channels (from 32 * ob_first + 8 * (lane % (4 * FO))) for several voxels; the group's
+// bias and shift are summed here, so a caller can load them before its main loop and
+// keep their latency out of the epilogue.
+struct EpiConst {
+  int o;          // first channel of the lane's group
+  int nch;        // channels of the group inside O (<= 0: none)
+  bool vec8;      // whole group with 16-byte accesses
+  float add8[8];  // bias + shift of the group's channels
+};
+
+template <int FO>
+__device__ __forceinline__ EpiConst epi_const(const ConvParams& p, int lane, int ob_first, int b) {
+  EpiConst e;
+  constexpr int G8 = FO * 4;
+  e.o = ob_first * 32 + (lane % G8) * 8;
+  e.nch = min(8, p.O - e.o);
+  e.vec8 = e.nch == 8 && p.ep_vec;
+#pragma unroll
+  for (int r = 0; r < 8; r++) e.add8[r] = 0.f;
+  const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
+  const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
+  if (e.nch > 0) {
+    if (e.vec8) {
+      if (bias) {
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + e.o);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + e.o + 4);
+#pragma unroll
+        for (int r = 0; r < 4; r++) { e.add8[r] = b0[r]; e.add8[r + 4] = b1[r]; }
+      }
+      if (shb) {
+        const f16x8 s8 = *reinterpret_cast<const f16x8*>(shb + e.o);
+#pragma unroll
+        for (int r = 0; r < 8; r++) e.add8[r] += (float)s8[r];
+      }
+    } else {
+      for (int r = 0; r < e.nch; r++) e.add8[r] = (bias ? bias[e.o + r] : 0.f) + (shb ? (float)shb[e.o + r] : 0.f);
+    }
+  }
+  return e;
+}
+
 // Epilogue of one wave's FO x FV block of 32 x 32 accumulator tiles, through its LDS
 // staging area `stg` (32 x (FO * 32 + 4) floats): voxels of the brick at (d0, h0, w0)
-// (slot (wv * FV + fv) * 32 + v), output channels from 32 * ob_first.
+// (slot (wv * FV + fv) * 32 + v), output channels from 32 * ob_first. Each wave stages
+// one 32-voxel column block at a time (its FO * 32 channels in fp32, voxel-major), then
+// each lane finishes its 8-channel group for 32 * G8 / 64 voxels -- bias and shift (from
+// `ec`), scale, residual, one rounding, activation -- and writes each as one 16-byte
+// store, the lanes of a voxel covering its channels contiguously. Voxel indices are
+// 32-bit (the host bounds B * output voxels below 2^31); the residual rows are all
+// requested before the first is used.
 template <int FO, int FV>
-__device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x16 (&acc)[FO][FV], float* stg, int lane,
-                                              int wv, int ob_first, int b, int sidx, int pd, int ph, int pw,
-                                              int d0, int h0, int w0) {
+__device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiConst& ec, f32x16 (&acc)[FO][FV],
+                                              float* stg, int lane, int wv, int b, int sidx, int pd, int ph,
+                                              int pw, int d0, int h0, int w0) {
   constexpr int EPW = FO * 32 + 4;   // staging pitch (floats): conflict-free both ways
-  // Epilogue through LDS: each wave stages one 32-voxel column block at a time (its
-  // FO * 32 channels in fp32, voxel-major), then each lane finishes 8 channels of
-  // 32 * G8 / 64 voxels -- bias, shift, scale, residual, one rounding, activation -- and
-  // writes each as one 16-byte store, the lanes of a voxel covering its channels
-  // contiguously. A lane's channel group is the same for every voxel it finishes, so
-  // its bias and shift are loaded once; the residual rows are all requested before the
-  // first is used.
   constexpr int G8 = FO * 4;         // 8-channel groups per voxel (divides 64)
   constexpr int NI = 32 * G8 / 64;   // voxels per lane per column block
   const int col = lane & 31, hf = lane >> 5;
   const int g = lane % G8;
-  const int o = ob_first * 32 + g * 8;
-  const int nch = min(8, p.O - o);   // channels of this lane's group (<= 0: none)
-  const bool vec8 = nch == 8 && p.ep_vec;
-  const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
-  const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
-  const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
-  float add8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // bias + shift
-  if (nch > 0) {
-    if (vec8) {
-      if (bias) {
-        const f32x4 b0 = *reinterpret_cast<const f32x4*>(bias + o);
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(bias + o + 4);
-#pragma unroll
-        for (int r = 0; r < 4; r++) { add8[r] = b0[r]; add8[r + 4] = b1[r]; }
-      }
-      if (shb) {
-        const f16x8 s8 = *reinterpret_cast<const f16x8*>(shb + o);
-#pragma unroll
-        for (int r = 0; r < 8; r++) add8[r] += (float)s8[r];
-      }
-    } else {
-      for (int r = 0; r < nch; r++) add8[r] = (bias ? bias[o + r] : 0.f) + (shb ? (float)shb[o + r] : 0.f);
-    }
-  }
+  const int o = ec.o, nch = ec.nch;
+  const bool vec8 = ec.vec8;
+  const int ovol = p.OD * p.OH * p.OW;
+  const bool pref_res = p.res && vec8 && p.split == 1;
   // One copy of the store loop per activation: no per-element branch on it.
   auto finish = [&](auto act_c) {
   constexpr int ACT = decltype(act_c)::value;
@@ -269,7 +294,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x16 (&acc)
         *reinterpret_cast<f32x4*>(stg + col * EPW + fo * 32 + j * 8 + 4 * hf) = q;
       }
     __builtin_amdgcn_wave_barrier();  // (LDS operations of a wave complete in order)
-    int64_t ov[NI];
+    int ov[NI];
     bool ok[NI];
     f16x8 re8[NI];
 #pragma unroll
@@ -281,41 +306,52 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, f32x16 (&acc)
       const int rd = d0 + vd, rh = h0 + vh, rw = w0 + vw;
       ok[i] = nch > 0 && vd < p.TD && rd < p.RD && rh < p.RH && rw < p.RW;
       if (p.upsample)
-        ov[i] = ((int64_t)(2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
+        ov[i] = ((2 * rd + pd) * p.OH + (2 * rh + ph)) * p.OW + 2 * rw + pw;
       else
-        ov[i] = ((int64_t)rd * p.OH + rh) * p.OW + rw;
-      ov[i] += (int64_t)b * ovol;
-      re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (ok[i] && p.res && vec8 && p.split == 1) re8[i] = *reinterpret_cast<const f16x8*>(p.res + ov[i] * p.resp + o);
+        ov[i] = (rd * p.OH + rh) * p.OW + rw;
+      ov[i] += b * ovol;
+    }
+    if (pref_res) {
+#pragma unroll
+      for (int i = 0; i < NI; i++)
+        re8[i] = ok[i] ? *reinterpret_cast<const f16x8*>(p.res + (int64_t)ov[i] * p.resp + o)
+                       : (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    } else {
+#pragma unroll
+      for (int i = 0; i < NI; i++) re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    f32x4 lo[NI], hi[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int v = lane / G8 + i * (64 / G8);
+      lo[i] = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
+      hi[i] = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
     }
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       if (!ok[i]) continue;
-      const int v = lane / G8 + i * (64 / G8);
-      const f32x4 lo = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
-      const f32x4 hi = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
-      const float r8[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      const float r8[8] = {lo[i][0], lo[i][1], lo[i][2], lo[i][3], hi[i][0], hi[i][1], hi[i][2], hi[i][3]};
       if (p.split > 1) {
         // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
         float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov[i]) * p.O + o;
         if (vec8) {
-          *reinterpret_cast<f32x4*>(prow) = lo;
-          *reinterpret_cast<f32x4*>(prow + 4) = hi;
+          *reinterpret_cast<f32x4*>(prow) = lo[i];
+          *reinterpret_cast<f32x4*>(prow + 4) = hi[i];
         } else {
           for (int r = 0; r < nch; r++) prow[r] = r8[r];
         }
         continue;
       }
-      f16* yrow = p.y + ov[i] * p.yp + o;
+      f16* yrow = p.y + (int64_t)ov[i] * p.yp + o;
       if (vec8) {
         f16x8 out;
 #pragma unroll
-        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + add8[r]) * p.scale + (float)re8[i][r]));
+        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + ec.add8[r]) * p.scale + (float)re8[i][r]));
         *reinterpret_cast<f16x8*>(yrow) = out;
       } else {
-        const f16* rrow = p.res ? p.res + ov[i] * p.resp + o : nullptr;
+        const f16* rrow = p.res ? p.res + (int64_t)ov[i] * p.resp + o : nullptr;
         for (int r = 0; r < nch; r++) {
-          float t = (r8[r] + add8[r]) * p.scale;
+          float t = (r8[r] + ec.add8[r]) * p.scale;
           if (rrow) t += (float)rrow[r];
           yrow[r] = post_act_t<ACT>((f16)t);
         }
@@ -346,6 +382,12 @@ __device__ __forceinline__ void interleave_reads_mfma() {
   }
 }
 
+// Halo slots per thread held in registers on the planned halo path: a thread's halo
+// voxels (tid / G + j * VPI) are the same for every channel chunk, so their source voxel
+// indices and LDS offsets are computed once per workgroup, and the next chunk's halo can
+// be loaded into registers while the current chunk's taps run.
+constexpr int NHMAX = 8;
+
 template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, int KSPL>
 __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   constexpr int NT = 256 * KSPL;
@@ -358,6 +400,11 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   constexpr int NFRAG = (BO / 32) * KSG;      // 1 KB weight fragments per group stage
   constexpr int WSTAGE = NFRAG * 512;         // halves per group stage
   constexpr int LW = (NFRAG + 3) / 4;         // weight DMAs per wave per stage
+  constexpr int G = CC / 8;                   // 16-byte channel groups per voxel
+  constexpr int VPI = NT / G;                 // halo voxels per pass of the workgroup
+  // Tap of each chunk after whose weight load the next chunk's halo is requested: the
+  // loads then have the last WPF - 1 taps of the chunk to land.
+  constexpr int TPF = TAPS - WPF;
   extern __shared__ __attribute__((aligned(16))) f16 smem[];
   f16* halo = smem + KSPL * WRING * WSTAGE;
 
@@ -389,6 +436,9 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   const int s = p.stride;
   const int gd0 = d0 * s + p.ID0, gh0 = h0 * s + p.IH0, gw0 = w0 * s + p.IW0;
   const int kq = 8 * (lane >> 5) + kg * KSG * 16;
+  const int ob0 = oblk * (BO / 32);
+  // The epilogue's bias and shift, requested now so the main loop hides their latency.
+  const EpiConst ec = epi_const<FO>(p, lane, ob0 + wo * FO, b);
 
   // Per-lane B-operand (voxel) bases in the halo.
   int lbase[FV];
@@ -407,7 +457,6 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   // (f / KSG, f % KSG)): one 1 KB fragment is one 16-byte-per-lane load, already in MFMA
   // lane order. A wave with fewer real fragments repeats one (same data to the same
   // place), so every wave issues LW loads per stage and the vmcnt wait is uniform.
-  const int ob0 = oblk * (BO / 32);
   const int c_begin = sidx * p.cps * CC;
   const int c_end = min(p.C, (sidx + 1) * p.cps * CC);
   const int nst = (c_end - c_begin + CC - 1) / CC * TAPS;
@@ -430,6 +479,96 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
     if (nleft > 0) {
       nleft--;
       if (++ntap == TAPS) { ntap = 0; nkc += KS; }
+    }
+  };
+
+  // Planned halo (16-byte channel groups and at most NHMAX slots per thread): per slot
+  // the source voxel index within the batch item (~0u outside the volume) and the LDS
+  // offset in halves (-1 past the halo).
+  const bool planned = VEC && p.nh > 0;
+  const bool xf = p.affine != nullptr || p.silu;
+  const int cg = tid % G;
+  unsigned hvi[NHMAX];
+  int hlo[NHMAX];
+  f16x8 hval[NHMAX];
+  const float* aff_s = reinterpret_cast<const float*>(smem + p.aff_off);  // (C, 2) of batch item b
+  if constexpr (VEC) {
+    if (planned) {
+      const int hvox = p.HD * p.HH * p.HW;
+#pragma unroll
+      for (int j = 0; j < NHMAX; j++) {
+        const int vox = tid / G + j * VPI;
+        const int t = fdiv(vox, p.rHW);
+        const int hw = vox - t * p.HW;
+        const int hd = fdiv(t, p.rHH);
+        const int hh = t - hd * p.HH;
+        const int id = gd0 + hd, ih = gh0 + hh, iw = gw0 + hw;
+        const bool in = vox < hvox && id >= 0 && id < p.D && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+        hvi[j] = in ? (unsigned)((id * p.H + ih) * p.W + iw) : ~0u;
+        hlo[j] = vox < hvox ? t * p.RS + hw * PITCH + cg * 8 : -1;
+      }
+      if (p.affine) {
+        // The affine of this batch item, (C, 2) fp32, into LDS once.
+        const float* ap = p.affine + (int64_t)b * p.C * 2;
+        float* as = reinterpret_cast<float*>(smem + p.aff_off);
+        for (int i = tid; i < p.C * 2; i += NT) as[i] = ap[i];
+      }
+    }
+  }
+  // Request the halo of channels [c0, c0 + CC) into hval: exactly NHMAX loads per thread
+  // (padding voxels, channels past C and unused slots read zeros through the buffer
+  // resource's range check).
+  auto halo_issue = [&](int c0) {
+    if constexpr (VEC) {
+      const bool in0 = c0 < p.C0;
+      const int64_t vol = (int64_t)p.D * p.H * p.W;
+      const f16* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
+      const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
+      const auto rs = make_rsrc(base, (unsigned)(vol * pitch2));
+      const int c = c0 + cg * 8;
+      const bool cval = c < p.C;
+      const unsigned cofs = (unsigned)((in0 ? c : c - p.C0) * 2);
+#pragma unroll
+      for (int j = 0; j < NHMAX; j++) {
+        const unsigned off = (hvi[j] != ~0u && cval) ? hvi[j] * pitch2 + cofs : 0xfffffff0u;
+        hval[j] = buffer_load16(rs, off);
+      }
+    }
+  };
+  // Write hval to the halo, with the affine + SiLU prologue and one fp16 rounding;
+  // padding voxels and channels past C stay zero.
+  auto halo_store = [&](int c0) {
+    if constexpr (VEC) {
+      const int c = c0 + cg * 8;
+      const bool cval = c < p.C;
+      float sc[8], of[8];
+      if (xf) {
+        if (p.affine && cval) {
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const f32x4 a4 = *reinterpret_cast<const f32x4*>(aff_s + c * 2 + q * 4);
+            sc[2 * q] = a4[0]; of[2 * q] = a4[1]; sc[2 * q + 1] = a4[2]; of[2 * q + 1] = a4[3];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; e++) { sc[e] = 1.f; of[e] = 0.f; }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < NHMAX; j++) {
+        if (hlo[j] < 0) continue;
+        f16x8 v = hval[j];
+        if (xf) {
+          const bool ok = cval && hvi[j] != ~0u;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            float yv = (float)v[e] * sc[e] + of[e];
+            if (p.silu) yv = silu_f(yv);
+            v[e] = ok ? (f16)yv : (f16)0;
+          }
+        }
+        *reinterpret_cast<f16x8*>(halo + hlo[j]) = v;
+      }
     }
   };
 
@@ -473,35 +612,57 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   };
 
   int st = 0;
+  bool pf = false;   // the current chunk's halo is already in hval
   for (int c0 = c_begin; c0 < c_end; c0 += CC) {
-    __syncthreads();  // previous chunk done with the halo
-    load_halo<CC, VEC, NT>(p, halo, b, c0, gd0, gh0, gw0);
-    // Every halo load -- and with them the weight stages issued so far -- has landed;
-    // saying so also clears the compiler's view of pending loads, which would otherwise
-    // drain the weight prefetch at every tap.
-    vmcnt_wait<0>();
+    if (planned) {
+      if (pf) {
+        // Requested during the previous chunk's last taps; younger than them are only
+        // the weight stages of its last WPF - 1 taps.
+        vmcnt_wait<(WPF - 1) * LW>();
+        __syncthreads();  // previous chunk done with the halo
+      } else {
+        halo_issue(c0);
+        // Every halo load -- and with them the weight stages issued so far -- has
+        // landed; saying so also clears the compiler's view of pending loads, which
+        // would otherwise drain the weight prefetch at every tap.
+        vmcnt_wait<0>();
+        __syncthreads();  // previous chunk done with the halo; the affine in LDS
+      }
+      halo_store(c0);
+    } else {
+      __syncthreads();  // previous chunk done with the halo
+      load_halo<CC, VEC, NT>(p, halo, b, c0, gd0, gh0, gw0);
+      vmcnt_wait<0>();
+    }
     __syncthreads();
+    // Prefetch the next chunk's halo during this chunk's last taps.
+    const bool pf_next = planned && TPF > 0 && c0 + CC < c_end;
     load_frags(0, st, 0);
 #pragma unroll
     for (int tap = 0; tap < TAPS; tap++, st++) {
-      // Stage st + 1 has landed once only stage st + 2's loads may be pending; the
-      // barrier publishes every wave's part of it and retires stage st - 1 (read into
-      // registers two taps ago), whose slot the next load reuses.
-      vmcnt_wait<LW>();
+      // Stage st + 1 has landed once only the WPF - 2 stages after it (and, after TPF,
+      // the next chunk's halo loads) may be pending; the barrier publishes every wave's
+      // part of it and retires stage st - 1 (read into registers two taps ago), whose
+      // slot the next load reuses.
+      if (tap > TPF && pf_next) vmcnt_wait<(WPF - 2) * LW + NHMAX>();
+      else vmcnt_wait<(WPF - 2) * LW>();
       __syncthreads();
       issue_stage((st + WPF) % WRING);
+      if (tap == TPF && pf_next) halo_issue(c0 + CC);
       if (tap + 1 < TAPS) load_frags((tap + 1) & 1, st + 1, tap + 1);
       mfma_frags(tap & 1);
       if (tap + 1 < TAPS) interleave_reads_mfma<(FO + FV) * KSG, FO * FV * KSG>();
     }
+    pf = pf_next;
   }
-  // Drain the trailing (repeated) weight loads before the LDS is reused.
+  // Drain the trailing (repeated) weight loads before the LDS is reused or released.
   vmcnt_wait<0>();
-  __syncthreads();  // every wave is done with the halo and the weight rings
 
   constexpr int EPW = FO * 32 + 4;   // epilogue staging pitch (floats)
   constexpr int RED = 4 * FO * FV * 1024;  // floats of the K-group reduction buffer
+  float* stg;
   if constexpr (KSPL == 2) {
+    __syncthreads();  // every wave is done with the halo and the weight rings
     // Group 1 hands its partial sums to group 0 (same wave slot, lane-major layout).
     float* red = reinterpret_cast<float*>(smem) + w4 * (FO * FV * 1024);
     if (kg == 1) {
@@ -528,10 +689,17 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
 #pragma unroll
           for (int r = 0; r < 4; r++) acc[fo][fv][e4 * 4 + r] += q[r];
         }
+    stg = reinterpret_cast<float*>(smem) + RED + w4 * 32 * EPW;
+  } else {
+    if (p.stg_off > 0) {
+      // A staging area of its own past the halo: no wait for the other waves.
+      stg = reinterpret_cast<float*>(smem) + p.stg_off + w4 * 32 * EPW;
+    } else {
+      __syncthreads();  // every wave is done with the halo and the weight rings
+      stg = reinterpret_cast<float*>(smem) + w4 * 32 * EPW;
+    }
   }
-
-  conv_epilogue<FO, FV>(p, acc, reinterpret_cast<float*>(smem) + (KSPL == 2 ? RED : 0) + w4 * 32 * EPW, lane, wv,
-                        ob0 + wo * FO, b, sidx, pd, ph, pw, d0, h0, w0);
+  conv_epilogue<FO, FV>(p, ec, acc, stg, lane, wv, b, sidx, pd, ph, pw, d0, h0, w0);
 }
 
 // Pointwise conv / dense layer: a GEMM whose operands both come straight from global
@@ -577,6 +745,7 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
   const auto rw = make_rsrc(p.w, (unsigned)((size_t)p.NOB * p.NKC * 1024));
   const unsigned aoff = (unsigned)lane * 16u;
   const float* aff = p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr;
+  const EpiConst ec = epi_const<FO>(p, lane, ob0, b);
 
   f16x8 ra[PD][FO], rb[PD][FV];
   auto load = [&](int set, int kc) {
@@ -644,7 +813,7 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
       }
     }
   }
-  conv_epilogue<FO, FV>(p, acc, reinterpret_cast<float*>(smem) + wave * 32 * EPW, lane, wv, ob0, b, 0, 0, 0,
+  conv_epilogue<FO, FV>(p, ec, acc, reinterpret_cast<float*>(smem) + wave * 32 * EPW, lane, wv, b, 0, 0, 0,
                         0, 0, 0, vb * BV);
 }
 
@@ -689,6 +858,7 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
   const auto rw = make_rsrc(p.w, (unsigned)((size_t)p.NOB * p.NKC * 1024));
   const unsigned aoff = (unsigned)lane * 16u;
   const float* aff = p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr;
+  const EpiConst ec = epi_const<FO>(p, lane, ob0, b);
 
   f16x8 ra[PD][FO], rb[PD][FV];
   auto load = [&](int set, int kc) {
@@ -783,7 +953,7 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
 #pragma unroll
           for (int r = 0; r < 4; r++) acc[fo][fv][e4 * 4 + r] += q[r];
         }
-  conv_epilogue<FO, FV>(p, acc, red + 3 * PART, lane, 0, ob0, b, 0, 0, 0, 0, 0, 0, vb * BV);
+  conv_epilogue<FO, FV>(p, ec, acc, red + 3 * PART, lane, 0, b, 0, 0, 0, 0, 0, 0, vb * BV);
 }
 
 // Split-K finish: sum the fp32 partial planes in split order, then the same epilogue
@@ -841,13 +1011,38 @@ static void pick_brick(const ConvParams& p, int BV, int s, int ks, int& TD, int&
 }
 
 template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, int KSPL>
-static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t lds) {
+static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t halo_bytes) {
   constexpr int BO = WO * FO * 32;
-  lds += (size_t)WRING * (BO / 32) * (CC / 16) * 512 * sizeof(f16);  // weight rings (all groups)
-  // End phase: K-group partial sums, then the epilogue staging.
-  const size_t tail = (size_t)(KSPL == 2 ? 4 * FO * FV * 1024 : 0) * sizeof(float) +
-                      (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
-  if (lds < tail) lds = tail;
+  constexpr int NT = 256 * KSPL, VPI = NT / (CC / 8);
+  auto al16 = [](size_t n) { return (n + 15) & ~(size_t)15; };
+  // LDS: weight rings (all K-groups), the halo, and with a planned halo and an affine the
+  // (C, 2) fp32 affine; then the epilogue (K-group partial sums and the staging).
+  const size_t ring = (size_t)WRING * (BO / 32) * (CC / 16) * 1024;
+  size_t main_bytes = ring + al16(halo_bytes);
+  const int hvox = p.HD * p.HH * p.HW;
+  p.nh = VEC ? (hvox + VPI - 1) / VPI : 0;
+  if (p.nh > NHMAX) p.nh = 0;
+  p.aff_off = 0;
+  if (p.nh > 0 && p.affine) {
+    p.aff_off = (int)(main_bytes / sizeof(f16));
+    main_bytes += al16((size_t)p.C * 2 * sizeof(float));
+  }
+  const size_t stg = (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
+  size_t lds;
+  p.stg_off = 0;
+  if constexpr (KSPL == 2) {
+    lds = std::max(main_bytes, (size_t)4 * FO * FV * 1024 * sizeof(float) + stg);
+  } else {
+    // The staging gets an area of its own (no barrier before the epilogue) unless that
+    // costs a workgroup per CU.
+    const size_t overlap = std::max(main_bytes, stg), sep = main_bytes + stg;
+    if (sep <= 160 * 1024 && (160 * 1024) / sep >= (160 * 1024) / overlap) {
+      p.stg_off = (int)(main_bytes / sizeof(float));
+      lds = sep;
+    } else {
+      lds = overlap;
+    }
+  }
   if (lds > 160 * 1024) return fail("conv3d: %zu bytes of LDS needed", lds);
   const int64_t nwg = (int64_t)p.NBD * p.NBH * p.NBW * ((p.O + BO - 1) / BO) * grid_z;
   if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
@@ -949,7 +1144,7 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   if (p.O <= 32) t = {1, 4, 1, 2, 32};
   else if (p.O <= 64) t = {1, 4, 2, 1, 32};
   else if (rows / 256 * ((p.O + 63) / 64) >= 512) t = {1, 4, 2, 2, 32};
-  else t = {2, 2, 1, 1, 32};
+  else t = {2, 2, 1, 1, vec && p.taps > 1 && p.C % 64 == 0 ? 64 : 32};  // small volumes: 64-channel chunks
   // LDX_CONV_TILE="WO,WV,FO,FV,CC" overrides the tile heuristic (tuning sweeps).
   bool forced = false;
   if (const char* env = getenv("LDX_CONV_TILE")) {
@@ -1022,6 +1217,7 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   const int64_t nvox = (int64_t)p.B * p.OD * p.OH * p.OW;
   ws_bytes = p.split > 1 ? (int64_t)p.split * nvox * p.O * (int64_t)sizeof(float) : 0;
   if ((int64_t)p.B * (p.upsample ? 8 : 1) * p.split > 65535) return fail("conv3d: batch too large");
+  if ((int64_t)p.B * p.OD * p.OH * p.OW >= ((int64_t)1 << 31)) return fail("conv3d: output too large");
   return LDX_OK;
 }
 
