@@ -16,6 +16,12 @@
 // SPLIT = 4 / 8: the waves own the same 32 queries and take interleaved key blocks with
 // private tiles; their (max, sum, O) states merge through LDS at the end -- more waves
 // for short sequences (1,600 tokens x 8 heads is only 400 query blocks).
+// attention_pipe_kernel (long key sequences, head width 32 or 64): the four-way split
+// with tiles moved global->LDS by DMA and the S^T MFMAs of the next block issued ahead
+// of the current block's softmax. Its exponent base moves only when a block raises a
+// query's maximum by more than 8 (log2 units), so probabilities lie in [0, 2^8] rather
+// than [0, 1]: the same fp16 relative rounding, with the accumulator rescale skipped on
+// most blocks.
 //
 // Reference semantics: flash_attention_half (src/lesiondiffusion_mlx/_attention_half.py:
 // 23-114): scores scaled by scale*log2(e) in fp32 (:70-72), exp2 online softmax
@@ -406,6 +412,316 @@ void attention_kernel(AttnParams p) {
   }
 }
 
+// Buffer resource (gfx9 descriptor: base, stride 0, num_records = bytes, the raw-buffer
+// flags of make_rsrc) as four scalars, for the asm DMA below.
+__device__ __forceinline__ i32x4 dma_rsrc(const void* base, unsigned bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32) & 0xffff);
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from a buffer (byte offset voff + soff; out of range reads zeros)
+// straight into LDS at lds + 16 * lane. Asm for the same reason as dma_b128: completion
+// is awaited with explicit vmcnt waits.
+__device__ __forceinline__ void dma_buffer_b128(i32x4 rs, unsigned voff, unsigned soff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs),
+               "s"(soff), "s"(lds)
+               : "memory");
+}
+
+// Key-split kernel with tiles moved by DMA and a software-pipelined block loop: a
+// workgroup's SPLIT waves own the same 32 * QB queries and take interleaved 32-key blocks
+// (block SPLIT * i + wave). Each wave has private tile buffers in LDS -- K three deep, V
+// two deep -- that direct global->LDS loads fill, so no register holds a tile in transit
+// and the S^T MFMAs of block it + 1 are issued before the softmax and P V of block it,
+// whose VALU work then runs under them. Tile rows are D halves without padding; 16-byte
+// chunk c of row r sits at chunk position c ^ (r mod KG) (KG = D / 8 chunks per row),
+// which spreads both the K-fragment reads and the transposing V reads over the banks. K
+// rows are permuted by key_row as in attention_kernel; the loads go through buffer
+// resources that end at the last key, so rows past the sequence read zeros (probability
+// zero).
+template <int D, int QB, int SPLIT>
+struct AttnPipeLds {
+  static constexpr int HT = 32 * D;                              // halves per K or V tile
+  static constexpr int MERGE = SPLIT * QB * (D * 32 + 64);       // floats for the merge
+  static constexpr size_t bytes = (size_t)(SPLIT * 5 * HT * 2 > MERGE * 4 ? SPLIT * 5 * HT * 2 : MERGE * 4);
+};
+
+template <int D, int QB, int SPLIT>
+__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 8)))
+void attention_pipe_kernel(AttnParams p) {
+  constexpr int NT = 64 * SPLIT;
+  constexpr int KB = 32;
+  constexpr int DK = D / 16, DB = D / 32, KG = D / 8;
+  constexpr int HT = AttnPipeLds<D, QB, SPLIT>::HT;
+  constexpr int NH = HT * 2 / 1024;           // 1 KB DMA instructions per K or V tile
+  constexpr int RPD = 1024 / (D * 2);
+  static_assert(D == 32 || D == 64, "DMA tiles for head widths 32 and 64");
+  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hf = lane >> 5, col = lane & 31;
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+  }
+  const int nqb = (p.L + 32 * QB - 1) / (32 * QB);
+  const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
+  const int q0 = qblk * 32 * QB;
+  f16* kbuf = smem + wave * 5 * HT;           // three K tiles, then two V tiles
+  f16* vbuf = kbuf + 3 * HT;
+  const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
+
+  const f16* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
+  const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
+  const f16* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+
+  int qi[QB];
+  const float* mrow[QB];
+#pragma unroll
+  for (int j = 0; j < QB; j++) {
+    qi[j] = min(q0 + 32 * j + col, p.L - 1);
+    mrow[j] = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi[j] * p.ms2 : nullptr;
+  }
+  f32x16 o[QB][DB];
+#pragma unroll
+  for (int j = 0; j < QB; j++)
+#pragma unroll
+    for (int i = 0; i < DB; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) o[j][i][e] = 0.f;
+  float m[QB], l[QB];
+#pragma unroll
+  for (int j = 0; j < QB; j++) { m[j] = -INFINITY; l[j] = 0.f; }
+
+  unsigned koff[NH], voff[NH];
+#pragma unroll
+  for (int j = 0; j < NH; j++) {
+    const int R = j * RPD + lane / KG, c = (lane % KG) ^ (R % KG);
+    koff[j] = (unsigned)(key_row(R) * p.ks1 + c * 8) * 2u;
+    voff[j] = (unsigned)(R * p.vs1 + c * 8) * 2u;
+  }
+  const i32x4 krs = dma_rsrc(kb_, (unsigned)(((int64_t)(p.LK - 1) * p.ks1 + D) * 2));
+  const i32x4 vrs = dma_rsrc(vb_, (unsigned)(((int64_t)(p.LK - 1) * p.vs1 + D) * 2));
+  const int nblk = (p.LK + KB - 1) / KB;
+  const int nit = (nblk - wave + SPLIT - 1) / SPLIT;   // this wave's blocks: wave + SPLIT * it
+  // Tiles past this wave's blocks are loaded too (their rows lie past the sequence and
+  // read zeros), so every pipeline step issues the same number of loads.
+  auto issue_k = [&](int it) {
+    const unsigned ks = (unsigned)((wave + SPLIT * it) * KB * p.ks1) * 2u;
+    const unsigned dst = kbuf_lds + (unsigned)((it % 3) * HT * 2);
+#pragma unroll
+    for (int j = 0; j < NH; j++) dma_buffer_b128(krs, koff[j], ks, dst + j * 1024);
+  };
+  auto issue_v = [&](int it) {
+    const unsigned vs = (unsigned)((wave + SPLIT * it) * KB * p.vs1) * 2u;
+    const unsigned dst = vbuf_lds + (unsigned)((it & 1) * HT * 2);
+#pragma unroll
+    for (int j = 0; j < NH; j++) dma_buffer_b128(vrs, voff[j], vs, dst + j * 1024);
+  };
+  const int vr0 = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int vd0 = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  auto vaddr = [&](int r, int d) { return r * D + (((d >> 3) ^ (r % KG)) << 3) + (d & 7); };
+
+  f16x8 qf[QB][DK];
+  // S^T = K Q^T of block it (rows = keys permuted by key_row, columns = queries).
+  auto compute_s = [&](int it, f32x16 (&s)[QB]) {
+    const f16* Kc = kbuf + (it % 3) * HT;
+#pragma unroll
+    for (int j = 0; j < QB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) s[j][e] = 0.f;
+#pragma unroll
+    for (int dk = 0; dk < DK; dk++) {
+      const int c = 2 * dk + hf;
+      const f16x8 kf = *reinterpret_cast<const f16x8*>(Kc + col * D + ((c ^ (col % KG)) << 3));
+#pragma unroll
+      for (int j = 0; j < QB; j++) s[j] = mfma32x(kf, qf[j][dk], s[j]);
+    }
+  };
+  const f16x2 ones = {(f16)1, (f16)1};
+  // V^T read addresses (halves, in the first V buffer; the second is HT further).
+  int va[2][DB][2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+    for (int db = 0; db < DB; db++) {
+      va[ks][db][0] = vaddr(vr0 + ks * 16, vd0 + db * 32);
+      va[ks][db][1] = vaddr(vr0 + ks * 16 + 4, vd0 + db * 32);
+    }
+  // Online softmax of block it and O^T += V^T P^T. The exponent base m of a query moves
+  // only when the block's maximum exceeds it by more than RB (log2 units): probabilities
+  // then stay below 2^RB (fp16-safe), and the accumulator rescale -- 16 multiplies per
+  // O^T block -- is skipped for all but the few blocks that raise the maximum that much.
+  constexpr float RB = 8.f;
+  auto softmax_pv = [&](int it, auto vpar_c, f32x16 (&s)[QB]) {
+    constexpr int VP = decltype(vpar_c)::value;
+    const int kbase = (wave + SPLIT * it) * KB;
+    const f16* Vc = vbuf + VP * HT;
+    f16x8 pf[QB][2];
+    float alpha[QB];
+    const bool full = kbase + KB <= p.LK && !p.mask;
+#pragma unroll
+    for (int j = 0; j < QB; j++) {
+      float top;
+      if (full) {
+        top = __builtin_amdgcn_fmed3f(s[j][0], s[j][1], INFINITY);
+#pragma unroll
+        for (int e = 2; e < 16; e++) top = __builtin_amdgcn_fmed3f(top, s[j][e], INFINITY);
+        top = halves_max(top) * p.c;
+      } else {
+        top = -INFINITY;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
+          float t = s[j][e] * p.c;
+          if (key >= p.LK) t = -INFINITY;
+          else if (mrow[j]) t += mrow[j][(int64_t)key * p.ms3] * 1.44269504088896341f;
+          s[j][e] = t;
+          top = fmaxf(top, t);
+        }
+        top = halves_max(top);
+      }
+      // A query with every key so far removed keeps m = -inf and contributes nothing.
+      const float mn = top > m[j] + RB ? top : m[j];
+      const float base = mn == -INFINITY ? 0.f : mn;
+      alpha[j] = __builtin_amdgcn_exp2f(m[j] - base);
+      m[j] = mn;
+      if (full) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) s[j][e] = s[j][e] * p.c - base;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 16; e++) s[j][e] -= base;
+      }
+      float sum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const f16x2 pr = {(f16)__builtin_amdgcn_exp2f(s[j][e]), (f16)__builtin_amdgcn_exp2f(s[j][e + 1])};
+        pf[j][e >> 3][e & 7] = pr[0];
+        pf[j][e >> 3][(e & 7) + 1] = pr[1];
+        sum = __builtin_amdgcn_fdot2(pr, ones, sum, false);
+      }
+      l[j] = l[j] * alpha[j] + sum;
+    }
+#pragma unroll
+    for (int j = 0; j < QB; j++) {
+      if (__ballot(alpha[j] != 1.f)) {
+#pragma unroll
+        for (int db = 0; db < DB; db++) scale_in_place(o[j][db], alpha[j]);
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+      for (int db = 0; db < DB; db++) {
+        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][0]));
+        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][1]));
+        const f16x8 vf = __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+#pragma unroll
+        for (int j = 0; j < QB; j++) o[j][db] = mfma32x(vf, pf[j][ks], o[j][db]);
+      }
+    }
+  };
+  // One pipeline step: S of block it + 1 goes to the MFMA unit, then block it's softmax
+  // and P V; then V(it + 2) refills the V buffer just read and K(it + 3) the K buffer
+  // read one step ago. VP = it % 2 (the loop runs two steps per iteration).
+  auto step = [&](int it, auto vpar_c, f32x16 (&cur)[QB], f32x16 (&nxt)[QB]) {
+    // K(it + 1) and V(it) have landed once only the previous step's loads may be pending.
+    vmcnt_wait<2 * NH>();
+    if (it + 1 < nit) compute_s(it + 1, nxt);
+    softmax_pv(it, vpar_c, cur);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's V reads have returned
+    issue_v(it + 2);
+    issue_k(it + 3);
+  };
+
+  issue_k(0); issue_v(0); issue_k(1); issue_v(1); issue_k(2);
+#pragma unroll
+  for (int j = 0; j < QB; j++)
+#pragma unroll
+    for (int dk = 0; dk < DK; dk++)
+      qf[j][dk] = *reinterpret_cast<const f16x8*>(qb_ + (int64_t)qi[j] * p.qs1 + dk * 16 + 8 * hf);
+  vmcnt_wait<0>();
+  f32x16 sa[QB], sb[QB];
+  if (nit > 0) compute_s(0, sa);
+  for (int it = 0; it < nit; it += 2) {
+    step(it, std::integral_constant<int, 0>(), sa, sb);
+    if (it + 1 < nit) step(it + 1, std::integral_constant<int, 1>(), sb, sa);
+  }
+
+  f16* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
+  float* mo = reinterpret_cast<float*>(smem);            // [QB][SPLIT][D][32] partial O^T
+  float* ml = mo + QB * SPLIT * D * 32;                   // [QB][SPLIT][32] m, then l
+  vmcnt_wait<0>();
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < QB; j++) {
+    const float lj = halves_sum(l[j]);
+#pragma unroll
+    for (int db = 0; db < DB; db++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int d = db * 32 + (e >> 2) * 8 + 4 * hf + (e & 3);
+        mo[((j * SPLIT + wave) * D + d) * 32 + col] = o[j][db][e];
+      }
+    if (hf == 0) {
+      ml[(j * SPLIT + wave) * 32 + col] = m[j];
+      ml[QB * SPLIT * 32 + (j * SPLIT + wave) * 32 + col] = lj;
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < QB * 32 * (D / 4); idx += NT) {
+    const int qq = idx & 31, d4 = ((idx >> 5) % (D / 4)) * 4, j = idx / (32 * (D / 4));
+    const float* mj = ml + j * SPLIT * 32;
+    const float* lj = ml + QB * SPLIT * 32 + j * SPLIT * 32;
+    const float* oj = mo + j * SPLIT * D * 32;
+    float mw[SPLIT], M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < SPLIT; w++) { mw[w] = mj[w * 32 + qq]; M = fmaxf(M, mw[w]); }
+    const float bse = M == -INFINITY ? 0.f : M;
+    float den = 0.f, f[SPLIT];
+#pragma unroll
+    for (int w = 0; w < SPLIT; w++) { f[w] = exp2f(mw[w] - bse); den += f[w] * lj[w * 32 + qq]; }
+    const float inv = den > 0.f ? 1.0f / den : 0.f;
+    const int qg = q0 + 32 * j + qq;
+    if (qg < p.L) {
+      f16x4 out;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < SPLIT; w++) acc += f[w] * oj[(w * D + d4 + r) * 32 + qq];
+        out[r] = (f16)(acc * inv);
+      }
+      *reinterpret_cast<f16x4*>(ob + (int64_t)qg * p.os1 + d4) = out;
+    }
+  }
+}
+
+template <int D, int QB, int SPLIT>
+static int launch_attn_pipe(const AttnParams& p, hipStream_t st) {
+  // Tile byte offsets within a (batch, head), up to three blocks past the last, are
+  // 32-bit.
+  if (((int64_t)p.LK + 96 * SPLIT + 64) * (p.ks1 > p.vs1 ? p.ks1 : p.vs1) * 2 >= ((int64_t)1 << 31))
+    return fail("attention: key range too large for the DMA kernel");
+  const int64_t n = (int64_t)((p.L + 32 * QB - 1) / (32 * QB)) * p.H * p.B;
+  if (n > 0x7fffffff) return fail("attention: grid too large");
+  constexpr size_t lds = AttnPipeLds<D, QB, SPLIT>::bytes;
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto kern = attention_pipe_kernel<D, QB, SPLIT>;
+  if (lds > 65536 &&
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return check_launch("attention: set LDS size");
+  hipLaunchKernelGGL(kern, dim3((unsigned)n), dim3(64 * SPLIT), lds, st, p);
+  return check_launch("attention");
+}
+
 template <int D, int SPLIT>
 static int launch_attn(const AttnParams& p, hipStream_t st) {
   const int per = SPLIT == 1 ? 128 : 32;
@@ -418,12 +734,19 @@ static int launch_attn(const AttnParams& p, hipStream_t st) {
 
 template <int D>
 static int launch_d(const AttnParams& p, hipStream_t st) {
-  // Key-split workgroups when 128-query workgroups would leave most CUs idle: eight
-  // waves per 32 queries for long key sequences (head width <= 64), else four.
+  // Key-split workgroups when 128-query workgroups would leave most CUs idle: for long
+  // key sequences the pipelined DMA kernel (head widths 32, 64) or eight waves per 32
+  // queries (16), else four.
   const int64_t wgs = (int64_t)((p.L + 127) / 128) * p.H * p.B;
   int split = 1;
   if (const char* env = getenv("LDX_ATTN_SPLIT")) split = atoi(env);
-  else if (D <= 128 && wgs < 512 && p.LK > 64) split = (D <= 64 && p.LK >= 512) ? 8 : 4;
+  else if (D <= 128 && wgs < 512 && p.LK > 64)
+    split = (D == 32 || D == 64) && p.LK >= 512 ? -4 : (D <= 64 && p.LK >= 512) ? 8 : 4;
+  if constexpr (D == 32 || D == 64) {
+    // Long key sequences: the DMA-fed, software-pipelined four-way key split
+    // (LDX_ATTN_SPLIT=-4 selects it for any length).
+    if (split == -4) return launch_attn_pipe<D, 1, 4>(p, st);
+  }
   if constexpr (D <= 64) {
     if (split == 8) return launch_attn<D, 8>(p, st);
   }

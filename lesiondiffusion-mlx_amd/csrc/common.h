@@ -48,4 +48,29 @@ __device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigne
   return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
 }
 
+// ---------------------------------------------------------------- LDS DMA
+
+// Byte offset of an LDS pointer within the workgroup's LDS (the low 32 bits of its
+// flat address).
+__device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned)(uintptr_t)p; }
+
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4). Issued as asm so that the compiler's wait insertion,
+// which cannot tell these writes from the halo, does not drain all of them before
+// every LDS read; completion is awaited explicitly with vmcnt_wait (+ a barrier when
+// other waves read the data).
+__device__ __forceinline__ void dma_b128(const void* src, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
+               : "memory");
+}
+
+// Wait until at most N vector-memory loads of this wave are outstanding.
+// (s_waitcnt immediate for gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt
+// 11:8 left at their no-wait maxima.)
+template <int N>
+__device__ __forceinline__ void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
 }  // namespace ldx

@@ -194,28 +194,6 @@ __device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
 constexpr int WRING = 4;
 constexpr int WPF = WRING - 1;
 
-// Byte offset of an LDS pointer within the workgroup's LDS (the low 32 bits of its
-// flat address).
-__device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned)(uintptr_t)p; }
-
-// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
-// (global_load_lds_dwordx4). Issued as asm so that the compiler's wait insertion,
-// which cannot tell these writes from the halo, does not drain all of them before
-// every LDS read; completion is awaited explicitly with vmcnt_wait + a barrier.
-__device__ __forceinline__ void dma_b128(const void* src, unsigned lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory");
-}
-
-// Wait until at most N vector-memory loads of this wave are outstanding.
-// (s_waitcnt immediate for gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt
-// 11:8 left at their no-wait maxima.)
-template <int N>
-__device__ __forceinline__ void vmcnt_wait() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
 // Per-lane epilogue constants. In the epilogue each lane finishes one group of 8 output
 // channels (from 32 * ob_first + 8 * (lane % (4 * FO))) for several voxels; the group's
 // bias and shift are summed here, so a caller can load them before its main loop and
