@@ -96,6 +96,11 @@ def _load() -> ctypes.CDLL:
         raise ImportError(
             f"{LIB_NAME} not found at {LIB_PATH}; build it with __graft_entry__.build() "
             "(hipcc --offload-arch=gfx950). There is no CPU fallback.")
+    # torch first: its HIP runtime (soname libamdhip64.so.7) then satisfies the library's
+    # dependency, so the process holds one runtime and the library sees torch's device
+    # and streams. Loaded the other way round, two runtimes coexist and the library's
+    # reports no device.
+    import torch  # noqa: F401
     lib = ctypes.CDLL(os.fspath(LIB_PATH))
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)  # AttributeError if the library lacks a declared symbol

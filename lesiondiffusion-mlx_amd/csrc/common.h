@@ -26,7 +26,28 @@ int check_launch(const char* what);  // hipGetLastError -> LDX_EHIP / LDX_OK
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 // ---------------------------------------------------------------- device math
-__device__ __forceinline__ float silu_f(float y) { return y / (1.0f + __expf(-y)); }
+// SiLU in fp32 from the hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32: about 2 ulp of
+// fp32, against ~15 instructions for an IEEE divide). Every caller rounds the result to
+// fp16, 2^13 fp32 ulps apart. Large negative y gives rcp(inf) = 0, i.e. -0.
+__device__ __forceinline__ float silu_f(float y) {
+  return y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(y * -1.4426950408889634f));
+}
+
+// q = n / d for 0 <= n < 2^31 and 1 <= d < 2^31 from a host-made multiplier: with
+// l = ceil(log2 d), s = 31 + l and m = ceil(2^s / d) < 2^32, n * m / 2^s exceeds n / d by
+// less than n / 2^s <= 1 / d, which never reaches the next integer.
+struct UDiv {
+  unsigned m, s;
+};
+__device__ __forceinline__ int udiv(int n, UDiv d) {
+  return (int)(((unsigned long long)(unsigned)n * d.m) >> d.s);
+}
+inline UDiv make_udiv(unsigned d) {
+  unsigned l = 0;
+  while ((1ull << l) < d) l++;
+  const unsigned s = 31 + l;
+  return UDiv{(unsigned)(((1ull << s) + d - 1) / d), s};
+}
 
 // One 16x16x32 f16 MFMA: D(16x16) += A(16x32) * B(32x16).
 // Lane l: A row l%16, k = 8*(l/16)+e; B col l%16, k = 8*(l/16)+e;

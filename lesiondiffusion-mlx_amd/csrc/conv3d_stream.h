@@ -1,0 +1,32 @@
+// Streamed 3x3x3 stride-1 convolution (conv3d_stream.hip): parameters and the entry used
+// by ldx_conv3d.
+#pragma once
+
+#include "common.h"
+
+namespace ldx {
+
+struct StreamParams {
+  int B, D, H, W;
+  int C0, C1, C, O;
+  int nchunk;               // 32-channel chunks of C0 + C1
+  int NKC;                  // 16-channel k-steps of the packed weight's row
+  int bo, TD, TH, TW;       // output tile and brick
+  int NBD, NBH, NBW, nob, nbr;
+  UDiv dv_nob, dv_nbr, dv_nbw, dv_nbh;
+  const f16* x0; int64_t x0p;
+  const f16* x1; int64_t x1p;
+  const f16* w;
+  const float* bias; int bias_batched;
+  const f16* shift; int64_t shiftp;
+  const float* affine; int silu;
+  const f16* res; int64_t resp;
+  float scale;
+  f16* y; int64_t yp;
+};
+
+// True (and *p planned) when the streamed kernel takes this conv.
+bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* p);
+int conv3d_stream_launch(StreamParams& p, hipStream_t st);
+
+}  // namespace ldx

@@ -1,0 +1,482 @@
+// Streamed implicit-GEMM 3x3x3 stride-1 convolution on gfx950 MFMA (v_mfma_f32_32x32x16_f16)
+// for the common shapes: input channels in 32-channel chunks (C0, C1 multiples of 32),
+// output channels a multiple of the 64- or 128-channel workgroup tile, 16-byte aligned
+// NDHWC rows, no output activation, enough bricks to fill the GPU. Everything else runs
+// through conv3d_kernel.
+//
+// Workgroup: 8 waves = 2 K-groups x 4 waves. Each wave owns a 64-channel x 64-voxel block
+// (2 x 2 MFMA tiles: every A and every B fragment read from LDS feeds two MFMAs, 1 KB of
+// LDS reads per MFMA); the two K-groups take the two 16-channel k-steps of every tap of
+// a 32-channel chunk, so each SIMD runs two waves of the same output tile.
+//
+// Per chunk the weights stream through a 4-slot LDS ring in 9 stages of 3 taps (one
+// (kd, kh) pair, kw = 0..2), filled by direct global->LDS loads. One barrier per stage,
+// placed between its second and third tap: after it the next stage's slot is readable,
+// so the next stage's operands are read from LDS while the third tap's MFMAs run, and
+// the slot two stages back is refilled (three stages ahead of its use). Operands sit
+// in three register sets (one per kw); every tap's offset in the halo is a compile-time
+// constant, so all operand reads are ds_read_b128 at a base register plus an immediate.
+// The brick's halo is double-buffered in LDS: the next chunk's halo is requested into
+// registers at stage 3 and written (with the fused GroupNorm affine + SiLU prologue, one
+// fp16 rounding) into the other buffer during the last stage.
+//
+// Epilogue: the K-groups swap half of their partial sums through LDS, so each wave
+// finishes one 64 x 32 half of its block: bias (+ per-batch-item bias) plus fp16 shift,
+// output scale, fp16 residual, one fp16 rounding, 8-byte stores straight from the
+// accumulator layout.
+//
+// Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619), prologue
+// _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421).
+
+#include "common.h"
+#include "conv3d_stream.h"
+
+#include <type_traits>
+
+namespace ldx {
+namespace cs {
+
+constexpr int CC = 32;            // channels per chunk (two k-steps, one per K-group)
+constexpr int PITCH = CC + 8;     // halves per halo voxel
+constexpr int NSTG = 9;           // stages per chunk: (kd, kh); a stage is kw = 0..2
+constexpr int NSLOT = 4;          // weight ring slots
+constexpr int NT = 512;           // 8 waves
+constexpr int G = CC / 8;         // 16-byte channel groups per halo voxel
+constexpr int VPI = NT / G;       // halo voxels per pass of the workgroup
+constexpr int HS = 3;             // stage at which the next chunk's halo is requested
+
+// Halo row stride in halves: each row of TW + 2 voxels padded so that consecutive rows of
+// a B fragment (TW voxels apart in the fragment) start TW 16-byte bank groups apart
+// (mod 16), which keeps the 16-byte reads of a wave free of bank conflicts.
+template <int TW>
+constexpr int row_stride() {
+  constexpr int pu = PITCH / 8, base = (TW + 2) * pu, target = TW % 16;
+  constexpr int pad = ((target - base) % 16 + 16) % 16;
+  return (base + pad) * 8;
+}
+
+template <int BO, int TD, int TH, int TW>
+struct Shape {
+  static constexpr int NOBT = BO / 32;              // 32-row output blocks of the tile
+  static constexpr int WO = BO / 64, WV = 4 / WO;   // waves over O, over voxels (per K-group)
+  static constexpr int BV = WV * 64;                // voxels per brick
+  static_assert(TD * TH * TW == BV, "the brick must hold the tile's voxels");
+  static constexpr int HD = TD + 2, HH = TH + 2, HW = TW + 2;
+  static constexpr int HVOX = HD * HH * HW;
+  static constexpr int NHS = (HVOX + VPI - 1) / VPI;  // halo slots per thread
+  static constexpr int NHL = NHS + 4;                 // loads of one halo request (+ affine)
+  static constexpr int RS = row_stride<TW>();
+  static constexpr int HALO = HD * HH * RS * 2;       // bytes of one halo buffer
+  static constexpr int NF = 3 * 2 * NOBT;             // 1 KB weight fragments per stage
+  static constexpr int LW = (NF + 7) / 8;             // DMAs per wave per stage
+  static constexpr int STAGE = NF * 1024;             // bytes per ring slot
+  static constexpr int RING = 2 * HALO;               // byte offset of the ring
+  static constexpr int XCH = 8 * 2 * 16 * 64 * 4;     // K-group exchange area (bytes)
+  static constexpr int LDS_MAIN = RING + NSLOT * STAGE;
+  static constexpr int LDS = LDS_MAIN > XCH ? LDS_MAIN : XCH;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(HALO % 16 == 0 && STAGE % 1024 == 0, "alignment");
+};
+
+__device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+template <int BO, int TD, int TH, int TW>
+__global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
+  using S = Shape<BO, TD, TH, TW>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kg = wave >> 2, w4 = wave & 3;
+  const int wo = w4 / S::WV, wv = w4 - wo * S::WV;
+
+  // Workgroup -> (output tile, brick, batch item); the bricks each XCD receives
+  // (workgroups are dealt to the 8 XCDs round-robin) are contiguous, so neighbouring
+  // halos meet in the same L2.
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+  }
+  const int q1 = udiv(wg, p.dv_nob);
+  const int oblk = wg - q1 * p.nob;
+  const int b = udiv(q1, p.dv_nbr);
+  const int brick = q1 - b * p.nbr;
+  const int bt = udiv(brick, p.dv_nbw), bw_i = brick - bt * p.NBW;
+  const int bd_i = udiv(bt, p.dv_nbh), bh_i = bt - bd_i * p.NBH;
+  const int d0 = bd_i * TD, h0 = bh_i * TH, w0 = bw_i * TW;
+
+  // ---- halo slots of this thread: halo voxel tid / G + j * VPI, channel group cg.
+  const int cg = tid % G;
+  unsigned hvi[S::NHS];   // source voxel within the batch item, ~0u outside the volume
+  int hlo[S::NHS];        // byte offset in a halo buffer, -1 past the halo
+#pragma unroll
+  for (int j = 0; j < S::NHS; j++) {
+    const int vox = tid / G + j * VPI;
+    const int hw = vox % S::HW, t = vox / S::HW, hh = t % S::HH, hd = t / S::HH;
+    const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
+    const bool in = vox < S::HVOX && id >= 0 && id < p.D && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
+    hvi[j] = in ? (unsigned)((id * p.H + ih) * p.W + iw) : ~0u;
+    hlo[j] = vox < S::HVOX ? ((hd * S::HH + hh) * S::RS + hw * PITCH + cg * 8) * 2 : -1;
+  }
+  const int64_t vol = (int64_t)p.D * p.H * p.W;
+  f16x8 hval[S::NHS];
+  f32x4 haff[4];
+  // Request chunk ch's halo (NHS 16-byte loads) and the affine of this thread's 8
+  // channels (4 loads): exactly NHL loads, zeros where a buffer range ends (padding
+  // voxels, no affine, a chunk past the last).
+  auto halo_issue = [&](int ch) {
+    const int c0 = ch * CC;
+    const bool live = c0 < p.C;
+    const bool in0 = c0 < p.C0;
+    const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
+    const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
+    const auto rs = make_rsrc(base, live ? (unsigned)(vol * pitch2) : 0u);
+    const unsigned cofs = (unsigned)(((in0 ? c0 : c0 - p.C0) + cg * 8) * 2);
+#pragma unroll
+    for (int j = 0; j < S::NHS; j++)
+      hval[j] = buffer_load16(rs, hvi[j] != ~0u ? hvi[j] * pitch2 + cofs : 0xfffffff0u);
+    const auto ra = make_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine,
+                              p.affine && live ? (unsigned)(p.C * 8) : 0u);
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      haff[q] = __builtin_bit_cast(f32x4, buffer_load16(ra, (unsigned)((c0 + cg * 8) * 8 + q * 16)));
+  };
+  // Write the requested halo into buffer `buf`: affine + SiLU in fp32, one fp16 rounding;
+  // padding voxels stay zero.
+  auto halo_store = [&](int buf) {
+    char* hb = smem + buf * S::HALO;
+    const bool xf = p.affine != nullptr || p.silu;
+#pragma unroll
+    for (int j = 0; j < S::NHS; j++) {
+      if (hlo[j] < 0) continue;
+      f16x8 v = hval[j];
+      if (xf) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float sc = p.affine ? haff[e >> 1][(e & 1) * 2] : 1.f;
+          const float of = p.affine ? haff[e >> 1][(e & 1) * 2 + 1] : 0.f;
+          float yv = (float)v[e] * sc + of;
+          if (p.silu) yv = silu_f(yv);
+          v[e] = hvi[j] != ~0u ? (f16)yv : (f16)0;
+        }
+      }
+      *reinterpret_cast<f16x8*>(hb + hlo[j]) = v;
+    }
+  };
+
+  // ---- weight ring: stage g = NSTG * chunk + (kd * 3 + kh) holds, at fragment
+  // f = (kw * 2 + k) * NOBT + ob, the packed fragment of output block oblk * NOBT + ob, tap
+  // (kd, kh, kw) and k-step 2 * chunk + k. Wave w moves fragments (w + 8 i) % NF (a repeat
+  // moves the same data to the same place, so every wave issues LW loads per stage).
+  const f16* wsrc[S::LW];
+  unsigned wdst[S::LW];
+#pragma unroll
+  for (int i = 0; i < S::LW; i++) {
+    const int f = (wave + 8 * i) % S::NF;
+    const int kw = f / (2 * S::NOBT), r = f % (2 * S::NOBT), k = r / S::NOBT, ob = r % S::NOBT;
+    wsrc[i] = p.w + ((int64_t)((oblk * S::NOBT + ob) * 27 + kw) * p.NKC + k) * 512 + lane * 8;
+    wdst[i] = lds_offset(smem) + (unsigned)(S::RING + f * 1024);
+  }
+  const int nst = p.nchunk * NSTG;
+  auto issue_stage = [&](int g) {
+    // Past the last stage: repeat it (the data it writes is never read again).
+    const int gg = g < nst ? g : nst - 1;
+    const int ch = gg / NSTG, t = gg - ch * NSTG;
+    const int64_t off = ((int64_t)(t * 3) * p.NKC + 2 * ch) * 512;   // tap (kd, kh, 0) = 3 t
+    const unsigned slot = (unsigned)((g % NSLOT) * S::STAGE);
+#pragma unroll
+    for (int i = 0; i < S::LW; i++) dma_b128(wsrc[i] + off, wdst[i] + slot);
+  };
+
+  // ---- operand bases: B at the lane's voxel, k-half and K-group in halo buffer 0; A at
+  // the lane's 16 bytes of fragment (kw = 0, k = kg, ob = 2 wo) in ring slot 0.
+  int bofs[2];
+#pragma unroll
+  for (int fv = 0; fv < 2; fv++) {
+    const int vloc = (wv * 2 + fv) * 32 + (lane & 31);
+    const int vw = vloc % TW, vh = (vloc / TW) % TH, vd = vloc / (TW * TH);
+    bofs[fv] = ((vd * S::HH + vh) * S::RS + vw * PITCH + 8 * (lane >> 5) + kg * 16) * 2;
+  }
+  const char* aptr = smem + S::RING + (kg * S::NOBT + wo * 2) * 1024 + lane * 16;
+
+  // ---- epilogue constants of the block column this wave finishes (fv = kg): bias plus
+  // shift of channels 32 fo + 8 j + 4 hf + r, requested now so the main loop hides them.
+  const int hf = lane >> 5;
+  float addv[2][4][4];
+  {
+    const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
+    const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
+#pragma unroll
+    for (int fo = 0; fo < 2; fo++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
+        const f32x4 b4 = bias ? *reinterpret_cast<const f32x4*>(bias + o) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        const f16x4 s4 = shb ? *reinterpret_cast<const f16x4*>(shb + o) : (f16x4){0, 0, 0, 0};
+#pragma unroll
+        for (int r = 0; r < 4; r++) addv[fo][j][r] = b4[r] + (float)s4[r];
+      }
+  }
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+
+  f16x8 ra[3][2], rb[3][2];   // operands of taps kw = 0, 1, 2: [kw][fo], [kw][fv]
+  auto tap_off = [&](int kd, int kh, int kw) { return ((kd * S::HH + kh) * S::RS + kw * PITCH) * 2; };
+  // A of tap kw of the stage at ring position `as`.
+  auto load_a = [&](int kw, const char* as) {
+#pragma unroll
+    for (int fo = 0; fo < 2; fo++)
+      ra[kw][fo] = *reinterpret_cast<const f16x8*>(as + (kw * 2 * S::NOBT + fo) * 1024);
+  };
+  // B of tap (kd, kh, kw) from halo buffer hb.
+  auto load_b = [&](int kw, int kd, int kh, const char* hb) {
+#pragma unroll
+    for (int fv = 0; fv < 2; fv++) rb[kw][fv] = *reinterpret_cast<const f16x8*>(hb + bofs[fv] + tap_off(kd, kh, kw));
+  };
+  auto mfma_tap = [&](int kw) {
+#pragma unroll
+    for (int fo = 0; fo < 2; fo++)
+#pragma unroll
+      for (int fv = 0; fv < 2; fv++) acc[fo][fv] = mfma(ra[kw][fo], rb[kw][fv], acc[fo][fv]);
+  };
+
+  // Prologue: chunk 0's halo and the first three weight stages, one wait, then stage 0's
+  // first operands.
+  halo_issue(0);
+  issue_stage(0);
+  issue_stage(1);
+  issue_stage(2);
+  vmcnt_wait<2 * S::LW>();   // halo 0 and stage 0 landed (stages 1, 2 may be pending)
+  halo_store(0);
+  __syncthreads();
+#pragma unroll
+  for (int kw = 0; kw < 3; kw++) {
+    load_a(kw, aptr);
+    load_b(kw, 0, 0, smem);
+  }
+
+  for (int ch = 0; ch < p.nchunk; ch++) {
+    const char* hb = smem + (ch & 1) * S::HALO;
+    const char* hb_next = smem + ((ch + 1) & 1) * S::HALO;
+#pragma unroll
+    for (int t = 0; t < NSTG; t++) {
+      const int g = ch * NSTG + t;
+      const int kd = t / 3, kh = t % 3;
+      (void)kd; (void)kh;
+      // taps 0 and 1 (operands read after the previous barrier)
+      mfma_tap(0);
+      mfma_tap(1);
+      if (t == NSTG - 1 && ch + 1 < p.nchunk) {
+        // The next chunk's halo, requested at stage HS, into the other buffer (last read
+        // in chunk ch - 1); younger than it are the stages issued since.
+        vmcnt_wait<(NSTG - 2 - HS) * S::LW>();
+        halo_store((ch + 1) & 1);
+      }
+      // Stage g + 1 has landed once only the loads issued after it may be pending: stage
+      // g + 2's, and the next chunk's halo when it was requested in between.
+      if (t == HS + 1 || t == HS + 2) vmcnt_wait<S::LW + S::NHL>();
+      else vmcnt_wait<S::LW>();
+      __syncthreads();   // stage g + 1 visible; every wave done with stage g - 1's slot
+      issue_stage(g + 3);
+      if (t == HS) halo_issue(ch + 1);
+      // stage g + 1's operands (the next chunk's halo after the last stage): taps 0 and 1
+      // while tap 2 of stage g runs, then tap 2 behind it
+      const char* an = aptr + ((g + 1) % NSLOT) * S::STAGE;
+      const char* hn = t + 1 < NSTG ? hb : hb_next;
+      const int kdn = t + 1 < NSTG ? (t + 1) / 3 : 0, khn = t + 1 < NSTG ? (t + 1) % 3 : 0;
+      load_a(0, an);
+      load_b(0, kdn, khn, hn);
+      load_a(1, an);
+      load_b(1, kdn, khn, hn);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      mfma_tap(2);
+      load_a(2, an);
+      load_b(2, kdn, khn, hn);
+    }
+  }
+  // The trailing (repeated) weight loads land before the LDS is reused or released.
+  vmcnt_wait<0>();
+  __syncthreads();   // every wave done with the halo buffers
+
+  // ---- K-group exchange: group k keeps column block fv = k and hands its other block to
+  // the partner wave (same w4) of the other group; sums are (group 0 + group 1) either way.
+  // Lane (hf, col) of the kept block holds voxel col and channels 32 fo + 8 j + 4 hf + r.
+  const int col = lane & 31;
+  const int vloc = (wv * 2 + kg) * 32 + col;
+  const int vw = vloc % TW, vh = (vloc / TW) % TH, vd = vloc / (TW * TH);
+  const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
+  const bool ok = od < p.D && oh < p.H && ow < p.W;
+  const int64_t ov = (int64_t)b * vol + ((int64_t)od * p.H + oh) * p.W + ow;
+  // The residual rows of the kept block, requested before the exchange.
+  f16x4 res[2][4];
+#pragma unroll
+  for (int fo = 0; fo < 2; fo++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
+      res[fo][j] = p.res && ok ? *reinterpret_cast<const f16x4*>(p.res + ov * p.resp + o) : (f16x4){0, 0, 0, 0};
+    }
+  float* xb = reinterpret_cast<float*>(smem);
+  auto xslot = [&](int grp, int fo, int e4) { return xb + ((((grp * 4 + w4) * 2 + fo) * 4 + e4) * 64 + lane) * 4; };
+  auto finish = [&](auto keep_c) {
+    constexpr int KEEP = decltype(keep_c)::value, SEND = 1 - KEEP;
+#pragma unroll
+    for (int fo = 0; fo < 2; fo++)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; e4++) {
+        const f32x4 q = {acc[fo][SEND][e4 * 4], acc[fo][SEND][e4 * 4 + 1], acc[fo][SEND][e4 * 4 + 2],
+                         acc[fo][SEND][e4 * 4 + 3]};
+        *reinterpret_cast<f32x4*>(xslot(KEEP, fo, e4)) = q;
+      }
+    __syncthreads();
+    if (!ok) return;
+#pragma unroll
+    for (int fo = 0; fo < 2; fo++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const f32x4 q = *reinterpret_cast<const f32x4*>(xslot(SEND, fo, j));
+        const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
+        f16x4 out;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          // (group 0 + group 1) in both groups, then bias + shift, scale, residual
+          const float mine = acc[fo][KEEP][j * 4 + r];
+          const float sum = KEEP == 0 ? mine + q[r] : q[r] + mine;
+          out[r] = (f16)((sum + addv[fo][j][r]) * p.scale + (float)res[fo][j][r]);
+        }
+        *reinterpret_cast<f16x4*>(p.y + ov * p.yp + o) = out;
+      }
+  };
+  if (kg == 0) finish(ic<0>());
+  else finish(ic<1>());
+}
+
+template <int BO, int TD, int TH, int TW>
+static int launch(StreamParams& p, hipStream_t st) {
+  using S = Shape<BO, TD, TH, TW>;
+  p.nob = p.O / BO;
+  p.NBD = (p.D + TD - 1) / TD;
+  p.NBH = (p.H + TH - 1) / TH;
+  p.NBW = (p.W + TW - 1) / TW;
+  const int64_t nbr = (int64_t)p.NBD * p.NBH * p.NBW;
+  const int64_t nwg = nbr * p.nob * p.B;
+  if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
+  p.nbr = (int)nbr;
+  p.dv_nob = make_udiv((unsigned)p.nob);
+  p.dv_nbr = make_udiv((unsigned)p.nbr);
+  p.dv_nbw = make_udiv((unsigned)p.NBW);
+  p.dv_nbh = make_udiv((unsigned)p.NBH);
+  auto kern = conv3s1_kernel<BO, TD, TH, TW>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS) !=
+      hipSuccess)
+    return check_launch("conv3d (streamed): set LDS size");
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(NT), S::LDS, st, p);
+  return check_launch("conv3d (streamed)");
+}
+
+struct Brick {
+  int TD, TH, TW;
+};
+
+// Instantiated bricks per tile width (256 voxels for 64-channel tiles, 128 for 128-channel
+// tiles; two halo buffers and the 4-slot ring must fit in 160 KB of LDS).
+static const Brick kBricks64[] = {{4, 8, 8}, {8, 4, 8}};
+static const Brick kBricks128[] = {{4, 4, 8}};
+
+// Bricks launched (with partial-brick waste) for a volume; the halo volume breaks ties.
+static int64_t brick_cost(const StreamParams& p, const Brick& k, int64_t* halo) {
+  *halo = (int64_t)(k.TD + 2) * (k.TH + 2) * (k.TW + 2);
+  return ceil_div64(p.D, k.TD) * ceil_div64(p.H, k.TH) * ceil_div64(p.W, k.TW);
+}
+
+}  // namespace cs
+
+// Eligibility, tile and brick choice: false leaves the conv to conv3d_kernel.
+bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out) {
+  using namespace cs;
+  if (const char* env = getenv("LDX_CONV_STREAM"))
+    if (atoi(env) == 0) return false;
+  if (a->ksize != 3 || a->stride != 1 || a->upsample || a->act != LDX_ACT_NONE) return false;
+  if (a->c0 % CC || a->c1 % CC || a->out_c % 64) return false;
+  if (a->c1 > 0 && !a->x1) return false;
+  if (a->x0_pitch % 8 || (a->c1 > 0 && a->x1_pitch % 8)) return false;
+  if ((uintptr_t)a->x0 % 16 || (a->c1 > 0 && (uintptr_t)a->x1 % 16)) return false;
+  if (a->y_pitch % 4 || (uintptr_t)a->y % 8) return false;
+  if (a->residual && (a->residual_pitch % 4 || (uintptr_t)a->residual % 8)) return false;
+  if (a->shift && (a->shift_pitch % 4 || (uintptr_t)a->shift % 8)) return false;
+  if (a->bias && (uintptr_t)a->bias % 16) return false;
+  const int64_t vol = (int64_t)a->in_d * a->in_h * a->in_w;
+  if (vol * a->x0_pitch * 2 >= ((int64_t)1 << 31)) return false;
+  if (a->c1 > 0 && vol * a->x1_pitch * 2 >= ((int64_t)1 << 31)) return false;
+  if ((int64_t)a->batch * vol >= ((int64_t)1 << 31)) return false;
+
+  StreamParams& p = *out;
+  p = StreamParams{};
+  p.B = a->batch; p.D = a->in_d; p.H = a->in_h; p.W = a->in_w;
+  p.C0 = a->c0; p.C1 = a->c1; p.C = a->c0 + a->c1; p.O = a->out_c;
+  p.nchunk = p.C / CC;
+  p.NKC = (p.C + 63) / 64 * 4;
+  p.x0 = (const f16*)a->x0; p.x0p = a->x0_pitch;
+  p.x1 = a->c1 > 0 ? (const f16*)a->x1 : p.x0; p.x1p = a->c1 > 0 ? a->x1_pitch : a->x0_pitch;
+  p.w = (const f16*)a->weight;
+  p.bias = a->bias; p.bias_batched = a->bias_batched ? 1 : 0;
+  p.shift = (const f16*)a->shift; p.shiftp = a->shift_pitch;
+  p.affine = a->affine; p.silu = a->silu ? 1 : 0;
+  p.res = (const f16*)a->residual; p.resp = a->residual_pitch;
+  p.scale = a->output_scale;
+  p.y = (f16*)a->y; p.yp = a->y_pitch;
+
+  // Among the tiles that launch at least 200 workgroups: the fewest launched voxel slots
+  // (partial-brick waste), then the fewest halo voxels per output, then 128-channel tiles
+  // (half the halo traffic per output channel).
+  // LDX_CONV_STREAM_MIN_WG lowers the fill threshold (tests use it to run small shapes
+  // through this kernel).
+  int64_t min_wg = 200;
+  if (const char* env = getenv("LDX_CONV_STREAM_MIN_WG")) min_wg = atoll(env);
+  int64_t best_slots = INT64_MAX, best_halo = INT64_MAX;
+  p.bo = 0;
+  for (int bo : {128, 64}) {
+    if (p.O % bo) continue;
+    const Brick* list = bo == 128 ? kBricks128 : kBricks64;
+    const int bv = bo == 128 ? 128 : 256;
+    for (int i = 0; i < (bo == 128 ? 1 : 2); i++) {
+      int64_t halo;
+      const int64_t nb = brick_cost(p, list[i], &halo);
+      if (nb * p.B * (p.O / bo) < min_wg) continue;
+      const int64_t slots = nb * bv;
+      const int64_t hpo = halo * 4096 / ((int64_t)bv * bo);
+      if (slots < best_slots || (slots == best_slots && hpo < best_halo)) {
+        best_slots = slots; best_halo = hpo; p.bo = bo;
+        p.TD = list[i].TD; p.TH = list[i].TH; p.TW = list[i].TW;
+      }
+    }
+  }
+  return p.bo != 0;
+}
+
+int conv3d_stream_launch(StreamParams& p, hipStream_t st) {
+  if (p.bo == 64) {
+    if (p.TD == 4 && p.TH == 8 && p.TW == 8) return cs::launch<64, 4, 8, 8>(p, st);
+    if (p.TD == 8 && p.TH == 4 && p.TW == 8) return cs::launch<64, 8, 4, 8>(p, st);
+  } else if (p.bo == 128) {
+    if (p.TD == 4 && p.TH == 4 && p.TW == 8) return cs::launch<128, 4, 4, 8>(p, st);
+  }
+  return fail("conv3d (streamed): no kernel for tile %d, brick %dx%dx%d", p.bo, p.TD, p.TH, p.TW);
+}
+
+}  // namespace ldx

@@ -16,6 +16,18 @@ from tests.conftest import ACCUMULATION_EPS, OPERAND_ROUNDING, assert_fp16_bar, 
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, params=["default", "streamed"])
+def conv_path(request, monkeypatch):
+    """Every case twice: with the library's own kernel choice, and with the streamed
+    3x3x3 kernel taking every shape it supports (its fill threshold lowered to one
+    workgroup), so small cases cover its partial bricks, batches, concat and fusions."""
+    if request.param == "streamed":
+        monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1")
+    else:
+        monkeypatch.delenv("LDX_CONV_STREAM_MIN_WG", raising=False)
+    return request.param
+
+
 def ndhwc(a: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(a.transpose(0, 2, 3, 4, 1))
 
@@ -207,6 +219,39 @@ def test_norm_silu_conv_fuses_normalisation_shift_and_residual(pkg, dev) -> None
     mag = ocv.conv3d_magnitude(normalized, w64, b.astype(np.float64))
     err = np.abs(ncdhw(host(y)) - expected)
     assert np.all(err <= half_spacing(expected) + (ACCUMULATION_EPS + OPERAND_ROUNDING) * mag)
+
+
+@pytest.mark.parametrize("shape,c0,out_c", [((2, 96, 5, 9, 11), 64, 128), ((1, 128, 6, 7, 18), 32, 64)])
+def test_conv_fuses_concat_norm_shift_residual_scale(pkg, dev, shape, c0, out_c) -> None:
+    """Everything a decoder ResBlock conv fuses (mlx_model.py:290-342, 644): concat([x, skip])
+    read from two tensors, GroupNorm affine + SiLU prologue (rounded to fp16 once), a
+    per-batch-item fp32 bias, an fp16 shift, output scale and a residual, one rounding of
+    the sum; extents that leave partial bricks on every axis."""
+    rng = np.random.default_rng(sum(shape))
+    x, w, b = case(shape, out_c, 3, 31)
+    c = shape[1]
+    gamma = rng.normal(size=(c,)).astype(np.float16)
+    beta = rng.normal(size=(c,)).astype(np.float16)
+    bias = rng.normal(size=(shape[0], out_c)).astype(np.float32)
+    shift = rng.normal(size=(shape[0], out_c)).astype(np.float16)
+    res = rng.normal(size=(shape[0], out_c, *shape[2:])).astype(np.float16)
+    scale = 0.5
+    x0t, x1t = to_dev(ndhwc(x[:, :c0]), dev), to_dev(ndhwc(x[:, c0:]), dev)
+    aff = pkg.ops.group_norm_affine(x0t, to_dev(gamma, dev), to_dev(beta, dev), groups=16, eps=1e-5, x1=x1t)
+    y = pkg.ops.nax_conv3d(x0t, pkg.ops.pack_weight(to_dev(w, dev)), to_dev(bias, dev), x1=x1t, affine=aff,
+                           silu=True, shift=to_dev(shift, dev), residual=to_dev(ndhwc(res), dev),
+                           output_scale=scale)
+    torch.cuda.synchronize()
+    normalized = ocv.f16(onm.silu(onm.group_norm(x.astype(np.float64), gamma, beta, groups=16, eps=1e-5)))
+    w64 = w.astype(np.float64)
+    products = ocv.conv3d(normalized, w64)
+    add = bias.astype(np.float64) + shift.astype(np.float64)
+    expected = (products + add[:, :, None, None, None]) * scale + res
+    mag = ocv.conv3d_magnitude(normalized, w64)
+    err = np.abs(ncdhw(host(y)) - expected)
+    # the normalised operand comes from the GPU's own statistics: allow its fp16 rounding
+    assert np.all(err <= half_spacing(expected) + (ACCUMULATION_EPS + 2 * OPERAND_ROUNDING) * mag * scale)
+    assert_fp16_bar(ncdhw(host(y)), expected)
 
 
 @pytest.mark.parametrize("with_bias", [True, False])
