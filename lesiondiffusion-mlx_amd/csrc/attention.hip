@@ -744,8 +744,12 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
     split = (D == 32 || D == 64) && p.LK >= 512 ? -4 : (D <= 64 && p.LK >= 512) ? 8 : 4;
   if constexpr (D == 32 || D == 64) {
     // Long key sequences: the DMA-fed, software-pipelined four-way key split
-    // (LDX_ATTN_SPLIT=-4 selects it for any length).
+    // (LDX_ATTN_SPLIT=-4 selects it for any length; -8 the eight-way split, -42 / -82 two
+    // 32-query blocks per wave with four / eight waves).
     if (split == -4) return launch_attn_pipe<D, 1, 4>(p, st);
+    if (split == -8) return launch_attn_pipe<D, 1, 8>(p, st);
+    if (split == -42) return launch_attn_pipe<D, 2, 4>(p, st);
+    if (split == -82) return launch_attn_pipe<D, 2, 8>(p, st);
   }
   if constexpr (D <= 64) {
     if (split == 8) return launch_attn<D, 8>(p, st);

@@ -238,6 +238,63 @@ __global__ __launch_bounds__(256) void gn_finalize_kernel(
   }
 }
 
+// Small tensors (coarse UNet levels): one launch, one workgroup per (group, batch item).
+// Thread t sums (x - K) and (x - K)^2 over the group's channels of voxels t, t + 256, ...
+// with K the group's first value (a shift against cancellation), converts them to
+// (n, mean, M2) and the 256 threads merge in a fixed tree, so results repeat bit for bit.
+__global__ __launch_bounds__(256) void gn_small_kernel(
+    const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,
+    int C, int G, int64_t S, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float eps, float* __restrict__ affine) {
+  __shared__ float sn[256], sm[256], s2[256];
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int gs = C / G, c0 = g * gs;
+  auto at = [&](int64_t v, int c) -> float {
+    const int64_t vi = (int64_t)b * S + v;
+    return (float)(c < C0 ? x0[vi * p0 + c] : x1[vi * p1 + (c - C0)]);
+  };
+  const float K = at(0, c0);
+  float sum = 0.f, sq = 0.f;
+  int64_t cnt = 0;
+  const bool vec = gs % 8 == 0 && (c0 + gs <= C0 || c0 >= C0) && p0 % 8 == 0 && p1 % 8 == 0 &&
+                   C0 % 8 == 0;
+  for (int64_t v = t; v < S; v += 256) {
+    if (vec) {
+      const int64_t vi = (int64_t)b * S + v;
+      const f16* row = c0 < C0 ? x0 + vi * p0 + c0 : x1 + vi * p1 + (c0 - C0);
+      for (int c = 0; c < gs; c += 8) {
+        const f16x8 h = *reinterpret_cast<const f16x8*>(row + c);
+#pragma unroll
+        for (int e = 0; e < 8; e++) { const float f = (float)h[e] - K; sum += f; sq += f * f; }
+      }
+    } else {
+      for (int c = c0; c < c0 + gs; c++) { const float f = at(v, c) - K; sum += f; sq += f * f; }
+    }
+    cnt += gs;
+  }
+  {
+    const float n = (float)cnt;
+    const float m = n > 0.f ? sum / n : 0.f;
+    sn[t] = n; sm[t] = K + m; s2[t] = n > 0.f ? fmaxf(sq - sum * m, 0.f) : 0.f;
+  }
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) {
+      const Moments r = merge(Moments{sn[t], sm[t], s2[t]}, Moments{sn[t + off], sm[t + off], s2[t + off]});
+      sn[t] = r.n; sm[t] = r.mean; s2[t] = r.m2;
+    }
+    __syncthreads();
+  }
+  const float mean = sm[0];
+  const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  for (int c = c0 + t; c < c0 + gs; c += 256) {
+    const float sc = gamma[c] * rstd;
+    affine[((int64_t)b * C + c) * 2] = sc;
+    affine[((int64_t)b * C + c) * 2 + 1] = beta[c] - sc * mean;
+  }
+}
+
 static int64_t gn_chunk(int64_t S, int batch) {
   // about 256 workgroups in pass 1 (one per CU), chunks of 64 .. 8192 voxels
   int64_t per = (S * batch + 255) / 256;
@@ -441,6 +498,12 @@ extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, con
   const int64_t nchunks = (voxels + chunk - 1) / chunk;
   if (nchunks > 0x7fffffff || batch > 65535 || groups > 65535) return fail("group_norm_affine: too large");
   hipStream_t st = as_stream(stream);
+  if (nchunks * batch <= 16) {
+    // Few chunks: the one-launch per-group kernel.
+    hipLaunchKernelGGL(gn_small_kernel, dim3(groups, batch), dim3(256), 0, st, (const f16*)x0, p0, c0,
+                       (const f16*)x1, p1, C, groups, voxels, gamma, beta, eps, affine);
+    return check_launch("group_norm_affine: small");
+  }
   float* part = (float*)workspace;
   if (vec)
     hipLaunchKernelGGL(gn_partial_kernel<8>, dim3((unsigned)nchunks, batch), dim3(256), 0, st,
