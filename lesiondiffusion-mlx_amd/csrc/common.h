@@ -85,6 +85,29 @@ __device__ __forceinline__ void dma_b128(const void* src, unsigned lds) {
                : "memory");
 }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource (gfx9 descriptor: base, stride 0, num_records = bytes, the raw-buffer
+// flags of make_rsrc) as four scalars, for the asm DMA below.
+__device__ __forceinline__ i32x4 dma_rsrc(const void* base, unsigned bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32) & 0xffff);
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;
+  return r;
+}
+
+// 16 bytes per lane from a buffer (byte offset voff + soff; out of range reads zeros)
+// straight into LDS at lds + 16 * lane. Asm for the same reason as dma_b128: completion
+// is awaited with explicit vmcnt waits.
+__device__ __forceinline__ void dma_buffer_b128(i32x4 rs, unsigned voff, unsigned soff, unsigned lds) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs),
+               "s"(soff), "s"(lds)
+               : "memory");
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding.
 // (s_waitcnt immediate for gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt
 // 11:8 left at their no-wait maxima.)

@@ -66,11 +66,13 @@ struct Shape {
   static constexpr int NHS = (HVOX + VPI - 1) / VPI;  // halo slots per thread
   static constexpr int NHL = NHS + 4;                 // loads of one halo request (+ affine)
   static constexpr int RS = row_stride<TW>();
-  static constexpr int HALO = HD * HH * RS * 2;       // bytes of one halo buffer
+  static constexpr int HALO = HD * HH * RS * 2;       // bytes of one halo
+  static constexpr int HALOP = (HALO + 8191) / 8192 * 8192;  // halo buffer: whole 8 KB rounds
+  static constexpr int NR = HALOP / 8192;             // halo DMAs per thread (direct halo)
   static constexpr int NF = 3 * 2 * NOBT;             // 1 KB weight fragments per stage
   static constexpr int LW = (NF + 7) / 8;             // DMAs per wave per stage
   static constexpr int STAGE = NF * 1024;             // bytes per ring slot
-  static constexpr int RING = 2 * HALO;               // byte offset of the ring
+  static constexpr int RING = 2 * HALOP;              // byte offset of the ring
   static constexpr int XCH = 8 * 2 * 16 * 64 * 4;     // K-group exchange area (bytes)
   static constexpr int LDS_MAIN = RING + NSLOT * STAGE;
   static constexpr int LDS = LDS_MAIN > XCH ? LDS_MAIN : XCH;
@@ -85,7 +87,11 @@ __device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
 template <int I>
 using ic = std::integral_constant<int, I>;
 
-template <int BO, int TD, int TH, int TW>
+// XF: the GroupNorm affine + SiLU prologue applies (halo staged through registers and
+// transformed); otherwise the halo is copied global -> LDS by DMA in its padded layout,
+// each lane loading the 16 bytes that belong at its position (padding positions and
+// voxels outside the volume read zeros).
+template <int BO, int TD, int TH, int TW, bool XF>
 __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   using S = Shape<BO, TD, TH, TW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -149,7 +155,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // Write the requested halo into buffer `buf`: affine + SiLU in fp32, one fp16 rounding;
   // padding voxels stay zero.
   auto halo_store = [&](int buf) {
-    char* hb = smem + buf * S::HALO;
+    char* hb = smem + buf * S::HALOP;
     const bool xf = p.affine != nullptr || p.silu;
 #pragma unroll
     for (int j = 0; j < S::NHS; j++) {
@@ -167,6 +173,39 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       }
       *reinterpret_cast<f16x8*>(hb + hlo[j]) = v;
     }
+  };
+
+  // ---- direct halo: this thread's NR positions, 16-byte unit (r * 8 + wave) * 64 + lane
+  // of a buffer; per position the source voxel (~0u for padding and for voxels outside the
+  // volume) and the 8-channel group within the chunk.
+  unsigned dvi[S::NR];
+  int dq[S::NR];
+#pragma unroll
+  for (int r = 0; r < S::NR; r++) {
+    const int pb = ((r * 8 + wave) * 64 + lane) * 16;
+    const int row = pb / (S::RS * 2), o = pb - row * (S::RS * 2);
+    const int hw = o / (PITCH * 2), q = (o - hw * PITCH * 2) / 16;
+    const int hd = row / S::HH, hh = row - hd * S::HH;
+    const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
+    const bool in = row < S::HD * S::HH && hw < S::HW && q < G && id >= 0 && id < p.D && ih >= 0 &&
+                    ih < p.H && iw >= 0 && iw < p.W;
+    dvi[r] = in ? (unsigned)((id * p.H + ih) * p.W + iw) : ~0u;
+    dq[r] = q;
+  }
+  // Chunk ch's halo into buffer buf: NR DMAs per thread (a chunk past the last reads zeros).
+  auto halo_dma = [&](int ch, int buf) {
+    const int c0 = ch * CC;
+    const bool live = c0 < p.C;
+    const bool in0 = c0 < p.C0;
+    const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
+    const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
+    const i32x4 rs = dma_rsrc(base, live ? (unsigned)(vol * pitch2) : 0u);
+    const unsigned cb = (unsigned)((in0 ? c0 : c0 - p.C0) * 2);
+    const unsigned dst = lds_offset(smem) + (unsigned)(buf * S::HALOP + wave * 1024);
+#pragma unroll
+    for (int r = 0; r < S::NR; r++)
+      dma_buffer_b128(rs, dvi[r] != ~0u ? dvi[r] * pitch2 + cb + (unsigned)dq[r] * 16u : 0xfffffff0u, 0,
+                      dst + (unsigned)(r * 8192));
   };
 
   // ---- weight ring: stage g = NSTG * chunk + (kd * 3 + kh) holds, at fragment
@@ -253,12 +292,13 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
 
   // Prologue: chunk 0's halo and the first three weight stages, one wait, then stage 0's
   // first operands.
-  halo_issue(0);
+  if constexpr (XF) halo_issue(0);
+  else halo_dma(0, 0);
   issue_stage(0);
   issue_stage(1);
   issue_stage(2);
   vmcnt_wait<2 * S::LW>();   // halo 0 and stage 0 landed (stages 1, 2 may be pending)
-  halo_store(0);
+  if constexpr (XF) halo_store(0);
   __syncthreads();
 #pragma unroll
   for (int kw = 0; kw < 3; kw++) {
@@ -267,8 +307,8 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   }
 
   for (int ch = 0; ch < p.nchunk; ch++) {
-    const char* hb = smem + (ch & 1) * S::HALO;
-    const char* hb_next = smem + ((ch + 1) & 1) * S::HALO;
+    const char* hb = smem + (ch & 1) * S::HALOP;
+    const char* hb_next = smem + ((ch + 1) & 1) * S::HALOP;
 #pragma unroll
     for (int t = 0; t < NSTG; t++) {
       const int g = ch * NSTG + t;
@@ -277,19 +317,26 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       // taps 0 and 1 (operands read after the previous barrier)
       mfma_tap(0);
       mfma_tap(1);
-      if (t == NSTG - 1 && ch + 1 < p.nchunk) {
-        // The next chunk's halo, requested at stage HS, into the other buffer (last read
-        // in chunk ch - 1); younger than it are the stages issued since.
-        vmcnt_wait<(NSTG - 2 - HS) * S::LW>();
-        halo_store((ch + 1) & 1);
+      if constexpr (XF) {
+        if (t == NSTG - 1 && ch + 1 < p.nchunk) {
+          // The next chunk's halo, requested at stage HS, into the other buffer (last read
+          // in chunk ch - 1); younger than it are the stages issued since.
+          vmcnt_wait<(NSTG - 2 - HS) * S::LW>();
+          halo_store((ch + 1) & 1);
+        }
       }
       // Stage g + 1 has landed once only the loads issued after it may be pending: stage
-      // g + 2's, and the next chunk's halo when it was requested in between.
-      if (t == HS + 1 || t == HS + 2) vmcnt_wait<S::LW + S::NHL>();
+      // g + 2's, and the next chunk's halo when it was requested in between. (A directly
+      // copied halo has landed with the stage after it, before this barrier.)
+      if (t == HS + 1 || t == HS + 2) vmcnt_wait<S::LW + (XF ? S::NHL : S::NR)>();
       else vmcnt_wait<S::LW>();
       __syncthreads();   // stage g + 1 visible; every wave done with stage g - 1's slot
       issue_stage(g + 3);
-      if (t == HS) halo_issue(ch + 1);
+      if (t == HS) {
+        // The next chunk's halo, into the buffer chunk ch - 1 used.
+        if constexpr (XF) halo_issue(ch + 1);
+        else halo_dma(ch + 1, (ch + 1) & 1);
+      }
       // stage g + 1's operands (the next chunk's halo after the last stage): taps 0 and 1
       // while tap 2 of stage g runs, then tap 2 behind it
       const char* an = aptr + ((g + 1) % NSLOT) * S::STAGE;
@@ -381,7 +428,7 @@ static int launch(StreamParams& p, hipStream_t st) {
   p.dv_nbr = make_udiv((unsigned)p.nbr);
   p.dv_nbw = make_udiv((unsigned)p.NBW);
   p.dv_nbh = make_udiv((unsigned)p.NBH);
-  auto kern = conv3s1_kernel<BO, TD, TH, TW>;
+  auto kern = p.affine || p.silu ? conv3s1_kernel<BO, TD, TH, TW, true> : conv3s1_kernel<BO, TD, TH, TW, false>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS) !=
       hipSuccess)
     return check_launch("conv3d (streamed): set LDS size");
