@@ -99,6 +99,12 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = wave >> 2, w4 = wave & 3;
   const int wo = w4 / S::WV, wv = w4 - wo * S::WV;
+  // Every kernel argument the prologue needs, fetched in one batch: left to itself the
+  // compiler requests them where first used, one scalar-cache round trip after another.
+  asm volatile("" ::"s"(p.x0), "s"(p.x1), "s"(p.x0p), "s"(p.x1p), "s"(p.w), "s"(p.C0), "s"(p.C), "s"(p.NKC),
+               "s"(p.nchunk), "s"(p.D), "s"(p.H), "s"(p.W), "s"(gridDim.x), "s"(p.nob), "s"(p.nbr), "s"(p.NBW),
+               "s"(p.NBH), "s"(p.dv_nob.m), "s"(p.dv_nob.s), "s"(p.dv_nbr.m), "s"(p.dv_nbr.s), "s"(p.dv_nbw.m),
+               "s"(p.dv_nbw.s), "s"(p.dv_nbh.m), "s"(p.dv_nbh.s));
 
   // Workgroup -> (output tile, brick, batch item); the bricks each XCD receives
   // (workgroups are dealt to the 8 XCDs round-robin) are contiguous, so neighbouring
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   int wg;
   {
     const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
-    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+    wg = x * per + min(x, rem) + k;   // XCD x's range starts at x * per + min(x, rem)
   }
   const int q1 = udiv(wg, p.dv_nob);
   const int oblk = wg - q1 * p.nob;
@@ -179,18 +185,26 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // of a buffer; per position the source voxel (~0u for padding and for voxels outside the
   // volume) and the 8-channel group within the chunk.
   unsigned dvi[S::NR];
-  int dq[S::NR];
+  unsigned dq[S::NR];
+  {
+    // Unsigned arithmetic throughout: the divisions by constants become multiply-shifts
+    // without sign fix-ups.
+    const unsigned u = (unsigned)(wave * 64 + lane) * 16u;
+    const unsigned dd = (unsigned)p.D, hh_ = (unsigned)p.H, ww = (unsigned)p.W;
 #pragma unroll
-  for (int r = 0; r < S::NR; r++) {
-    const int pb = ((r * 8 + wave) * 64 + lane) * 16;
-    const int row = pb / (S::RS * 2), o = pb - row * (S::RS * 2);
-    const int hw = o / (PITCH * 2), q = (o - hw * PITCH * 2) / 16;
-    const int hd = row / S::HH, hh = row - hd * S::HH;
-    const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
-    const bool in = row < S::HD * S::HH && hw < S::HW && q < G && id >= 0 && id < p.D && ih >= 0 &&
-                    ih < p.H && iw >= 0 && iw < p.W;
-    dvi[r] = in ? (unsigned)((id * p.H + ih) * p.W + iw) : ~0u;
-    dq[r] = q;
+    for (int r = 0; r < S::NR; r++) {
+      const unsigned pb = (unsigned)r * 8192u + u;
+      const unsigned row = pb / (unsigned)(S::RS * 2), o = pb - row * (unsigned)(S::RS * 2);
+      const unsigned hw = o / (unsigned)(PITCH * 2), q = (o - hw * (unsigned)(PITCH * 2)) / 16u;
+      const unsigned hd = row / (unsigned)S::HH, hh = row - hd * (unsigned)S::HH;
+      const unsigned id = (unsigned)(d0 - 1) + hd, ih = (unsigned)(h0 - 1) + hh, iw = (unsigned)(w0 - 1) + hw;
+      // Bitwise tests, one unsigned compare per axis (id = -1 wraps past the bound), so the
+      // selection compiles to masks rather than branches.
+      const bool in = (row < (unsigned)(S::HD * S::HH)) & (hw < (unsigned)S::HW) & (q < (unsigned)G) & (id < dd) &
+                      (ih < hh_) & (iw < ww);
+      dvi[r] = in ? (id * hh_ + ih) * ww + iw : ~0u;
+      dq[r] = q * 16u;
+    }
   }
   // Chunk ch's halo into buffer buf: NR DMAs per thread (a chunk past the last reads zeros).
   auto halo_dma = [&](int ch, int buf) {
@@ -204,7 +218,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     const unsigned dst = lds_offset(smem) + (unsigned)(buf * S::HALOP + wave * 1024);
 #pragma unroll
     for (int r = 0; r < S::NR; r++)
-      dma_buffer_b128(rs, dvi[r] != ~0u ? dvi[r] * pitch2 + cb + (unsigned)dq[r] * 16u : 0xfffffff0u, 0,
+      dma_buffer_b128(rs, dvi[r] != ~0u ? dvi[r] * pitch2 + cb + dq[r] : 0xfffffff0u, 0,
                       dst + (unsigned)(r * 8192));
   };
 
@@ -243,24 +257,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   }
   const char* aptr = smem + S::RING + (kg * S::NOBT + wo * 2) * 1024 + lane * 16;
 
-  // ---- epilogue constants of the block column this wave finishes (fv = kg): bias plus
-  // shift of channels 32 fo + 8 j + 4 hf + r, requested now so the main loop hides them.
   const int hf = lane >> 5;
-  float addv[2][4][4];
-  {
-    const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
-    const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
-#pragma unroll
-    for (int fo = 0; fo < 2; fo++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
-        const f32x4 b4 = bias ? *reinterpret_cast<const f32x4*>(bias + o) : (f32x4){0.f, 0.f, 0.f, 0.f};
-        const f16x4 s4 = shb ? *reinterpret_cast<const f16x4*>(shb + o) : (f16x4){0, 0, 0, 0};
-#pragma unroll
-        for (int r = 0; r < 4; r++) addv[fo][j][r] = b4[r] + (float)s4[r];
-      }
-  }
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -369,15 +366,25 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
   const bool ok = od < p.D && oh < p.H && ow < p.W;
   const int64_t ov = (int64_t)b * vol + ((int64_t)od * p.H + oh) * p.W + ow;
-  // The residual rows of the kept block, requested before the exchange.
+  // The epilogue operands of the kept block -- bias (+ per-batch-item bias), fp16 shift
+  // and residual of channels 32 fo + 8 j + 4 hf + r -- requested before the exchange, so
+  // that it hides their latency (and none of these loads delays the prologue's DMA).
   f16x4 res[2][4];
+  f32x4 bv[2][4];
+  f16x4 sv[2][4];
+  {
+    const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
+    const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
 #pragma unroll
-  for (int fo = 0; fo < 2; fo++)
+    for (int fo = 0; fo < 2; fo++)
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
-      res[fo][j] = p.res && ok ? *reinterpret_cast<const f16x4*>(p.res + ov * p.resp + o) : (f16x4){0, 0, 0, 0};
-    }
+      for (int j = 0; j < 4; j++) {
+        const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
+        bv[fo][j] = bias ? *reinterpret_cast<const f32x4*>(bias + o) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        sv[fo][j] = shb ? *reinterpret_cast<const f16x4*>(shb + o) : (f16x4){0, 0, 0, 0};
+        res[fo][j] = p.res && ok ? *reinterpret_cast<const f16x4*>(p.res + ov * p.resp + o) : (f16x4){0, 0, 0, 0};
+      }
+  }
   float* xb = reinterpret_cast<float*>(smem);
   auto xslot = [&](int grp, int fo, int e4) { return xb + ((((grp * 4 + w4) * 2 + fo) * 4 + e4) * 64 + lane) * 4; };
   auto finish = [&](auto keep_c) {
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
           // (group 0 + group 1) in both groups, then bias + shift, scale, residual
           const float mine = acc[fo][KEEP][j * 4 + r];
           const float sum = KEEP == 0 ? mine + q[r] : q[r] + mine;
-          out[r] = (f16)((sum + addv[fo][j][r]) * p.scale + (float)res[fo][j][r]);
+          out[r] = (f16)((sum + (bv[fo][j][r] + (float)sv[fo][j][r])) * p.scale + (float)res[fo][j][r]);
         }
         *reinterpret_cast<f16x4*>(p.y + ov * p.yp + o) = out;
       }
