@@ -422,10 +422,13 @@ void attention_kernel(AttnParams p) {
 // rows are permuted by key_row as in attention_kernel; the loads go through buffer
 // resources that end at the last key, so rows past the sequence read zeros (probability
 // zero).
+// Whole unmasked blocks (all but possibly a wave's last) take a branch-free softmax
+// instantiation; for one query block per wave the V^T operands are read before the
+// softmax so that their LDS latency runs under it.
 template <int D, int QB, int SPLIT>
 struct AttnPipeLds {
   static constexpr int HT = 32 * D;                              // halves per K or V tile
-  static constexpr int MERGE = SPLIT * QB * (D * 32 + 64);       // floats for the merge
+  static constexpr int MERGE = QB * SPLIT * 32 * (D + 4) + 2 * QB * 32 * SPLIT;   // floats for the merge
   static constexpr size_t bytes = (size_t)(SPLIT * 5 * HT * 2 > MERGE * 4 ? SPLIT * 5 * HT * 2 : MERGE * 4);
 };
 
@@ -473,9 +476,9 @@ void attention_pipe_kernel(AttnParams p) {
     for (int i = 0; i < DB; i++)
 #pragma unroll
       for (int e = 0; e < 16; e++) o[j][i][e] = 0.f;
-  float m[QB], l[QB];
+  float l[QB];
 #pragma unroll
-  for (int j = 0; j < QB; j++) { m[j] = -INFINITY; l[j] = 0.f; }
+  for (int j = 0; j < QB; j++) l[j] = 0.f;
 
   unsigned koff[NH], voff[NH];
 #pragma unroll
@@ -507,13 +510,14 @@ void attention_pipe_kernel(AttnParams p) {
   auto vaddr = [&](int r, int d) { return r * D + (((d >> 3) ^ (r % KG)) << 3) + (d & 7); };
 
   f16x8 qf[QB][DK];
+  float m[QB];   // exponent base of each query (log2 units), -inf before its first key
+#pragma unroll
+  for (int j = 0; j < QB; j++) m[j] = -INFINITY;
   // S^T = K Q^T of block it (rows = keys permuted by key_row, columns = queries).
   auto compute_s = [&](int it, f32x16 (&s)[QB]) {
     const f16* Kc = kbuf + (it % 3) * HT;
 #pragma unroll
-    for (int j = 0; j < QB; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) s[j][e] = 0.f;
+    for (int j = 0; j < QB; j++) s[j] = (f32x16){};
 #pragma unroll
     for (int dk = 0; dk < DK; dk++) {
       const int c = 2 * dk + hf;
@@ -532,27 +536,40 @@ void attention_pipe_kernel(AttnParams p) {
       va[ks][db][0] = vaddr(vr0 + ks * 16, vd0 + db * 32);
       va[ks][db][1] = vaddr(vr0 + ks * 16 + 4, vd0 + db * 32);
     }
-  // Online softmax of block it and O^T += V^T P^T. The exponent base m of a query moves
-  // only when the block's maximum exceeds it by more than RB (log2 units): probabilities
-  // then stay below 2^RB (fp16-safe), and the accumulator rescale -- 16 multiplies per
-  // O^T block -- is skipped for all but the few blocks that raise the maximum that much.
+  // Online softmax of block it and O^T += V^T P^T. FULL: every key of the block lies in
+  // the sequence and there is no mask.
   constexpr float RB = 8.f;
-  auto softmax_pv = [&](int it, auto vpar_c, f32x16 (&s)[QB]) {
+  auto softmax_pv = [&](int it, auto vpar_c, auto full_c, f32x16 (&s)[QB]) {
     constexpr int VP = decltype(vpar_c)::value;
-    const int kbase = (wave + SPLIT * it) * KB;
+    constexpr bool FULL = decltype(full_c)::value;
     const f16* Vc = vbuf + VP * HT;
+    auto read_v = [&](int ks, int db) {
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][0]));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][1]));
+      return __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+    };
+    // One query block: the V^T operands first, so their LDS latency runs under the softmax
+    // (two query blocks have no registers to spare for that).
+    f16x8 vf[2][DB];
+    if constexpr (QB == 1) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+        for (int db = 0; db < DB; db++) vf[ks][db] = read_v(ks, db);
+    }
     f16x8 pf[QB][2];
     float alpha[QB];
-    const bool full = kbase + KB <= p.LK && !p.mask;
 #pragma unroll
     for (int j = 0; j < QB; j++) {
       float top;
-      if (full) {
-        top = __builtin_amdgcn_fmed3f(s[j][0], s[j][1], INFINITY);
-#pragma unroll
-        for (int e = 2; e < 16; e++) top = __builtin_amdgcn_fmed3f(top, s[j][e], INFINITY);
-        top = halves_max(top) * p.c;
+      if constexpr (FULL) {
+        // maximum over the 32 keys: a tree of three-input maxima, then the partner lane's
+        const float t0 = fmaxf(fmaxf(s[j][0], s[j][1]), s[j][2]), t1 = fmaxf(fmaxf(s[j][3], s[j][4]), s[j][5]);
+        const float t2 = fmaxf(fmaxf(s[j][6], s[j][7]), s[j][8]), t3 = fmaxf(fmaxf(s[j][9], s[j][10]), s[j][11]);
+        const float t4 = fmaxf(fmaxf(s[j][12], s[j][13]), s[j][14]);
+        top = halves_max(fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, s[j][15]))) * p.c;
       } else {
+        const int kbase = (wave + SPLIT * it) * KB;
         top = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
@@ -565,12 +582,15 @@ void attention_pipe_kernel(AttnParams p) {
         }
         top = halves_max(top);
       }
-      // A query with every key so far removed keeps m = -inf and contributes nothing.
+      // The exponent base moves only when the block's maximum exceeds it by more than RB
+      // (log2 units): probabilities stay below 2^RB (fp16-safe), and the accumulator
+      // rescale is skipped for all but the few blocks that raise the maximum that much. A
+      // query with every key so far removed keeps m = -inf and contributes nothing.
       const float mn = top > m[j] + RB ? top : m[j];
       const float base = mn == -INFINITY ? 0.f : mn;
       alpha[j] = __builtin_amdgcn_exp2f(m[j] - base);
       m[j] = mn;
-      if (full) {
+      if constexpr (FULL) {
 #pragma unroll
         for (int e = 0; e < 16; e++) s[j][e] = s[j][e] * p.c - base;
       } else {
@@ -595,90 +615,117 @@ void attention_pipe_kernel(AttnParams p) {
       }
     }
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
+    for (int ks = 0; ks < 2; ks++)
 #pragma unroll
       for (int db = 0; db < DB; db++) {
-        const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][0]));
-        const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][1]));
-        const f16x8 vf = __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        if constexpr (QB > 1) vf[ks][db] = read_v(ks, db);
 #pragma unroll
-        for (int j = 0; j < QB; j++) o[j][db] = mfma32x(vf, pf[j][ks], o[j][db]);
+        for (int j = 0; j < QB; j++) o[j][db] = mfma32x(vf[ks][db], pf[j][ks], o[j][db]);
       }
-    }
   };
   // One pipeline step: S of block it + 1 goes to the MFMA unit, then block it's softmax
   // and P V; then V(it + 2) refills the V buffer just read and K(it + 3) the K buffer
   // read one step ago. VP = it % 2 (the loop runs two steps per iteration).
-  auto step = [&](int it, auto vpar_c, f32x16 (&cur)[QB], f32x16 (&nxt)[QB]) {
+  auto step = [&](int it, auto vpar_c, auto full_c, f32x16 (&cur)[QB], f32x16 (&nxt)[QB]) {
     // K(it + 1) and V(it) have landed once only the previous step's loads may be pending.
     vmcnt_wait<2 * NH>();
     if (it + 1 < nit) compute_s(it + 1, nxt);
-    softmax_pv(it, vpar_c, cur);
+    softmax_pv(it, vpar_c, full_c, cur);
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's V reads have returned
     issue_v(it + 2);
     issue_k(it + 3);
   };
 
-  issue_k(0); issue_v(0); issue_k(1); issue_v(1); issue_k(2);
+  // Q^T fragments by asm loads, issued before the tile DMAs: the compiler's own wait for a
+  // load it could see would drain every DMA issued after it. Only Q and K(0) are awaited
+  // before the first S MFMAs; the empty asm keeps every use of the fragments behind the wait.
 #pragma unroll
   for (int j = 0; j < QB; j++)
 #pragma unroll
     for (int dk = 0; dk < DK; dk++)
-      qf[j][dk] = *reinterpret_cast<const f16x8*>(qb_ + (int64_t)qi[j] * p.qs1 + dk * 16 + 8 * hf);
-  vmcnt_wait<0>();
+      asm volatile("global_load_dwordx4 %0, %1, off"
+                   : "=v"(qf[j][dk])
+                   : "v"(qb_ + (int64_t)qi[j] * p.qs1 + dk * 16 + 8 * hf)
+                   : "memory");
+  issue_k(0); issue_v(0); issue_k(1); issue_v(1); issue_k(2);
+  vmcnt_wait<4 * NH>();   // Q and K(0) have landed; V(0), K(1), V(1), K(2) may be pending
+#pragma unroll
+  for (int j = 0; j < QB; j++)
+#pragma unroll
+    for (int dk = 0; dk < DK; dk++) asm volatile("" : "+v"(qf[j][dk]));
   f32x16 sa[QB], sb[QB];
   if (nit > 0) compute_s(0, sa);
-  for (int it = 0; it < nit; it += 2) {
-    step(it, std::integral_constant<int, 0>(), sa, sb);
-    if (it + 1 < nit) step(it + 1, std::integral_constant<int, 1>(), sb, sa);
+  // Blocks before nfull are whole and unmasked (only the sequence's last block can be
+  // partial, and only the wave that owns it has it as its last).
+  const int nfull = p.mask ? 0 : (p.LK % KB == 0 || (nblk - 1 - wave) % SPLIT != 0 ? nit : nit - 1);
+  using T = std::integral_constant<bool, true>;
+  using F = std::integral_constant<bool, false>;
+  using V0 = std::integral_constant<int, 0>;
+  using V1 = std::integral_constant<int, 1>;
+  int it = 0;
+  for (; it + 1 < nfull; it += 2) {
+    step(it, V0(), T(), sa, sb);
+    step(it + 1, V1(), T(), sb, sa);
+  }
+  for (; it < nit; it += 2) {
+    if (it < nfull) step(it, V0(), T(), sa, sb);
+    else step(it, V0(), F(), sa, sb);
+    if (it + 1 < nit) step(it + 1, V1(), F(), sb, sa);
   }
 
+  // Merge: every wave publishes its (base, sum) per query; then each scales its O^T by
+  // exp2(m_w - M) / den (M and den over the waves) and stores it as [wave][query][d] fp32
+  // rows padded to D + 4 (16-byte writes free of bank conflicts); each thread then sums
+  // the SPLIT partials of 8 consecutive d of one query into one 16-byte store.
   f16* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
-  float* mo = reinterpret_cast<float*>(smem);            // [QB][SPLIT][D][32] partial O^T
-  float* ml = mo + QB * SPLIT * D * 32;                   // [QB][SPLIT][32] m, then l
+  constexpr int RP = D + 4;
+  float* mo = reinterpret_cast<float*>(smem);            // [QB][SPLIT][32][RP] scaled partial O
+  float* ml = mo + QB * SPLIT * 32 * RP;                  // [QB][32][SPLIT] m, then the same for l
   vmcnt_wait<0>();
-  __syncthreads();
+  __syncthreads();   // every wave done with its tiles (the merge area overlaps them)
 #pragma unroll
   for (int j = 0; j < QB; j++) {
     const float lj = halves_sum(l[j]);
-#pragma unroll
-    for (int db = 0; db < DB; db++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int d = db * 32 + (e >> 2) * 8 + 4 * hf + (e & 3);
-        mo[((j * SPLIT + wave) * D + d) * 32 + col] = o[j][db][e];
-      }
     if (hf == 0) {
-      ml[(j * SPLIT + wave) * 32 + col] = m[j];
-      ml[QB * SPLIT * 32 + (j * SPLIT + wave) * 32 + col] = lj;
+      ml[(j * 32 + col) * SPLIT + wave] = m[j];
+      ml[QB * 32 * SPLIT + (j * 32 + col) * SPLIT + wave] = lj;
     }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < QB * 32 * (D / 4); idx += NT) {
-    const int qq = idx & 31, d4 = ((idx >> 5) % (D / 4)) * 4, j = idx / (32 * (D / 4));
-    const float* mj = ml + j * SPLIT * 32;
-    const float* lj = ml + QB * SPLIT * 32 + j * SPLIT * 32;
-    const float* oj = mo + j * SPLIT * D * 32;
-    float mw[SPLIT], M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < SPLIT; w++) { mw[w] = mj[w * 32 + qq]; M = fmaxf(M, mw[w]); }
+  for (int j = 0; j < QB; j++) {
+    float M = -INFINITY, mw[SPLIT];
+#pragma unroll
+    for (int w = 0; w < SPLIT; w++) { mw[w] = ml[(j * 32 + col) * SPLIT + w]; M = fmaxf(M, mw[w]); }
     const float bse = M == -INFINITY ? 0.f : M;
-    float den = 0.f, f[SPLIT];
+    float den = 0.f;
 #pragma unroll
-    for (int w = 0; w < SPLIT; w++) { f[w] = exp2f(mw[w] - bse); den += f[w] * lj[w * 32 + qq]; }
-    const float inv = den > 0.f ? 1.0f / den : 0.f;
-    const int qg = q0 + 32 * j + qq;
-    if (qg < p.L) {
-      f16x4 out;
+    for (int w = 0; w < SPLIT; w++)
+      den += __builtin_amdgcn_exp2f(mw[w] - bse) * ml[QB * 32 * SPLIT + (j * 32 + col) * SPLIT + w];
+    const float f = den > 0.f ? __builtin_amdgcn_exp2f(m[j] - bse) / den : 0.f;
+    float* row = mo + ((j * SPLIT + wave) * 32 + col) * RP + 4 * hf;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        float acc = 0.f;
+    for (int db = 0; db < DB; db++)
 #pragma unroll
-        for (int w = 0; w < SPLIT; w++) acc += f[w] * oj[(w * D + d4 + r) * 32 + qq];
-        out[r] = (f16)(acc * inv);
+      for (int g = 0; g < 4; g++) {
+        const f32x4 v = {o[j][db][4 * g] * f, o[j][db][4 * g + 1] * f, o[j][db][4 * g + 2] * f, o[j][db][4 * g + 3] * f};
+        *reinterpret_cast<f32x4*>(row + db * 32 + g * 8) = v;
       }
-      *reinterpret_cast<f16x4*>(ob + (int64_t)qg * p.os1 + d4) = out;
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < QB * 32 * (D / 8); idx += NT) {
+    const int d8 = (idx % (D / 8)) * 8, qq = (idx / (D / 8)) % 32, j = idx / (32 * (D / 8));
+    const int qg = q0 + 32 * j + qq;
+    if (qg >= p.L) continue;
+    f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < SPLIT; w++) {
+      const float* r = mo + ((j * SPLIT + w) * 32 + qq) * RP + d8;
+      a0 += *reinterpret_cast<const f32x4*>(r);
+      a1 += *reinterpret_cast<const f32x4*>(r + 4);
     }
+    const f16x8 out = {(f16)a0[0], (f16)a0[1], (f16)a0[2], (f16)a0[3], (f16)a1[0], (f16)a1[1], (f16)a1[2], (f16)a1[3]};
+    *reinterpret_cast<f16x8*>(ob + (int64_t)qg * p.os1 + d8) = out;
   }
 }
 
@@ -722,12 +769,9 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
     split = (D == 32 || D == 64) && p.LK >= 512 ? -4 : (D <= 64 && p.LK >= 512) ? 8 : 4;
   if constexpr (D == 32 || D == 64) {
     // Long key sequences: the DMA-fed, software-pipelined four-way key split
-    // (LDX_ATTN_SPLIT=-4 selects it for any length; -8 the eight-way split, -42 / -82 two
-    // 32-query blocks per wave with four / eight waves).
+    // (LDX_ATTN_SPLIT=-4 selects it for any length; -8 the eight-way split).
     if (split == -4) return launch_attn_pipe<D, 1, 4>(p, st);
     if (split == -8) return launch_attn_pipe<D, 1, 8>(p, st);
-    if (split == -42) return launch_attn_pipe<D, 2, 4>(p, st);
-    if (split == -82) return launch_attn_pipe<D, 2, 8>(p, st);
   }
   if constexpr (D <= 64) {
     if (split == 8) return launch_attn<D, 8>(p, st);
