@@ -108,6 +108,21 @@ __device__ __forceinline__ void dma_buffer_b128(i32x4 rs, unsigned voff, unsigne
                : "memory");
 }
 
+// 16 bytes per lane from a buffer (byte offset voff + soff; out of range reads zeros) into
+// registers, by asm: the compiler's wait insertion does not see it (and so drains nothing
+// on its account). The caller awaits it with vmcnt_wait and then passes the value through
+// pin_value before its first use.
+__device__ __forceinline__ f16x8 buffer_load16_asm(i32x4 rs, unsigned voff, unsigned soff = 0) {
+  f16x8 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rs), "s"(soff) : "memory");
+  return v;
+}
+// Orders every later use of v after this point (after the wait that made it valid).
+template <typename T>
+__device__ __forceinline__ void pin_value(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding.
 // (s_waitcnt immediate for gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt
 // 11:8 left at their no-wait maxima.)

@@ -140,27 +140,33 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   f32x4 haff[4];
   // Request chunk ch's halo (NHS 16-byte loads) and the affine of this thread's 8
   // channels (4 loads): exactly NHL loads, zeros where a buffer range ends (padding
-  // voxels, no affine, a chunk past the last).
+  // voxels, no affine, a chunk past the last). The loads are asm, so that the compiler
+  // inserts no wait of its own for them (its count would ignore the weight DMAs issued
+  // after them and drain those too); halo_store runs after an explicit wait.
   auto halo_issue = [&](int ch) {
     const int c0 = ch * CC;
     const bool live = c0 < p.C;
     const bool in0 = c0 < p.C0;
     const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
     const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
-    const auto rs = make_rsrc(base, live ? (unsigned)(vol * pitch2) : 0u);
+    const i32x4 rs = dma_rsrc(base, live ? (unsigned)(vol * pitch2) : 0u);
     const unsigned cofs = (unsigned)(((in0 ? c0 : c0 - p.C0) + cg * 8) * 2);
 #pragma unroll
     for (int j = 0; j < S::NHS; j++)
-      hval[j] = buffer_load16(rs, hvi[j] != ~0u ? hvi[j] * pitch2 + cofs : 0xfffffff0u);
-    const auto ra = make_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine,
+      hval[j] = buffer_load16_asm(rs, hvi[j] != ~0u ? hvi[j] * pitch2 + cofs : 0xfffffff0u);
+    const i32x4 ra = dma_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine,
                               p.affine && live ? (unsigned)(p.C * 8) : 0u);
 #pragma unroll
     for (int q = 0; q < 4; q++)
-      haff[q] = __builtin_bit_cast(f32x4, buffer_load16(ra, (unsigned)((c0 + cg * 8) * 8 + q * 16)));
+      haff[q] = __builtin_bit_cast(f32x4, buffer_load16_asm(ra, (unsigned)((c0 + cg * 8) * 8 + q * 16)));
   };
   // Write the requested halo into buffer `buf`: affine + SiLU in fp32, one fp16 rounding;
-  // padding voxels stay zero.
+  // padding voxels stay zero. Called after the wait that covers halo_issue's loads.
   auto halo_store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < S::NHS; j++) pin_value(hval[j]);
+#pragma unroll
+    for (int q = 0; q < 4; q++) pin_value(haff[q]);
     char* hb = smem + buf * S::HALOP;
     const bool xf = p.affine != nullptr || p.silu;
 #pragma unroll
