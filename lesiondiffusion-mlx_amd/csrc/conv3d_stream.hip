@@ -21,9 +21,9 @@
 // fp16 rounding) into the other buffer during the last stage.
 //
 // Epilogue: the K-groups swap half of their partial sums through LDS, so each wave
-// finishes one 64 x 32 half of its block: bias (+ per-batch-item bias) plus fp16 shift,
-// output scale, fp16 residual, one fp16 rounding, 8-byte stores straight from the
-// accumulator layout.
+// finishes one 64 x 32 half of its block; the sums pass through wave-private LDS rows so
+// that each lane then finishes 8 consecutive channels of a voxel: bias (+ per-batch-item
+// bias) plus fp16 shift, output scale, fp16 residual, one fp16 rounding, 16-byte stores.
 //
 // Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619), prologue
 // _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421).
@@ -74,8 +74,10 @@ struct Shape {
   static constexpr int STAGE = NF * 1024;             // bytes per ring slot
   static constexpr int RING = 2 * HALOP;              // byte offset of the ring
   static constexpr int XCH = 8 * 2 * 16 * 64 * 4;     // K-group exchange area (bytes)
+  static constexpr int RP = 64 + 4;                   // floats per epilogue row (padded)
+  static constexpr int EPI = XCH + 8 * 32 * RP * 4;   // exchange area + the waves' rows
   static constexpr int LDS_MAIN = RING + NSLOT * STAGE;
-  static constexpr int LDS = LDS_MAIN > XCH ? LDS_MAIN : XCH;
+  static constexpr int LDS = LDS_MAIN > EPI ? LDS_MAIN : EPI;
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert(HALO % 16 == 0 && STAGE % 1024 == 0, "alignment");
 };
@@ -363,37 +365,44 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   vmcnt_wait<0>();
   __syncthreads();   // every wave done with the halo buffers
 
-  // ---- K-group exchange: group k keeps column block fv = k and hands its other block to
-  // the partner wave (same w4) of the other group; sums are (group 0 + group 1) either way.
-  // Lane (hf, col) of the kept block holds voxel col and channels 32 fo + 8 j + 4 hf + r.
-  const int col = lane & 31;
-  const int vloc = (wv * 2 + kg) * 32 + col;
-  const int vw = vloc % TW, vh = (vloc / TW) % TH, vd = vloc / (TW * TH);
-  const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
-  const bool ok = od < p.D && oh < p.H && ow < p.W;
-  const int64_t ov = (int64_t)b * vol + ((int64_t)od * p.H + oh) * p.W + ow;
-  // The epilogue operands of the kept block -- bias (+ per-batch-item bias), fp16 shift
-  // and residual of channels 32 fo + 8 j + 4 hf + r -- requested before the exchange, so
-  // that it hides their latency (and none of these loads delays the prologue's DMA).
-  f16x4 res[2][4];
-  f32x4 bv[2][4];
-  f16x4 sv[2][4];
-  {
-    const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
-    const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
+  // ---- K-group exchange, then whole rows. Group k keeps column block fv = k and hands its
+  // other block to the partner wave (same w4) of the other group; sums are (group 0 +
+  // group 1) either way. The kept 32 voxels x 64 channels (lane (hf, col): voxel col,
+  // channels 32 fo + 8 j + 4 hf + r) go through wave-private fp32 rows in LDS, so that the
+  // stores are whole 16-byte channel groups: lane l finishes channels 8 (l % 8) .. + 7 of
+  // voxels l / 8 + 8 i, i < 4 (128 contiguous bytes per voxel, 1 KB per store instruction
+  // when the 64 channels are the whole row).
+  const int col = lane & 31, g8 = lane & 7;
+  const int o8 = oblk * BO + wo * 64 + g8 * 8;
+  int64_t ovr[4];
+  bool okr[4];
 #pragma unroll
-    for (int fo = 0; fo < 2; fo++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
-        bv[fo][j] = bias ? *reinterpret_cast<const f32x4*>(bias + o) : (f32x4){0.f, 0.f, 0.f, 0.f};
-        sv[fo][j] = shb ? *reinterpret_cast<const f16x4*>(shb + o) : (f16x4){0, 0, 0, 0};
-        res[fo][j] = p.res && ok ? *reinterpret_cast<const f16x4*>(p.res + ov * p.resp + o) : (f16x4){0, 0, 0, 0};
-      }
+  for (int i = 0; i < 4; i++) {
+    const int vloc = (wv * 2 + kg) * 32 + (lane >> 3) + 8 * i;
+    const int vw = vloc % TW, vh = (vloc / TW) % TH, vd = vloc / (TW * TH);
+    const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
+    okr[i] = od < p.D && oh < p.H && ow < p.W;
+    ovr[i] = (int64_t)b * vol + ((int64_t)od * p.H + oh) * p.W + ow;
   }
+  // The epilogue operands of these rows -- bias (+ per-batch-item bias), fp16 shift and
+  // residual -- requested before the exchange, so that it hides their latency (and none
+  // of these loads delays the prologue's DMA).
+  f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
+  f16x8 sv = {};
+  f16x8 res[4];
+  if (p.bias) {
+    const float* bias = p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o8;
+    bv0 = *reinterpret_cast<const f32x4*>(bias);
+    bv1 = *reinterpret_cast<const f32x4*>(bias + 4);
+  }
+  if (p.shift) sv = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o8);
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    res[i] = p.res && okr[i] ? *reinterpret_cast<const f16x8*>(p.res + ovr[i] * p.resp + o8) : (f16x8){};
   float* xb = reinterpret_cast<float*>(smem);
   auto xslot = [&](int grp, int fo, int e4) { return xb + ((((grp * 4 + w4) * 2 + fo) * 4 + e4) * 64 + lane) * 4; };
-  auto finish = [&](auto keep_c) {
+  float* rows = reinterpret_cast<float*>(smem + S::XCH) + wave * (32 * S::RP);
+  auto exchange = [&](auto keep_c) {
     constexpr int KEEP = decltype(keep_c)::value, SEND = 1 - KEEP;
 #pragma unroll
     for (int fo = 0; fo < 2; fo++)
@@ -404,26 +413,37 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
         *reinterpret_cast<f32x4*>(xslot(KEEP, fo, e4)) = q;
       }
     __syncthreads();
-    if (!ok) return;
 #pragma unroll
     for (int fo = 0; fo < 2; fo++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         const f32x4 q = *reinterpret_cast<const f32x4*>(xslot(SEND, fo, j));
-        const int o = oblk * BO + wo * 64 + fo * 32 + 4 * hf + 8 * j;
-        f16x4 out;
+        f32x4 v;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          // (group 0 + group 1) in both groups, then bias + shift, scale, residual
           const float mine = acc[fo][KEEP][j * 4 + r];
-          const float sum = KEEP == 0 ? mine + q[r] : q[r] + mine;
-          out[r] = (f16)((sum + (bv[fo][j][r] + (float)sv[fo][j][r])) * p.scale + (float)res[fo][j][r]);
+          v[r] = KEEP == 0 ? mine + q[r] : q[r] + mine;
         }
-        *reinterpret_cast<f16x4*>(p.y + ov * p.yp + o) = out;
+        *reinterpret_cast<f32x4*>(rows + col * S::RP + fo * 32 + 8 * j + 4 * hf) = v;
       }
   };
-  if (kg == 0) finish(ic<0>());
-  else finish(ic<1>());
+  if (kg == 0) exchange(ic<0>());
+  else exchange(ic<1>());
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's rows are written
+  __builtin_amdgcn_wave_barrier();
+  // (group 0 + group 1), then bias + shift, scale, residual, one rounding
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float* rw = rows + ((lane >> 3) + 8 * i) * S::RP + g8 * 8;
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(rw), s1 = *reinterpret_cast<const f32x4*>(rw + 4);
+    f16x8 out;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      out[e] = (f16)((s0[e] + (bv0[e] + (float)sv[e])) * p.scale + (float)res[i][e]);
+      out[e + 4] = (f16)((s1[e] + (bv1[e] + (float)sv[e + 4])) * p.scale + (float)res[i][e + 4]);
+    }
+    if (okr[i]) *reinterpret_cast<f16x8*>(p.y + ovr[i] * p.yp + o8) = out;
+  }
 }
 
 template <int BO, int TD, int TH, int TW>
@@ -476,9 +496,9 @@ bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out) {
   if (a->c1 > 0 && !a->x1) return false;
   if (a->x0_pitch % 8 || (a->c1 > 0 && a->x1_pitch % 8)) return false;
   if ((uintptr_t)a->x0 % 16 || (a->c1 > 0 && (uintptr_t)a->x1 % 16)) return false;
-  if (a->y_pitch % 4 || (uintptr_t)a->y % 8) return false;
-  if (a->residual && (a->residual_pitch % 4 || (uintptr_t)a->residual % 8)) return false;
-  if (a->shift && (a->shift_pitch % 4 || (uintptr_t)a->shift % 8)) return false;
+  if (a->y_pitch % 8 || (uintptr_t)a->y % 16) return false;
+  if (a->residual && (a->residual_pitch % 8 || (uintptr_t)a->residual % 16)) return false;
+  if (a->shift && (a->shift_pitch % 8 || (uintptr_t)a->shift % 16)) return false;
   if (a->bias && (uintptr_t)a->bias % 16) return false;
   const int64_t vol = (int64_t)a->in_d * a->in_h * a->in_w;
   if (vol * a->x0_pitch * 2 >= ((int64_t)1 << 31)) return false;
