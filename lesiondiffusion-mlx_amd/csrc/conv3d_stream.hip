@@ -20,10 +20,10 @@
 // registers at stage 3 and written (with the fused GroupNorm affine + SiLU prologue, one
 // fp16 rounding) into the other buffer during the last stage.
 //
-// Epilogue: the K-groups swap half of their partial sums through LDS, so each wave
-// finishes one 64 x 32 half of its block; the sums pass through wave-private LDS rows so
-// that each lane then finishes 8 consecutive channels of a voxel: bias (+ per-batch-item
-// bias) plus fp16 shift, output scale, fp16 residual, one fp16 rounding, 16-byte stores.
+// Epilogue: both K-groups leave their partial sums as fp32 voxel rows in LDS; each wave
+// then finishes one 64-channel x 32-voxel half of its block, a lane 8 consecutive channels
+// of a voxel: (group 0 + group 1), bias (+ per-batch-item bias) plus fp16 shift, output
+// scale, fp16 residual, one fp16 rounding, 16-byte stores.
 //
 // Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619), prologue
 // _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421).
@@ -73,9 +73,8 @@ struct Shape {
   static constexpr int LW = (NF + 7) / 8;             // DMAs per wave per stage
   static constexpr int STAGE = NF * 1024;             // bytes per ring slot
   static constexpr int RING = 2 * HALOP;              // byte offset of the ring
-  static constexpr int XCH = 8 * 2 * 16 * 64 * 4;     // K-group exchange area (bytes)
   static constexpr int RP = 64 + 4;                   // floats per epilogue row (padded)
-  static constexpr int EPI = XCH + 8 * 32 * RP * 4;   // exchange area + the waves' rows
+  static constexpr int EPI = 16 * 32 * RP * 4;        // epilogue rows: [w4][fv][group] x 32 voxels
   static constexpr int LDS_MAIN = RING + NSLOT * STAGE;
   static constexpr int LDS = LDS_MAIN > EPI ? LDS_MAIN : EPI;
   static_assert(LDS <= 160 * 1024, "LDS budget");
@@ -365,13 +364,11 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   vmcnt_wait<0>();
   __syncthreads();   // every wave done with the halo buffers
 
-  // ---- K-group exchange, then whole rows. Group k keeps column block fv = k and hands its
-  // other block to the partner wave (same w4) of the other group; sums are (group 0 +
-  // group 1) either way. The kept 32 voxels x 64 channels (lane (hf, col): voxel col,
-  // channels 32 fo + 8 j + 4 hf + r) go through wave-private fp32 rows in LDS, so that the
-  // stores are whole 16-byte channel groups: lane l finishes channels 8 (l % 8) .. + 7 of
-  // voxels l / 8 + 8 i, i < 4 (128 contiguous bytes per voxel, 1 KB per store instruction
-  // when the 64 channels are the whole row).
+  // ---- Epilogue rows. The wave's kept block is column block fv = kg: 32 voxels x 64
+  // channels, summed (group 0 + group 1) from both K-groups' partial rows; lane l finishes
+  // channels 8 (l % 8) .. + 7 of voxels l / 8 + 8 i, i < 4 (128 contiguous bytes per voxel,
+  // 1 KB per store instruction when the 64 channels are the whole row). In the MFMA layout
+  // lane (hf, col) holds voxel col, channels 32 fo + 8 j + 4 hf + r.
   const int col = lane & 31, g8 = lane & 7;
   const int o8 = oblk * BO + wo * 64 + g8 * 8;
   int64_t ovr[4];
@@ -385,8 +382,8 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     ovr[i] = (int64_t)b * vol + ((int64_t)od * p.H + oh) * p.W + ow;
   }
   // The epilogue operands of these rows -- bias (+ per-batch-item bias), fp16 shift and
-  // residual -- requested before the exchange, so that it hides their latency (and none
-  // of these loads delays the prologue's DMA).
+  // residual -- requested before the partial rows are written, which hides their latency
+  // (and none of these loads delays the prologue's DMA).
   f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
   f16x8 sv = {};
   f16x8 res[4];
@@ -399,43 +396,28 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
 #pragma unroll
   for (int i = 0; i < 4; i++)
     res[i] = p.res && okr[i] ? *reinterpret_cast<const f16x8*>(p.res + ovr[i] * p.resp + o8) : (f16x8){};
-  float* xb = reinterpret_cast<float*>(smem);
-  auto xslot = [&](int grp, int fo, int e4) { return xb + ((((grp * 4 + w4) * 2 + fo) * 4 + e4) * 64 + lane) * 4; };
-  float* rows = reinterpret_cast<float*>(smem + S::XCH) + wave * (32 * S::RP);
-  auto exchange = [&](auto keep_c) {
-    constexpr int KEEP = decltype(keep_c)::value, SEND = 1 - KEEP;
+  // Both K-groups leave their partial sums as fp32 rows, [w4][fv][group][voxel][channel]
+  // (rows padded to RP floats: 16-byte writes free of bank conflicts).
+  float* rowsb = reinterpret_cast<float*>(smem);
+  auto rowp = [&](int fv, int grp) { return rowsb + ((w4 * 2 + fv) * 2 + grp) * (32 * S::RP); };
 #pragma unroll
-    for (int fo = 0; fo < 2; fo++)
+  for (int fo = 0; fo < 2; fo++)
 #pragma unroll
-      for (int e4 = 0; e4 < 4; e4++) {
-        const f32x4 q = {acc[fo][SEND][e4 * 4], acc[fo][SEND][e4 * 4 + 1], acc[fo][SEND][e4 * 4 + 2],
-                         acc[fo][SEND][e4 * 4 + 3]};
-        *reinterpret_cast<f32x4*>(xslot(KEEP, fo, e4)) = q;
-      }
-    __syncthreads();
-#pragma unroll
-    for (int fo = 0; fo < 2; fo++)
+    for (int fv = 0; fv < 2; fv++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const f32x4 q = *reinterpret_cast<const f32x4*>(xslot(SEND, fo, j));
-        f32x4 v;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float mine = acc[fo][KEEP][j * 4 + r];
-          v[r] = KEEP == 0 ? mine + q[r] : q[r] + mine;
-        }
-        *reinterpret_cast<f32x4*>(rows + col * S::RP + fo * 32 + 8 * j + 4 * hf) = v;
+        const f32x4 v = {acc[fo][fv][4 * j], acc[fo][fv][4 * j + 1], acc[fo][fv][4 * j + 2], acc[fo][fv][4 * j + 3]};
+        *reinterpret_cast<f32x4*>(rowp(fv, kg) + col * S::RP + fo * 32 + 8 * j + 4 * hf) = v;
       }
-  };
-  if (kg == 0) exchange(ic<0>());
-  else exchange(ic<1>());
-  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this wave's rows are written
-  __builtin_amdgcn_wave_barrier();
-  // (group 0 + group 1), then bias + shift, scale, residual, one rounding
+  __syncthreads();
+  // Rows fv = kg: (group 0 + group 1), then bias + shift, scale, residual, one rounding.
 #pragma unroll
   for (int i = 0; i < 4; i++) {
-    const float* rw = rows + ((lane >> 3) + 8 * i) * S::RP + g8 * 8;
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(rw), s1 = *reinterpret_cast<const f32x4*>(rw + 4);
+    const int ro = ((lane >> 3) + 8 * i) * S::RP + g8 * 8;
+    const float* r0 = rowp(kg, 0) + ro;
+    const float* r1 = rowp(kg, 1) + ro;
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(r0) + *reinterpret_cast<const f32x4*>(r1);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(r0 + 4) + *reinterpret_cast<const f32x4*>(r1 + 4);
     f16x8 out;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
