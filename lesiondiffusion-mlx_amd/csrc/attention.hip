@@ -757,6 +757,290 @@ static int launch_attn(const AttnParams& p, hipStream_t st) {
   return check_launch("attention");
 }
 
+// Wide heads (D = 128, 256; the VQ decoder's single 256-wide head over 51,200 tokens): a
+// workgroup's 4 waves own 4 x 32 queries and share every K/V tile. Tiles move global->LDS
+// by DMA (rows of D halves, 16-byte chunk c of row r at chunk position c ^ (r mod D/8);
+// K rows permuted by key_row), three deep for K and for V, each wave moving a quarter of
+// each tile; one barrier per key block, after which the slots the previous block freed
+// are refilled. The S^T MFMAs of block it + 1 are issued before block it's softmax, so its
+// VALU work runs under them; the exponent base moves only past a 2^8 margin (as in
+// attention_pipe_kernel).
+template <int D>
+struct AttnWideLds {
+  static constexpr int TB = 32 * D * 2;          // bytes per K or V tile (and per wave's Q block)
+  static constexpr bool QL = D == 256;           // Q fragments read from LDS (registers too few)
+  static constexpr size_t bytes = (QL ? 10 : 6) * (size_t)TB;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1, D == 128 ? 2 : 1)))
+void attention_wide_kernel(AttnParams p) {
+  constexpr int KB = 32;
+  constexpr int DK = D / 16, DB = D / 32, KG = D / 8;
+  constexpr int TB = AttnWideLds<D>::TB;
+  constexpr int NHW = TB / 1024 / 4;          // 1 KB DMA instructions per wave per tile
+  constexpr int RPD = 1024 / (D * 2);         // tile rows per DMA instruction
+  constexpr bool QL = AttnWideLds<D>::QL;
+  static_assert(D == 128 || D == 256, "wide heads");
+  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hf = lane >> 5, col = lane & 31;
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x * per + min(x, rem) + k;
+  }
+  const int nqb = (p.L + 127) / 128;
+  const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
+  const int q0 = qblk * 128 + wave * 32;
+  f16* kbuf = smem;                 // K tiles 0..2, then V tiles 0..2
+  f16* vbuf = smem + 3 * (TB / 2);
+  const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
+
+  const f16* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
+  const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
+  const f16* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+  const int qi = min(q0 + col, p.L - 1);
+  const float* mrow = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi * p.ms2 : nullptr;
+
+  // Q^T fragments: in registers (D = 128), or (D = 256, where O^T alone takes 128
+  // registers) in this wave's LDS block, laid out like a K tile without the row
+  // permutation and read with the K fragments.
+  f16x8 qf[QL ? 1 : DK];
+  if constexpr (!QL) {
+#pragma unroll
+    for (int dk = 0; dk < DK; dk++) qf[dk] = *reinterpret_cast<const f16x8*>(qb_ + (int64_t)qi * p.qs1 + dk * 16 + 8 * hf);
+  }
+  f16* qbuf = smem + 6 * (TB / 2) + wave * (TB / 2);
+  f32x16 o[DB];
+#pragma unroll
+  for (int i = 0; i < DB; i++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[i][e] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  // This wave's DMA instructions of a tile: j = wave * NHW + jj covers rows RPD j ..
+  // + RPD - 1; lane -> row RPD j + lane / KG, chunk position lane % KG.
+  unsigned koff[NHW], voff[NHW];
+#pragma unroll
+  for (int jj = 0; jj < NHW; jj++) {
+    const int R = (wave * NHW + jj) * RPD + lane / KG, c = (lane % KG) ^ (R % KG);
+    koff[jj] = (unsigned)(key_row(R) * p.ks1 + c * 8) * 2u;
+    voff[jj] = (unsigned)(R * p.vs1 + c * 8) * 2u;
+  }
+  const int nblk = (p.LK + KB - 1) / KB;
+  // Block it's tile through a buffer resource that ends at the sequence's last key (none
+  // past it: a block beyond the last reads zeros).
+  auto issue = [&](const f16* base, int64_t rs1, const unsigned (&off)[NHW], unsigned dst_base, int it) {
+    const int kbase = it * KB;
+    const int rows = min(KB, p.LK - kbase);
+    const i32x4 rs = dma_rsrc(rows > 0 ? base + (int64_t)kbase * rs1 : base,
+                              rows > 0 ? (unsigned)(((rows - 1) * rs1 + D) * 2) : 0u);
+    const unsigned dst = dst_base + (unsigned)((it % 3) * TB + wave * NHW * 1024);
+#pragma unroll
+    for (int jj = 0; jj < NHW; jj++) dma_buffer_b128(rs, off[jj], 0, dst + jj * 1024);
+  };
+  auto issue_k = [&](int it) { issue(kb_, p.ks1, koff, kbuf_lds, it); };
+  auto issue_v = [&](int it) { issue(vb_, p.vs1, voff, vbuf_lds, it); };
+
+  // Fragment read addresses, in bytes from the tile base: (lane part + slot base) ^ (a
+  // compile-time constant per k-step, row group and block of dims). K: row col, chunk
+  // position (2 dk + hf) ^ (col mod KG) = (hf ^ col mod KG) ^ 2 dk. V^T (transposing
+  // reads): row vr0 + 16 ks + 4 hi and dims vd0 + 32 db, whose bits are disjoint, so that
+  // row and chunk position each split into a lane part and a constant part by XOR. The lane
+  // parts pass through an empty asm once per block, so that the compiler forms the
+  // addresses at each read instead of keeping every one of them in a register.
+  const int vr0 = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int vd0 = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const unsigned ka_lane = (unsigned)(col * D * 2 + ((hf ^ (col % KG)) << 4));
+  const unsigned va_lane = (unsigned)(2 * D * vr0 + (((vd0 >> 3) ^ (vr0 % KG)) << 4) + 2 * (vd0 & 7));
+  auto kconst = [](int dk) { return (unsigned)(dk << 5); };
+  auto vconst = [](int ks, int hi, int db) {
+    const int rc = 16 * ks + 4 * hi;                         // row bits added to vr0
+    const int cc = (4 * db) ^ (rc % KG);                     // chunk bits added to vd0 / 8
+    return (unsigned)(2 * D * rc) ^ (unsigned)(cc << 4);
+  };
+  const char* kbase_p = reinterpret_cast<const char*>(kbuf);
+  const char* qbase_p = reinterpret_cast<const char*>(qbuf);
+  const char* vbase_p = reinterpret_cast<const char*>(vbuf);
+  // S^T = K Q^T of block it (rows = keys permuted by key_row, columns = queries).
+  // (Operands are read four k-steps at a time, fenced from the scheduler, so that the
+  // fragments in flight stay within the register budget.)
+  auto compute_s = [&](int it, f32x16& s) {
+    unsigned ka = ka_lane + (unsigned)((it % 3) * TB);
+    asm volatile("" : "+v"(ka));
+    s = (f32x16){};
+#pragma unroll
+    for (int g = 0; g < DK; g += 4) {
+      f16x8 kf[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) kf[u] = *reinterpret_cast<const f16x8*>(kbase_p + (ka ^ kconst(g + u)));
+      if constexpr (QL) {
+        f16x8 qg[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) qg[u] = *reinterpret_cast<const f16x8*>(qbase_p + (ka_lane ^ kconst(g + u)));
+#pragma unroll
+        for (int u = 0; u < 4; u++) s = mfma32x(kf[u], qg[u], s);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; u++) s = mfma32x(kf[u], qf[g + u], s);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const f16x2 ones = {(f16)1, (f16)1};
+  constexpr float RB = 8.f;
+  auto softmax_pv = [&](int it, auto full_c, f32x16& s) {
+    constexpr bool FULL = decltype(full_c)::value;
+    unsigned va = va_lane + (unsigned)((it % 3) * TB);
+    float top;
+    if constexpr (FULL) {
+      const float t0 = fmaxf(fmaxf(s[0], s[1]), s[2]), t1 = fmaxf(fmaxf(s[3], s[4]), s[5]);
+      const float t2 = fmaxf(fmaxf(s[6], s[7]), s[8]), t3 = fmaxf(fmaxf(s[9], s[10]), s[11]);
+      const float t4 = fmaxf(fmaxf(s[12], s[13]), s[14]);
+      top = halves_max(fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, s[15]))) * p.c;
+    } else {
+      const int kbase = it * KB;
+      top = -INFINITY;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
+        float t = s[e] * p.c;
+        if (key >= p.LK) t = -INFINITY;
+        else if (mrow) t += mrow[(int64_t)key * p.ms3] * 1.44269504088896341f;
+        s[e] = t;
+        top = fmaxf(top, t);
+      }
+      top = halves_max(top);
+    }
+    // The exponent base moves only when the block raises the query's maximum by more than
+    // RB (log2 units); a query with every key so far removed keeps m = -inf.
+    const float mn = top > m + RB ? top : m;
+    const float base = mn == -INFINITY ? 0.f : mn;
+    const float alpha = __builtin_amdgcn_exp2f(m - base);
+    m = mn;
+    if constexpr (FULL) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) s[e] = s[e] * p.c - base;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; e++) s[e] -= base;
+    }
+    f16x8 pf[2];
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const f16x2 pr = {(f16)__builtin_amdgcn_exp2f(s[e]), (f16)__builtin_amdgcn_exp2f(s[e + 1])};
+      pf[e >> 3][e & 7] = pr[0];
+      pf[e >> 3][(e & 7) + 1] = pr[1];
+      sum = __builtin_amdgcn_fdot2(pr, ones, sum, false);
+    }
+    l = l * alpha + sum;
+    // (Plain multiplies: the accumulators may live in AGPRs, which the rescale reaches
+    // through the compiler's own moves.)
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int db = 0; db < DB; db++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) o[db][e] *= alpha;
+    }
+    asm volatile("" : "+v"(va));
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int g = 0; g < DB; g += 4) {
+        f16x8 vf[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const f16* a0 = reinterpret_cast<const f16*>(vbase_p + (va ^ vconst(ks, 0, g + u)));
+          const f16* a1 = reinterpret_cast<const f16*>(vbase_p + (va ^ vconst(ks, 1, g + u)));
+          const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(a0));
+          const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(a1));
+          vf[u] = __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) o[g + u] = mfma32x(vf[u], pf[ks], o[g + u]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  };
+  // One step: K(it + 1) and V(it) landed in every wave (own wait, then the barrier, which
+  // also retires every read of block it - 1); refill the slots block it - 1 freed, issue
+  // S of block it + 1, then block it's softmax and P V.
+  auto step = [&](int it, auto full_c, f32x16& cur, f32x16& nxt) {
+    vmcnt_wait<2 * NHW>();
+    __syncthreads();
+    issue_k(it + 3);
+    issue_v(it + 2);
+    if (it + 1 < nblk) compute_s(it + 1, nxt);
+    softmax_pv(it, full_c, cur);
+  };
+
+  if constexpr (QL) {
+    // This wave's 32 query rows (rows past the sequence read zeros), 16 DMA instructions.
+    const int rows = min(32, p.L - q0);
+    const i32x4 rs = dma_rsrc(qb_ + (int64_t)q0 * p.qs1, rows > 0 ? (unsigned)(((rows - 1) * p.qs1 + D) * 2) : 0u);
+    const unsigned dst = lds_offset(qbuf);
+#pragma unroll
+    for (int j = 0; j < TB / 1024; j++) {
+      const int R = j * RPD + lane / KG, c = (lane % KG) ^ (R % KG);
+      dma_buffer_b128(rs, (unsigned)(R * p.qs1 + c * 8) * 2u, 0, dst + j * 1024);
+    }
+  }
+  issue_k(0); issue_v(0); issue_k(1); issue_v(1); issue_k(2);
+  vmcnt_wait<0>();
+  __syncthreads();
+  f32x16 sa, sb;
+  if (nblk > 0) compute_s(0, sa);
+  const int nfull = p.mask ? 0 : (p.LK % KB == 0 ? nblk : nblk - 1);
+  using T = std::integral_constant<bool, true>;
+  using F = std::integral_constant<bool, false>;
+  // Pairs of whole blocks, then the rest (at most a whole block and the partial one, or
+  // every block under a mask) through the general softmax, which is exact for whole
+  // blocks too. (A tail that mixed the two instantiations per iteration doubled the live
+  // registers.)
+  int it = 0;
+  for (; it + 1 < nfull; it += 2) {
+    step(it, T(), sa, sb);
+    step(it + 1, T(), sb, sa);
+  }
+  for (; it + 1 < nblk; it += 2) {
+    step(it, F(), sa, sb);
+    step(it + 1, F(), sb, sa);
+  }
+  if (it < nblk) step(it, F(), sa, sb);
+  vmcnt_wait<0>();   // trailing DMAs land before the workgroup's LDS is released
+  l = halves_sum(l);
+  const int qo = q0 + col;
+  if (qo < p.L) {
+    f16* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; db++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        f16x4 out;
+#pragma unroll
+        for (int r = 0; r < 4; r++) out[r] = (f16)(o[db][j * 4 + r] * inv);
+        *reinterpret_cast<f16x4*>(orow + db * 32 + j * 8 + 4 * hf) = out;
+      }
+  }
+}
+
+template <int D>
+static int launch_attn_wide(const AttnParams& p, hipStream_t st) {
+  const int64_t n = (int64_t)((p.L + 127) / 128) * p.H * p.B;
+  if (n > 0x7fffffff) return fail("attention: grid too large");
+  constexpr size_t lds = AttnWideLds<D>::bytes;
+  static_assert(lds <= 160 * 1024, "LDS");
+  auto kern = attention_wide_kernel<D>;
+  if (lds > 65536 &&
+      hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+    return check_launch("attention: set LDS size");
+  hipLaunchKernelGGL(kern, dim3((unsigned)n), dim3(256), lds, st, p);
+  return check_launch("attention (wide heads)");
+}
+
 template <int D>
 static int launch_d(const AttnParams& p, hipStream_t st) {
   // Key-split workgroups when 128-query workgroups would leave most CUs idle: for long
@@ -765,6 +1049,7 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
   const int64_t wgs = (int64_t)((p.L + 127) / 128) * p.H * p.B;
   int split = 1;
   if (const char* env = getenv("LDX_ATTN_SPLIT")) split = atoi(env);
+  else if (D == 128 && wgs >= 256) split = -1;   // enough 128-query workgroups to fill the CUs
   else if (D <= 128 && wgs < 512 && p.LK > 64)
     split = (D == 32 || D == 64) && p.LK >= 512 ? -4 : (D <= 64 && p.LK >= 512) ? 8 : 4;
   if constexpr (D == 32 || D == 64) {
@@ -778,6 +1063,11 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
   }
   if constexpr (D <= 128) {
     if (split == 4 || split == 8) return launch_attn<D, 4>(p, st);
+  }
+  if constexpr (D == 128 || D == 256) {
+    // Wide heads with 128-query workgroups: the DMA-fed pipelined kernel by default
+    // (LDX_ATTN_SPLIT=-1 forces it, =1 keeps the register-staged one).
+    if (split == -1 || (split == 1 && getenv("LDX_ATTN_SPLIT") == nullptr)) return launch_attn_wide<D>(p, st);
   }
   return launch_attn<D, 1>(p, st);
 }

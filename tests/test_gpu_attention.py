@@ -121,3 +121,34 @@ def test_attention_key_split_variants_match_float64(pkg, dev, monkeypatch, split
     act = host(out)
     np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
     assert_fp16_bar(act, exp)
+
+
+@pytest.mark.parametrize("split", ["default", "1", "-1"])
+@pytest.mark.parametrize(("b", "h", "lq", "lk", "d", "masked", "mag"), [
+    (1, 1, 300, 300, 256, False, 1.0),   # VQ mid-attention width, ragged query and key blocks
+    (2, 2, 129, 77, 128, True, 1.0),     # additive mask, one query past a 128-query block
+    (1, 1, 70, 1000, 256, False, 3.0),   # many key blocks, peaked rows (base moves)
+    (1, 2, 256, 96, 128, False, 1.0),    # whole blocks only
+])
+def test_attention_wide_heads_match_float64(pkg, dev, monkeypatch, split, b, h, lq, lk, d, masked, mag) -> None:
+    """Head widths 128 and 256: the launcher's choice, the register-staged 128-query
+    kernel (LDX_ATTN_SPLIT=1) and the DMA-fed pipelined one (=-1) against float64
+    softmax attention."""
+    if split == "default":
+        monkeypatch.delenv("LDX_ATTN_SPLIT", raising=False)
+    else:
+        monkeypatch.setenv("LDX_ATTN_SPLIT", split)
+    rng = np.random.default_rng(lq + 7 * lk + d)
+    q, k = ((rng.normal(size=(b, h, n, d)) * mag).astype(np.float16) for n in (lq, lk))
+    v = rng.normal(size=(b, h, lk, d)).astype(np.float16)
+    m_host = m_dev = None
+    if masked:
+        m_host = rng.normal(size=(b, 1, lq, lk)).astype(np.float32)
+        m_host[..., 3:7] = -np.inf
+        m_dev = to_dev(m_host, dev)
+    out = pkg.ops.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), d ** -0.5, m_dev)
+    torch.cuda.synchronize()
+    exp = oatt.attention(q, k, v, d ** -0.5, m_host)
+    act = host(out)
+    np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
+    assert_fp16_bar(act, exp)
