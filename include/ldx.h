@@ -94,6 +94,16 @@ typedef struct ldx_conv3d_args {
 size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* args);
 int ldx_conv3d(const ldx_conv3d_args* args, void* stream);
 
+/* A pointwise conv (dense layer: ksize 1, one input, no affine / SiLU, c0 a multiple of 16
+ * and at most 512) whose input rows are first layer-normalized over their c0 channels:
+ * x' = half((x - mean) * rsqrt(var + eps) * gamma[c] + beta[c]) with fp32 row statistics
+ * (mean, then the mean squared deviation), then ldx_conv3d's product and epilogue on x'.
+ * One launch for the reference's LayerNorm followed by its dense layer
+ * (mlx_model.py:541-548: norm1 -> attn1 q/k/v, norm2 -> attn2 to_q, norm3 -> ff); gamma
+ * and beta are fp32 (c0), 16-byte aligned. */
+int ldx_dense_ln(const ldx_conv3d_args* args, const float* gamma, const float* beta, float eps,
+                 void* stream);
+
 /* Pack a Torch-layout fp16 weight (O, C, K, K, K) (K = 3 or 1; a dense (O, C)
  * weight is K = 1) into the kernel's fragment-major layout of
  * ldx_packed_weight_elems(O, C, K, 0) halves: with NOB = 4*ceil(O/128), NKC =

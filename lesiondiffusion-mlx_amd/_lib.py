@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_abi_version": (c_i32, []),
     "ldx_conv3d_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(ConvArgs)]),
     "ldx_conv3d": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
+    "ldx_dense_ln": (c_i32, [ctypes.POINTER(ConvArgs), c_vp, c_vp, c_f32, c_vp]),
     "ldx_packed_weight_elems": (ctypes.c_size_t, [c_i32, c_i32, c_i32, c_i32]),
     "ldx_pack_weight": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "ldx_pack_upsample_weight": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),

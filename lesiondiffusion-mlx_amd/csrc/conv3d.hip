@@ -62,6 +62,9 @@ struct ConvParams {
   int nh;                  // planned halo: register slots per thread (0: generic staging loop)
   int stg_off;             // > 0: LDS offset (floats) of the epilogue staging, past the halo
   int nob, nbr;            // output-channel blocks of the workgroup tile; bricks per batch item
+  const float* ln_g;       // dense_ksplit with LayerNorm: per-channel gamma, beta and eps
+  const float* ln_b;
+  float ln_eps;
   UDiv dv_nob, dv_nbr, dv_split, dv_nbw, dv_nbh;  // division by nob, nbr, split, NBW, NBH
 };
 
@@ -820,7 +823,11 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
 // dependent chain per wave, all of its operands requested up front), then add their
 // partial sums through LDS in a fixed order (waves 1, 2, 3 into wave 0), which finishes
 // the epilogue.
-template <int FO, int FV>
+// LN: the input rows are layer-normalized first (ldx_dense_ln; one 32 x 32 tile, C <= 512
+// so that every k-step of a wave is in registers at once): row mean, then the mean squared
+// deviation (two passes, as the standalone LayerNorm kernel), summed per lane, lane pair
+// and wave, then fp16((x - mean) * rstd * gamma + beta) as the B operand.
+template <int FO, int FV, bool LN = false>
 __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
   constexpr int BO = FO * 32, BV = FV * 32;
   constexpr int PD = 8;                       // k-steps of operands in flight per wave
@@ -905,26 +912,81 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
+  float* red = reinterpret_cast<float*>(smem);
+  if constexpr (LN) {
+    static_assert(FO == 1 && FV == 1, "LayerNorm dense: one 32 x 32 tile");
+    const int nks = ke - kb;   // <= PD (the host bounds C)
 #pragma unroll
-  for (int j = 0; j < PD - 1; j++)
-    if (kb + j < ke) load(j, kb + j);
-  for (int kc0 = kb; kc0 < ke; kc0 += PD) {
+    for (int j = 0; j < PD; j++)
+      if (j < nks) load(j, kb + j);
+    // gamma and beta of the whole row into LDS (read back after the first barrier): kept
+    // out of registers, so that four waves per SIMD still fit.
+    float* lnr = red + 3 * PART + 32 * EPW;   // [2][4 waves][32 rows], then gamma, beta
+    float* lng = lnr + 256;
+    for (int i = threadIdx.x; i < p.C / 4; i += 256) {
+      *reinterpret_cast<f32x4*>(lng + 4 * i) = *reinterpret_cast<const f32x4*>(p.ln_g + 4 * i);
+      *reinterpret_cast<f32x4*>(lng + 512 + 4 * i) = *reinterpret_cast<const f32x4*>(p.ln_b + 4 * i);
+    }
+    const int col = lane & 31;
+    float sm = 0.f;
 #pragma unroll
-    for (int j = 0; j < PD; j++) {
-      const int kc = kc0 + j;
-      if (kc < ke) {
-        if (kc + PD - 1 < ke) load((j + PD - 1) % PD, kc + PD - 1);
-        prep(j, kc);
+    for (int j = 0; j < PD; j++)
+      if (j < nks)
 #pragma unroll
-        for (int fo = 0; fo < FO; fo++)
+        for (int e = 0; e < 8; e++) sm += (float)rb[j][0][e];
+    sm += __shfl_xor(sm, 32);
+    if (hf == 0) lnr[wave * 32 + col] = sm;
+    __syncthreads();
+    const float mean = (((lnr[col] + lnr[32 + col]) + lnr[64 + col]) + lnr[96 + col]) / (float)p.C;
+    float sq = 0.f;
 #pragma unroll
-          for (int fv = 0; fv < FV; fv++) acc[fo][fv] = mfma32(ra[j][fo], rb[j][fv], acc[fo][fv]);
+    for (int j = 0; j < PD; j++)
+      if (j < nks)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float dv = (float)rb[j][0][e] - mean;
+          sq += dv * dv;
+        }
+    sq += __shfl_xor(sq, 32);
+    if (hf == 0) lnr[128 + wave * 32 + col] = sq;
+    __syncthreads();
+    const float var = (((lnr[128 + col] + lnr[160 + col]) + lnr[192 + col]) + lnr[224 + col]) / (float)p.C;
+    const float rstd = 1.0f / sqrtf(var + p.ln_eps);
+#pragma unroll
+    for (int j = 0; j < PD; j++)
+      if (j < nks) {
+        const int c = (kb + j) * 16 + hf * 8;
+        const f32x4 g0 = *reinterpret_cast<const f32x4*>(lng + c), g1 = *reinterpret_cast<const f32x4*>(lng + c + 4);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(lng + 512 + c);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(lng + 512 + c + 4);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          rb[j][0][e] = (f16)(((float)rb[j][0][e] - mean) * rstd * g0[e] + b0[e]);
+          rb[j][0][e + 4] = (f16)(((float)rb[j][0][e + 4] - mean) * rstd * g1[e] + b1[e]);
+        }
+        acc[0][0] = mfma32(ra[j][0], rb[j][0], acc[0][0]);
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < PD - 1; j++)
+      if (kb + j < ke) load(j, kb + j);
+    for (int kc0 = kb; kc0 < ke; kc0 += PD) {
+#pragma unroll
+      for (int j = 0; j < PD; j++) {
+        const int kc = kc0 + j;
+        if (kc < ke) {
+          if (kc + PD - 1 < ke) load((j + PD - 1) % PD, kc + PD - 1);
+          prep(j, kc);
+#pragma unroll
+          for (int fo = 0; fo < FO; fo++)
+#pragma unroll
+            for (int fv = 0; fv < FV; fv++) acc[fo][fv] = mfma32(ra[j][fo], rb[j][fv], acc[fo][fv]);
+        }
       }
     }
   }
 
   // Partial sums of waves 1..3 -> LDS (lane-major), then wave 0 adds them in order.
-  float* red = reinterpret_cast<float*>(smem);
   if (wave > 0) {
 #pragma unroll
     for (int fo = 0; fo < FO; fo++)
@@ -1269,7 +1331,7 @@ static int launch_dense(ConvParams p, hipStream_t st) {
   return check_launch("conv3d: pointwise");
 }
 
-template <int FO, int FV>
+template <int FO, int FV, bool LN = false>
 static int launch_dense_ksplit(ConvParams p, hipStream_t st) {
   constexpr int BO = FO * 32, BV = FV * 32;
   const int NV = p.D * p.H * p.W;
@@ -1283,8 +1345,8 @@ static int launch_dense_ksplit(ConvParams p, hipStream_t st) {
   p.part = nullptr;
   const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
   if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
-  const size_t lds = (size_t)(3 * FO * FV * 1024 + 32 * (FO * 32 + 4)) * sizeof(float);
-  hipLaunchKernelGGL((dense_ksplit_kernel<FO, FV>), dim3((unsigned)nwg), dim3(256), lds, st, p);
+  const size_t lds = (size_t)(3 * FO * FV * 1024 + 32 * (FO * 32 + 4) + (LN ? 256 + 1024 : 0)) * sizeof(float);
+  hipLaunchKernelGGL((dense_ksplit_kernel<FO, FV, LN>), dim3((unsigned)nwg), dim3(256), lds, st, p);
   return check_launch("conv3d: pointwise (k-split)");
 }
 
@@ -1360,4 +1422,26 @@ extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
   const unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
   hipLaunchKernelGGL(conv_reduce_kernel, dim3(blocks), dim3(256), 0, st, p, nvox);
   return check_launch("conv3d: split reduce");
+}
+
+extern "C" int ldx_dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps,
+                            void* stream) {
+  if (!a || !gamma || !beta) return fail("dense_ln: null pointer");
+  if (a->ksize != 1 || a->c1 != 0 || a->affine || a->silu || a->stride != 1 || a->upsample)
+    return fail("dense_ln: a pointwise conv of one input without affine or SiLU");
+  if (a->c0 % 16 || a->c0 > 512) return fail("dense_ln: C = %d must be a multiple of 16, at most 512", a->c0);
+  if ((uintptr_t)gamma % 16 || (uintptr_t)beta % 16) return fail("dense_ln: gamma and beta must be 16-byte aligned");
+  if (!(eps > 0.f)) return fail("dense_ln: eps must be positive");
+  ConvParams p;
+  Tile t;
+  size_t lds;
+  bool vec;
+  int64_t ws = 0;
+  int rc = plan_conv(a, p, t, lds, vec, ws);
+  if (rc != LDX_OK) return rc;
+  if (!use_dense(a, vec)) return fail("dense_ln: input rows must be 16-byte aligned channel groups");
+  p.ln_g = gamma;
+  p.ln_b = beta;
+  p.ln_eps = eps;
+  return launch_dense_ksplit<1, 1, true>(p, as_stream(stream));
 }

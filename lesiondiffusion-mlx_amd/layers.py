@@ -84,8 +84,17 @@ class SourceLayers:
                               output_scale=output_scale)
 
     def dense(self, x: torch.Tensor, key: str, *, residual: torch.Tensor | None = None,
-              act: str | None = None, affine: torch.Tensor | None = None) -> torch.Tensor:
-        """Linear layer on the last axis, one rounding (mlx_model.py:204-217)."""
+              act: str | None = None, affine: torch.Tensor | None = None,
+              ln: str | None = None, ln_eps: float = 1e-5) -> torch.Tensor:
+        """Linear layer on the last axis, one rounding (mlx_model.py:204-217); ``ln`` names
+        a LayerNorm applied to ``x`` first -- fused into the same launch when the width
+        allows (a multiple of 16, at most 512 channels), else as its own kernel."""
+        if ln is not None:
+            c = int(x.shape[-1])
+            if affine is None and c % 16 == 0 and c <= 512:
+                return ops.dense(x, self.packed[key], self.bias32.get(key), residual=residual, act=act,
+                                 ln=(self.vec32[ln + ".weight"], self.vec32[ln + ".bias"], ln_eps))
+            x = self.layer_norm(x, ln, ln_eps)
         return ops.dense(x, self.packed[key], self.bias32.get(key), residual=residual, act=act, affine=affine)
 
     def norm_affine(self, x: torch.Tensor, key: str, *, groups: int, eps: float,

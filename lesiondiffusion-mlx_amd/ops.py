@@ -177,13 +177,15 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
                upsample: bool = False, output_scale: float = 1.0,
                residual: torch.Tensor | None = None, x1: torch.Tensor | None = None,
                act: str | None = None, out: torch.Tensor | None = None,
-               shift: torch.Tensor | None = None) -> torch.Tensor:
+               shift: torch.Tensor | None = None,
+               ln: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
     """Fused conv of NDHWC ``x`` (optionally ``concat([x, x1], channels)``) with a packed
     weight: ``half((conv(prep(x)) + bias + shift) * output_scale + residual)``, ``prep`` =
     the per-(b, c) ``affine`` then SiLU, rounded to fp16 once (nax_conv3d,
     _nax_conv.py:451-500). ``shift`` is an fp16 ``(B, O)`` per-batch term (a row slice of
     a wider tensor is fine). ``act="gelu"`` / ``"silu"`` additionally stores
-    ``half(act(y))``.
+    ``half(act(y))``. ``ln = (gamma, beta, eps)`` (pointwise convs of one input only)
+    layer-normalizes each input row first, in the same launch (ldx_dense_ln).
 
     Returns NDHWC ``(B, D', H', W', O)`` fp16 (written into ``out`` when given, which may
     be a channel slice of a wider tensor).
@@ -260,6 +262,14 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     if ws_bytes:
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+    if ln is not None:
+        gamma, beta, eps = ln
+        for t, name in ((gamma, "ln gamma"), (beta, "ln beta")):
+            if t.dtype != torch.float32 or not t.is_cuda or t.numel() != c0 or not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous device float32 with {c0} values")
+        check(lib.ldx_dense_ln(ctypes.byref(a), gamma.data_ptr(), beta.data_ptr(), float(eps), _stream()),
+              "dense_ln")
+        return out
     check(lib.ldx_conv3d(ctypes.byref(a), _stream()), "conv3d")
     return out
 
@@ -278,9 +288,11 @@ def conv3d(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
 
 def dense(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = None, *,
           residual: torch.Tensor | None = None, act: str | None = None,
-          out: torch.Tensor | None = None, affine: torch.Tensor | None = None) -> torch.Tensor:
+          out: torch.Tensor | None = None, affine: torch.Tensor | None = None,
+          ln: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
     """``half(x @ W^T + bias (+ residual))`` over the last axis of fp16 ``x`` with fp32
-    accumulation and one rounding (SourceLayers.dense native path, mlx_model.py:204-217)."""
+    accumulation and one rounding (SourceLayers.dense native path, mlx_model.py:204-217).
+    ``ln = (gamma, beta, eps)`` applies ``layer_norm`` to ``x`` first, in the same launch."""
     if packed.ksize != 1:
         raise ValueError("dense needs a (O, C) weight packed with pack_weight")
     lead = x.shape[:-1]
@@ -288,7 +300,7 @@ def dense(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = Non
     x5 = x.reshape(1, 1, 1, rows, x.shape[-1])
     r5 = None if residual is None else residual.reshape(1, 1, 1, rows, packed.out_channels)
     o5 = None if out is None else out.reshape(1, 1, 1, rows, packed.out_channels)
-    y = nax_conv3d(x5, packed, bias, residual=r5, act=act, out=o5, affine=affine)
+    y = nax_conv3d(x5, packed, bias, residual=r5, act=act, out=o5, affine=affine, ln=ln)
     return y.reshape(*lead, packed.out_channels)
 
 

@@ -97,13 +97,15 @@ class LdmUnet(SourceLayers):
                                    groups=groups_for(h.shape[-1]), eps=1e-5, residual=skip)
 
     def _attend(self, tok: torch.Tensor, att: str, heads: int, kv: tuple[torch.Tensor, torch.Tensor] | None,
-                residual: torch.Tensor) -> torch.Tensor:
+                residual: torch.Tensor, ln: str) -> torch.Tensor:
+        """``residual + attention(layer_norm(tok, ln))``; the LayerNorm runs inside the
+        q/k/v (or to_q) dense layer's launch."""
         c = tok.shape[-1]
         if kv is None:
-            qkv = self.dense(tok, att + ".qkv")
+            qkv = self.dense(tok, att + ".qkv", ln=ln)
             q, k, v = qkv[..., :c], qkv[..., c:2 * c], qkv[..., 2 * c:]
         else:
-            q = self.dense(tok, att + ".to_q")
+            q = self.dense(tok, att + ".to_q", ln=ln)
             k, v = kv
         o = ops.flash_attention(q, k, v, heads=heads, scale=(c // heads) ** -0.5)
         return self.dense(o, att + ".to_out.0", residual=residual)
@@ -116,12 +118,12 @@ class LdmUnet(SourceLayers):
         tok = self.conv(x, key + ".proj_in", affine=aff).view(b, d * h * w, c)
         heads = c // self.config.num_head_channels
         blk = key + ".transformer_blocks.0"
-        tok = self._attend(self.layer_norm(tok, blk + ".norm1"), blk + ".attn1", heads, None, tok)
+        tok = self._attend(tok, blk + ".attn1", heads, None, tok, blk + ".norm1")
         kv = None if context_kv is None else context_kv.get(blk + ".attn2")
         if kv is None and not self.config.skip_context and context_kv is not None:
             raise ValueError(f"missing projected context for {blk}.attn2")
-        tok = self._attend(self.layer_norm(tok, blk + ".norm2"), blk + ".attn2", heads, kv, tok)
-        ff = self.dense(self.layer_norm(tok, blk + ".norm3"), blk + ".ff.net.0.0", act="gelu")
+        tok = self._attend(tok, blk + ".attn2", heads, kv, tok, blk + ".norm2")
+        ff = self.dense(tok, blk + ".ff.net.0.0", act="gelu", ln=blk + ".norm3")
         tok = self.dense(ff, blk + ".ff.net.2", residual=tok)
         return self.conv(tok.view(b, d, h, w, c), key + ".proj_out", residual=x)
 

@@ -287,3 +287,41 @@ def test_dense_rounds_once_and_fuses_gelu(pkg, dev) -> None:
     assert np.all(np.abs(yy - expected) <= half_spacing(expected) + ACCUMULATION_EPS * mag)
     want = onm.gelu(yy)  # GELU of the stored half value, rounded once more
     assert np.all(np.abs(host(g) - want) <= half_spacing(want) * 1.001 + 1e-7)
+
+
+@pytest.mark.parametrize(("rows", "c", "o", "act", "with_res"), [
+    (800, 256, 768, None, False),    # LINet level-2 norm1 -> q/k/v
+    (100, 256, 1024, "gelu", False),  # level-3 norm3 -> feed-forward with GELU
+    (37, 512, 64, None, True),        # widest fused LayerNorm, ragged row block, residual
+    (5, 16, 32, None, False),         # one k-step in total
+])
+def test_dense_layer_norm_matches_float64(pkg, dev, rows, c, o, act, with_res) -> None:
+    """ldx_dense_ln: LayerNorm of each row (mlx_model.py:360-367) then the dense layer in
+    one launch, against float64 (LayerNorm, one fp16 rounding of its output, product), and
+    against the two separate kernels."""
+    rng = np.random.default_rng(rows + c + o)
+    x = (rng.normal(size=(1, rows, c)) * 2 + 0.5).astype(np.float16)
+    g = rng.normal(size=c).astype(np.float32)
+    bb = rng.normal(size=c).astype(np.float32)
+    w = (rng.normal(size=(o, c)) / np.sqrt(c)).astype(np.float16)
+    bias = rng.normal(size=(o,)).astype(np.float16)
+    res = rng.normal(size=(1, rows, o)).astype(np.float16) if with_res else None
+    pk = pkg.ops.pack_weight(to_dev(w, dev))
+    gd, bd = to_dev(g, dev), to_dev(bb, dev)
+    xd = to_dev(x, dev)
+    rd = to_dev(res, dev) if with_res else None
+    y = pkg.ops.dense(xd, pk, to_dev(bias, dev), residual=rd, act=act, ln=(gd, bd, 1e-5))
+    sep = pkg.ops.dense(pkg.ops.layer_norm(xd, gd, bd, 1e-5), pk, to_dev(bias, dev), residual=rd, act=act)
+    torch.cuda.synchronize()
+    xn = onm.layer_norm(x.astype(np.float64), g, bb, 1e-5)
+    w64 = w.astype(np.float64)
+    pre = xn @ w64.T + bias.astype(np.float64) + (res.astype(np.float64) if with_res else 0)
+    expected = onm.gelu(pre) if act == "gelu" else pre
+    # one fp16 rounding of the normalized input (2^-11 relative each, 2^-10 allowed for the
+    # fused statistics' summation order), the accumulation, one rounding of the output
+    mag = np.abs(xn) @ np.abs(w64).T
+    bound = 2 * half_spacing(expected) + 2.0 ** -10 * mag + ACCUMULATION_EPS * (mag + np.abs(pre))
+    yy = host(y)
+    assert np.all(np.isfinite(yy))
+    assert np.all(np.abs(yy - expected) <= bound)
+    assert np.all(np.abs(yy - host(sep)) <= bound)
