@@ -1308,7 +1308,8 @@ extern "C" size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* a) {
   if (plan_conv(a, p, t, lds, vec, ws) != LDX_OK) return 0;
   if (use_dense(a, vec)) return 0;
   StreamParams sp;
-  if (conv3d_stream_plan(a, &sp)) return 0;
+  if (conv3d_stream_plan(a, &sp, false))
+    return sp.split > 1 ? (size_t)sp.split * (size_t)p.B * p.OD * p.OH * p.OW * p.O * sizeof(float) : 0;
   return (size_t)ws;
 }
 
@@ -1392,7 +1393,19 @@ extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
   if (use_dense(a, vec)) return run_dense(p, as_stream(stream));
   {
     StreamParams sp;
-    if (conv3d_stream_plan(a, &sp)) return conv3d_stream_launch(sp, as_stream(stream));
+    if (conv3d_stream_plan(a, &sp)) {
+      rc = conv3d_stream_launch(sp, as_stream(stream));
+      if (rc != LDX_OK || sp.split == 1) return rc;
+      // Split over channel chunks: the same fixed-order reduce and epilogue as the general
+      // kernel's split-K.
+      p.split = sp.split;
+      p.part = sp.part;
+      const int64_t nvox = (int64_t)p.B * p.OD * p.OH * p.OW;
+      const int64_t n = nvox * p.O;
+      const unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+      hipLaunchKernelGGL(conv_reduce_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), p, nvox);
+      return check_launch("conv3d (streamed): split reduce");
+    }
   }
   if (p.split > 1 && (!a->workspace || a->workspace_bytes < (size_t)ws)) {
     // No (or too small a) workspace: one pass over all channels.

@@ -13,7 +13,10 @@ struct StreamParams {
   int NKC;                  // 16-channel k-steps of the packed weight's row
   int bo, TD, TH, TW;       // output tile and brick
   int NBD, NBH, NBW, nob, nbr;
-  UDiv dv_nob, dv_nbr, dv_nbw, dv_nbh;
+  UDiv dv_nob, dv_nbr, dv_nbw, dv_nbh, dv_g1;
+  int split, cps;           // split-K: workgroup ranges of cps channel chunks (split > 1)
+  int g1;                   // workgroups per split: bricks x output blocks x batch items
+  float* part;              // split > 1: fp32 partial sums [split][B * D * H * W][O]
   const f16* x0; int64_t x0p;
   const f16* x1; int64_t x1p;
   const f16* w;
@@ -25,8 +28,10 @@ struct StreamParams {
   f16* y; int64_t yp;
 };
 
-// True (and *p planned) when the streamed kernel takes this conv.
-bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* p);
+// True (and *p planned) when the streamed kernel takes this conv. A plan that splits the
+// reduction over channel chunks (p->split > 1) needs split * voxels * O floats of
+// workspace: with check_ws, a conv whose caller passed less is not taken.
+bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* p, bool check_ws = true);
 int conv3d_stream_launch(StreamParams& p, hipStream_t st);
 
 }  // namespace ldx

@@ -115,6 +115,12 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
     wg = x * per + min(x, rem) + k;   // XCD x's range starts at x * per + min(x, rem)
   }
+  // Split-K (the slowest index, so that each XCD's contiguous range shares one chunk range):
+  // workgroup ranges of cps channel chunks.
+  const int sk = p.split > 1 ? udiv(wg, p.dv_g1) : 0;
+  wg -= sk * p.g1;
+  const int cb = sk * p.cps;
+  const int ce = min(p.nchunk, cb + p.cps);
   const int q1 = udiv(wg, p.dv_nob);
   const int oblk = wg - q1 * p.nob;
   const int b = udiv(q1, p.dv_nbr);
@@ -146,7 +152,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // after them and drain those too); halo_store runs after an explicit wait.
   auto halo_issue = [&](int ch) {
     const int c0 = ch * CC;
-    const bool live = c0 < p.C;
+    const bool live = ch < ce;
     const bool in0 = c0 < p.C0;
     const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
     const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
@@ -213,10 +219,11 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       dq[r] = q * 16u;
     }
   }
-  // Chunk ch's halo into buffer buf: NR DMAs per thread (a chunk past the last reads zeros).
+  // Chunk ch's halo into buffer buf: NR DMAs per thread (a chunk past this workgroup's
+  // range reads zeros).
   auto halo_dma = [&](int ch, int buf) {
     const int c0 = ch * CC;
-    const bool live = c0 < p.C;
+    const bool live = ch < ce;
     const bool in0 = c0 < p.C0;
     const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
     const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
@@ -296,21 +303,22 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
 
   // Prologue: chunk 0's halo and the first three weight stages, one wait, then stage 0's
   // first operands.
-  if constexpr (XF) halo_issue(0);
-  else halo_dma(0, 0);
-  issue_stage(0);
-  issue_stage(1);
-  issue_stage(2);
-  vmcnt_wait<2 * S::LW>();   // halo 0 and stage 0 landed (stages 1, 2 may be pending)
-  if constexpr (XF) halo_store(0);
+  const int g0 = cb * NSTG;
+  if constexpr (XF) halo_issue(cb);
+  else halo_dma(cb, cb & 1);
+  issue_stage(g0);
+  issue_stage(g0 + 1);
+  issue_stage(g0 + 2);
+  vmcnt_wait<2 * S::LW>();   // the first halo and stage landed (the next two may be pending)
+  if constexpr (XF) halo_store(cb & 1);
   __syncthreads();
 #pragma unroll
   for (int kw = 0; kw < 3; kw++) {
-    load_a(kw, aptr);
-    load_b(kw, 0, 0, smem);
+    load_a(kw, aptr + (g0 % NSLOT) * S::STAGE);
+    load_b(kw, 0, 0, smem + (cb & 1) * S::HALOP);
   }
 
-  for (int ch = 0; ch < p.nchunk; ch++) {
+  for (int ch = cb; ch < ce; ch++) {
     const char* hb = smem + (ch & 1) * S::HALOP;
     const char* hb_next = smem + ((ch + 1) & 1) * S::HALOP;
 #pragma unroll
@@ -322,7 +330,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       mfma_tap(0);
       mfma_tap(1);
       if constexpr (XF) {
-        if (t == NSTG - 1 && ch + 1 < p.nchunk) {
+        if (t == NSTG - 1 && ch + 1 < ce) {
           // The next chunk's halo, requested at stage HS, into the other buffer (last read
           // in chunk ch - 1); younger than it are the stages issued since.
           vmcnt_wait<(NSTG - 2 - HS) * S::LW>();
@@ -387,15 +395,16 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
   f16x8 sv = {};
   f16x8 res[4];
-  if (p.bias) {
+  if (p.bias && p.split == 1) {
     const float* bias = p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o8;
     bv0 = *reinterpret_cast<const f32x4*>(bias);
     bv1 = *reinterpret_cast<const f32x4*>(bias + 4);
   }
-  if (p.shift) sv = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o8);
+  if (p.shift && p.split == 1) sv = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o8);
 #pragma unroll
   for (int i = 0; i < 4; i++)
-    res[i] = p.res && okr[i] ? *reinterpret_cast<const f16x8*>(p.res + ovr[i] * p.resp + o8) : (f16x8){};
+    res[i] = p.res && p.split == 1 && okr[i] ? *reinterpret_cast<const f16x8*>(p.res + ovr[i] * p.resp + o8)
+                                             : (f16x8){};
   // Both K-groups leave their partial sums as fp32 rows, [w4][fv][group][voxel][channel]
   // (rows padded to RP floats: 16-byte writes free of bank conflicts).
   float* rowsb = reinterpret_cast<float*>(smem);
@@ -410,7 +419,8 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
         *reinterpret_cast<f32x4*>(rowp(fv, kg) + col * S::RP + fo * 32 + 8 * j + 4 * hf) = v;
       }
   __syncthreads();
-  // Rows fv = kg: (group 0 + group 1), then bias + shift, scale, residual, one rounding.
+  // Rows fv = kg: (group 0 + group 1), then bias + shift, scale, residual, one rounding --
+  // or, split over channel chunks, the fp32 sums of this range (the reduce finishes them).
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int ro = ((lane >> 3) + 8 * i) * S::RP + g8 * 8;
@@ -418,6 +428,14 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     const float* r1 = rowp(kg, 1) + ro;
     const f32x4 s0 = *reinterpret_cast<const f32x4*>(r0) + *reinterpret_cast<const f32x4*>(r1);
     const f32x4 s1 = *reinterpret_cast<const f32x4*>(r0 + 4) + *reinterpret_cast<const f32x4*>(r1 + 4);
+    if (p.split > 1) {
+      if (okr[i]) {
+        float* prow = p.part + ((int64_t)sk * p.B * vol + ovr[i]) * p.O + o8;
+        *reinterpret_cast<f32x4*>(prow) = s0;
+        *reinterpret_cast<f32x4*>(prow + 4) = s1;
+      }
+      continue;
+    }
     f16x8 out;
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -437,8 +455,10 @@ static int launch(StreamParams& p, hipStream_t st) {
   p.NBW = (p.W + TW - 1) / TW;
   const int64_t nbr = (int64_t)p.NBD * p.NBH * p.NBW;
   const int64_t nwg = nbr * p.nob * p.B;
-  if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
+  if (nwg * p.split > 0x7fffffff) return fail("conv3d: grid too large");
   p.nbr = (int)nbr;
+  p.g1 = (int)nwg;
+  p.dv_g1 = make_udiv((unsigned)p.g1);
   p.dv_nob = make_udiv((unsigned)p.nob);
   p.dv_nbr = make_udiv((unsigned)p.nbr);
   p.dv_nbw = make_udiv((unsigned)p.NBW);
@@ -447,7 +467,7 @@ static int launch(StreamParams& p, hipStream_t st) {
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS) !=
       hipSuccess)
     return check_launch("conv3d (streamed): set LDS size");
-  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(NT), S::LDS, st, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)(nwg * p.split)), dim3(NT), S::LDS, st, p);
   return check_launch("conv3d (streamed)");
 }
 
@@ -469,7 +489,7 @@ static int64_t brick_cost(const StreamParams& p, const Brick& k, int64_t* halo) 
 }  // namespace cs
 
 // Eligibility, tile and brick choice: false leaves the conv to conv3d_kernel.
-bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out) {
+bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out, bool check_ws) {
   using namespace cs;
   if (const char* env = getenv("LDX_CONV_STREAM"))
     if (atoi(env) == 0) return false;
@@ -506,27 +526,51 @@ bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out) {
   // Among the tiles that launch at least 200 workgroups: the fewest launched voxel slots
   // (partial-brick waste), then the fewest halo voxels per output, then 128-channel tiles
   // (half the halo traffic per output channel).
-  // LDX_CONV_STREAM_MIN_WG lowers the fill threshold (tests use it to run small shapes
-  // through this kernel).
+  // LDX_CONV_STREAM_MIN_WG sets the fill threshold (tests use it to run small shapes
+  // through this kernel) and, when set, also admits tiles whose workgroups, split over
+  // ranges of channel chunks, reach about that many -- provided their bricks waste at
+  // most a quarter of the launched voxels. (Split-K is not the default: on the UNet's
+  // 16x20x20 level, 128 -> 128 channels, it measured 23.9 us with its reduce against
+  // 16.2 us for the general kernel; every workgroup repays the fixed prologue and
+  // epilogue for one or two chunks, and the fp32 partials cost a second pass.)
   int64_t min_wg = 200;
-  if (const char* env = getenv("LDX_CONV_STREAM_MIN_WG")) min_wg = atoll(env);
-  int64_t best_slots = INT64_MAX, best_halo = INT64_MAX;
-  p.bo = 0;
-  for (int bo : {128, 64}) {
-    if (p.O % bo) continue;
-    const Brick* list = bo == 128 ? kBricks128 : kBricks64;
-    const int bv = bo == 128 ? 128 : 256;
-    for (int i = 0; i < (bo == 128 ? 1 : 2); i++) {
-      int64_t halo;
-      const int64_t nb = brick_cost(p, list[i], &halo);
-      if (nb * p.B * (p.O / bo) < min_wg) continue;
-      const int64_t slots = nb * bv;
-      const int64_t hpo = halo * 4096 / ((int64_t)bv * bo);
-      if (slots < best_slots || (slots == best_slots && hpo < best_halo)) {
-        best_slots = slots; best_halo = hpo; p.bo = bo;
-        p.TD = list[i].TD; p.TH = list[i].TH; p.TW = list[i].TW;
+  int passes = 1;
+  if (const char* env = getenv("LDX_CONV_STREAM_MIN_WG")) { min_wg = atoll(env); passes = 2; }
+  const int64_t nvox = (int64_t)p.B * vol;
+  for (int pass = 0; pass < passes && p.bo == 0; pass++) {
+    int64_t best_slots = INT64_MAX, best_halo = INT64_MAX;
+    for (int bo : {128, 64}) {
+      if (p.O % bo) continue;
+      const Brick* list = bo == 128 ? kBricks128 : kBricks64;
+      const int bv = bo == 128 ? 128 : 256;
+      for (int i = 0; i < (bo == 128 ? 1 : 2); i++) {
+        int64_t halo;
+        const int64_t nb = brick_cost(p, list[i], &halo);
+        const int64_t g1 = nb * p.B * (p.O / bo);
+        int split = 1, cps = p.nchunk;
+        if (pass == 0) {
+          if (g1 < min_wg) continue;
+        } else {
+          if (p.nchunk < 2 || nb * bv * 4 > nvox * 5) continue;
+          const int64_t want = (min_wg + g1 - 1) / g1;
+          cps = (int)((p.nchunk + want - 1) / want);
+          split = (p.nchunk + cps - 1) / cps;
+          if (split < 2 || g1 * split * 4 < min_wg * 3) continue;
+        }
+        const int64_t slots = nb * bv;
+        const int64_t hpo = halo * 4096 / ((int64_t)bv * bo);
+        if (slots < best_slots || (slots == best_slots && hpo < best_halo)) {
+          best_slots = slots; best_halo = hpo; p.bo = bo;
+          p.TD = list[i].TD; p.TH = list[i].TH; p.TW = list[i].TW;
+          p.split = split; p.cps = cps;
+        }
       }
     }
+  }
+  if (p.bo != 0 && p.split > 1) {
+    const size_t need = (size_t)p.split * (size_t)nvox * (size_t)p.O * sizeof(float);
+    if (check_ws && (!a->workspace || a->workspace_bytes < need)) return false;
+    p.part = (float*)a->workspace;
   }
   return p.bo != 0;
 }

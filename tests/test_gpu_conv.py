@@ -16,13 +16,17 @@ from tests.conftest import ACCUMULATION_EPS, OPERAND_ROUNDING, assert_fp16_bar, 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True, params=["default", "streamed"])
+@pytest.fixture(autouse=True, params=["default", "streamed", "streamed-split"])
 def conv_path(request, monkeypatch):
-    """Every case twice: with the library's own kernel choice, and with the streamed
+    """Every case three times: with the library's own kernel choice; with the streamed
     3x3x3 kernel taking every shape it supports (its fill threshold lowered to one
-    workgroup), so small cases cover its partial bricks, batches, concat and fusions."""
+    workgroup), so small cases cover its partial bricks, batches, concat and fusions; and
+    with that threshold out of reach, so every streamed shape with two or more channel
+    chunks splits them over workgroups (fp32 partial sums, fixed-order reduce)."""
     if request.param == "streamed":
         monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1")
+    elif request.param == "streamed-split":
+        monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1000000")
     else:
         monkeypatch.delenv("LDX_CONV_STREAM_MIN_WG", raising=False)
     return request.param
