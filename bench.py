@@ -35,7 +35,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 # HBM bytes per config-1 conv launch: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
 # this script with --copy-calibration, each divided by what the counter reports per byte
 # of a plain 512 MiB device copy (FETCH 0.5, WRITE 1.0); profiles/conv3d_config1.txt.
-CONV_CONFIG1_TRAFFIC_BYTES = 17.95e6
+CONV_CONFIG1_TRAFFIC_BYTES = 17.94e6
 
 
 # Each timed region is one replay of the K captured launches; the reported figure is the
