@@ -94,6 +94,18 @@ typedef struct ldx_conv3d_args {
 size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* args);
 int ldx_conv3d(const ldx_conv3d_args* args, void* stream);
 
+/* ldx_conv3d that also leaves the GroupNorm partial moments of its stored output -- the
+ * fused GroupNorm-statistics epilogue of the conv that feeds a norm_silu_conv
+ * (mlx_model.py:290-342 normalises what the previous conv wrote; here that conv's
+ * epilogue reduces it while it is still in registers). moments: fp32
+ * [batch][chunks][out_c / 2][3], per channel pair and block of output voxels
+ * (count, mean, M2), 16-byte aligned; chunks = ldx_conv3d_stats_chunks(args) for the
+ * same args (workspace included: it decides split-K). Returns 0 chunks (and
+ * ldx_conv3d_stats LDX_EINVAL) for convs whose plan keeps no moments: pointwise and
+ * dense layers, out_c not a multiple of 8, unaligned rows. Same y as ldx_conv3d. */
+int64_t ldx_conv3d_stats_chunks(const ldx_conv3d_args* args);
+int ldx_conv3d_stats(const ldx_conv3d_args* args, float* moments, void* stream);
+
 /* A pointwise conv (dense layer: ksize 1, one input, no affine / SiLU, c0 a multiple of 16
  * and at most 512) whose input rows are first layer-normalized over their c0 channels:
  * x' = half((x - mean) * rsqrt(var + eps) * gamma[c] + beta[c]) with fp32 row statistics
@@ -138,6 +150,16 @@ int ldx_group_norm_affine(const void* x0, int64_t x0_pitch, int32_t c0,
                           int32_t batch, int64_t voxels, int32_t groups,
                           const float* gamma, const float* beta, float eps,
                           float* affine, void* workspace, void* stream);
+
+/* group_norm_affine from moments a conv left (ldx_conv3d_stats) instead of a pass over x:
+ * m0 holds x0's (chunks0 blocks, c0 / 2 pairs), m1 x1's for the concat (c1 = 0: none).
+ * Merged per group in a fixed order (Chan's pairwise update); c0, c1 and C / groups
+ * must be even. Same (batch, C, 2) output as ldx_group_norm_affine. */
+int ldx_group_norm_affine_moments(const float* m0, int64_t chunks0, int32_t c0,
+                                  const float* m1, int64_t chunks1, int32_t c1,
+                                  int32_t batch, int32_t groups,
+                                  const float* gamma, const float* beta, float eps,
+                                  float* affine, void* stream);
 
 /* LayerNorm over the last axis of fp16 (rows, features) (mx.fast.layer_norm,
  * mlx_model.py:360-367): y = half((x - mean) * rsqrt(var + eps) * gamma + beta),

@@ -69,11 +69,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_abi_version": (c_i32, []),
     "ldx_conv3d_workspace_bytes": (ctypes.c_size_t, [ctypes.POINTER(ConvArgs)]),
     "ldx_conv3d": (c_i32, [ctypes.POINTER(ConvArgs), c_vp]),
+    "ldx_conv3d_stats_chunks": (c_i64, [ctypes.POINTER(ConvArgs)]),
+    "ldx_conv3d_stats": (c_i32, [ctypes.POINTER(ConvArgs), c_vp, c_vp]),
     "ldx_dense_ln": (c_i32, [ctypes.POINTER(ConvArgs), c_vp, c_vp, c_f32, c_vp]),
     "ldx_packed_weight_elems": (ctypes.c_size_t, [c_i32, c_i32, c_i32, c_i32]),
     "ldx_pack_weight": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "ldx_pack_upsample_weight": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_group_norm_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i64, c_i32, c_i32]),
+    "ldx_group_norm_affine_moments": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32,
+                                               c_vp, c_vp, c_f32, c_vp, c_vp]),
     "ldx_group_norm_affine": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
                                       c_vp, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "ldx_layer_norm": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),

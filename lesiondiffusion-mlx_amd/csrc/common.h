@@ -123,6 +123,65 @@ __device__ __forceinline__ void pin_value(T& v) {
   asm volatile("" : "+v"(v));
 }
 
+// (count, mean, M2) of a set of values, merged pairwise (Chan et al.): no cancellation.
+struct Moments { float n, mean, m2; };
+
+__device__ __forceinline__ Moments merge(Moments a, Moments b) {
+  const float n = a.n + b.n;
+  if (n == 0.0f) return a;
+  const float d = b.mean - a.mean;
+  const float fb = b.n / n;
+  return {n, a.mean + d * fb, a.m2 + b.m2 + d * d * a.n * fb};
+}
+
+// GroupNorm partial moments of one wave's block of finished outputs, per channel pair.
+// Each lane holds 8 consecutive channels (4 pairs) of NI voxels (ok[i]: the voxel is an
+// output); the lanes holding the same channels are L apart (L a power of two, <= 32).
+// Two passes over the values -- the pair's mean, then its squared deviations -- each
+// summed over those lanes by an xor butterfly (every lane ends with the same sums), so the
+// block's (count, mean, M2) carry no cancellation. With `store`, the lane writes its four
+// pairs' moments as 12 consecutive floats at dst (16-byte aligned).
+template <int NI, int L>
+__device__ __forceinline__ void pair_moments(const f16x8 (&v)[NI], const bool (&ok)[NI], float* dst,
+                                             bool store) {
+  float cnt = 0.f, s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NI; i++)
+    if (ok[i]) {
+      cnt += 2.f;
+#pragma unroll
+      for (int q = 0; q < 4; q++) s[q] += (float)v[i][2 * q] + (float)v[i][2 * q + 1];
+    }
+#pragma unroll
+  for (int m = L; m < 64; m <<= 1) {
+    cnt += __shfl_xor(cnt, m);
+#pragma unroll
+    for (int q = 0; q < 4; q++) s[q] += __shfl_xor(s[q], m);
+  }
+  float mean[4], m2[4];
+#pragma unroll
+  for (int q = 0; q < 4; q++) { mean[q] = cnt > 0.f ? s[q] / cnt : 0.f; m2[q] = 0.f; }
+#pragma unroll
+  for (int i = 0; i < NI; i++)
+    if (ok[i]) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float d0 = (float)v[i][2 * q] - mean[q], d1 = (float)v[i][2 * q + 1] - mean[q];
+        m2[q] += d0 * d0 + d1 * d1;
+      }
+    }
+#pragma unroll
+  for (int m = L; m < 64; m <<= 1)
+#pragma unroll
+    for (int q = 0; q < 4; q++) m2[q] += __shfl_xor(m2[q], m);
+  if (store) {
+    f32x4* d = reinterpret_cast<f32x4*>(dst);
+    d[0] = (f32x4){cnt, mean[0], m2[0], cnt};
+    d[1] = (f32x4){mean[1], m2[1], cnt, mean[2]};
+    d[2] = (f32x4){m2[2], cnt, mean[3], m2[3]};
+  }
+}
+
 // Wait until at most N vector-memory loads of this wave are outstanding.
 // (s_waitcnt immediate for gfx9: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt
 // 11:8 left at their no-wait maxima.)

@@ -65,6 +65,8 @@ struct ConvParams {
   const float* ln_g;       // dense_ksplit with LayerNorm: per-channel gamma, beta and eps
   const float* ln_b;
   float ln_eps;
+  float* stats;            // GroupNorm partial moments [B][schunks][O / 2][3], or null
+  int schunks;             // voxel blocks per batch item the moments are kept for
   UDiv dv_nob, dv_nbr, dv_split, dv_nbw, dv_nbh;  // division by nob, nbr, split, NBW, NBH
 };
 
@@ -256,11 +258,13 @@ __device__ __forceinline__ EpiConst epi_const(const ConvParams& p, int lane, int
 // `ec`), scale, residual, one rounding, activation -- and writes each as one 16-byte
 // store, the lanes of a voxel covering its channels contiguously. Voxel indices are
 // 32-bit (the host bounds B * output voxels below 2^31); the residual rows are all
-// requested before the first is used.
+// requested before the first is used. With p.stats and schunk >= 0, each column block
+// also leaves the GroupNorm partial moments of its stored values (pair_moments) as voxel
+// block schunk + fv of batch item b.
 template <int FO, int FV>
 __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiConst& ec, f32x16 (&acc)[FO][FV],
                                               float* stg, int lane, int wv, int b, int sidx, int pd, int ph,
-                                              int pw, int d0, int h0, int w0) {
+                                              int pw, int d0, int h0, int w0, int schunk = -1) {
   constexpr int EPW = FO * 32 + 4;   // staging pitch (floats): conflict-free both ways
   constexpr int G8 = FO * 4;         // 8-channel groups per voxel (divides 64)
   constexpr int NI = 32 * G8 / 64;   // voxels per lane per column block
@@ -311,8 +315,10 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
       for (int i = 0; i < NI; i++) re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
     }
     f32x4 lo[NI], hi[NI];
+    f16x8 outv[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
+      outv[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
       const int v = lane / G8 + i * (64 / G8);
       lo[i] = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
       hi[i] = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
@@ -336,7 +342,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
       }
       f16* yrow = p.y + (int64_t)ov[i] * p.yp + o;
       if (vec8) {
-        f16x8 out;
+        f16x8& out = outv[i];
 #pragma unroll
         for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + ec.add8[r]) * p.scale + (float)re8[i][r]));
         *reinterpret_cast<f16x8*>(yrow) = out;
@@ -350,6 +356,16 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
           yrow[r] = post_act_t<ACT>((f16)t);
         }
       }
+    }
+    // GroupNorm partial moments of the stored values (16-byte epilogue only; the host
+    // admits stats with O a multiple of 8 and aligned rows): block schunk + fv of batch
+    // item b; lanes g, g + G8, ... hold the same 8 channels.
+    if (p.stats && schunk >= 0 && p.split == 1) {
+      bool okv[NI];
+#pragma unroll
+      for (int i = 0; i < NI; i++) okv[i] = ok[i] && vec8;
+      pair_moments<NI, G8>(outv, okv, p.stats + (((int64_t)b * p.schunks + schunk + fv) * (p.O / 2) + o / 2) * 3,
+                           lane < G8 && vec8);
     }
     __builtin_amdgcn_wave_barrier();
   }
@@ -700,7 +716,8 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
       stg = reinterpret_cast<float*>(smem) + w4 * 32 * EPW;
     }
   }
-  conv_epilogue<FO, FV>(p, ec, acc, stg, lane, wv, b, sidx, pd, ph, pw, d0, h0, w0);
+  conv_epilogue<FO, FV>(p, ec, acc, stg, lane, wv, b, sidx, pd, ph, pw, d0, h0, w0,
+                        (parity * p.nbr + brick) * (WV * FV) + wv * FV);
 }
 
 // Pointwise conv / dense layer: a GEMM whose operands both come straight from global
@@ -1033,6 +1050,111 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
     v = (v + add) * p.scale;
     if (p.res) v += (float)p.res[ov * p.resp + o];
     p.y[ov * p.yp + o] = post_act((f16)v, p.act);
+  }
+}
+
+// Split-K finish that also leaves GroupNorm partial moments: workgroup (k, b) of 1024
+// threads finishes output voxels [32 k, 32 k + 32) of batch item b, thread t the 8
+// channels 8 (t % G8) .. (G8 = O / 8 <= 64) of voxels t / G8 + j * VP (VP = 1024 / G8 per
+// pass, at most two passes) -- partial planes summed in split order, then the
+// conv_reduce_kernel epilogue, 16-byte accesses. Per channel pair, the block's (count,
+// mean, M2): per-thread sums added through LDS in voxel order, the mean first, then the
+// squared deviations of the values the thread kept.
+constexpr int RS_THREADS = 1024;
+constexpr int RS_PASSES = 2;   // 32 / VP passes: VP >= 16 for O <= 512
+__global__ __launch_bounds__(RS_THREADS) void conv_reduce_stats_kernel(ConvParams p, int ovol) {
+  __shared__ float part4[RS_THREADS * 4];
+  __shared__ float pmean[256];
+  const int G8 = p.O >> 3, VP = RS_THREADS / G8;
+  const int t = threadIdx.x, g = t % G8, vs = t / G8, o = g * 8;
+  const int k = blockIdx.x, b = blockIdx.y;
+  const int nv = min(32, ovol - k * 32);
+  const int64_t plane = (int64_t)p.B * ovol * p.O;
+  f16x8 keep[RS_PASSES];
+  bool okj[RS_PASSES];
+  f32x4 lo[RS_PASSES], hi[RS_PASSES];
+  f16x8 rs[RS_PASSES];
+  int64_t ov[RS_PASSES];
+  // Every pass's operands requested before any is summed.
+#pragma unroll
+  for (int j = 0; j < RS_PASSES; j++) {
+    const int v = vs + j * VP;
+    okj[j] = vs < VP && v < nv;
+    ov[j] = (int64_t)b * ovol + k * 32 + (okj[j] ? v : 0);
+    lo[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    hi[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    rs[j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    if (okj[j] && p.res) rs[j] = *reinterpret_cast<const f16x8*>(p.res + ov[j] * p.resp + o);
+  }
+#pragma unroll 4
+  for (int s2 = 0; s2 < p.split; s2++)
+#pragma unroll
+    for (int j = 0; j < RS_PASSES; j++)
+      if (okj[j]) {
+        const float* src = p.part + s2 * plane + ov[j] * p.O + o;
+        lo[j] += *reinterpret_cast<const f32x4*>(src);
+        hi[j] += *reinterpret_cast<const f32x4*>(src + 4);
+      }
+  float add[8];
+  {
+    const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o : nullptr;
+    f32x4 b0 = {0.f, 0.f, 0.f, 0.f}, b1 = {0.f, 0.f, 0.f, 0.f};
+    if (bias && vs < VP) { b0 = *reinterpret_cast<const f32x4*>(bias); b1 = *reinterpret_cast<const f32x4*>(bias + 4); }
+    f16x8 sh = {};
+    if (p.shift && vs < VP) sh = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o);
+#pragma unroll
+    for (int r = 0; r < 4; r++) { add[r] = b0[r] + (float)sh[r]; add[r + 4] = b1[r] + (float)sh[r + 4]; }
+  }
+  float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < RS_PASSES; j++) {
+    keep[j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    if (!okj[j]) continue;
+    f16x8 out;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      out[r] = post_act((f16)((lo[j][r] + add[r]) * p.scale + (float)rs[j][r]), p.act);
+      out[r + 4] = post_act((f16)((hi[j][r] + add[r + 4]) * p.scale + (float)rs[j][r + 4]), p.act);
+    }
+    *reinterpret_cast<f16x8*>(p.y + ov[j] * p.yp + o) = out;
+    keep[j] = out;
+#pragma unroll
+    for (int q = 0; q < 4; q++) s4[q] += (float)out[2 * q] + (float)out[2 * q + 1];
+  }
+  const float n = 2.0f * (float)nv;
+  const int npair = p.O >> 1;
+#pragma unroll
+  for (int q = 0; q < 4; q++) part4[t * 4 + q] = s4[q];
+  __syncthreads();
+  if (t < npair) {
+    float a = 0.f;
+    for (int u = 0; u < VP; u++) a += part4[(u * G8 + t / 4) * 4 + t % 4];
+    pmean[t] = a / n;
+  }
+  __syncthreads();
+  float m4[4] = {0.f, 0.f, 0.f, 0.f};
+  if (vs < VP) {
+    float mu[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) mu[q] = pmean[g * 4 + q];
+#pragma unroll
+    for (int j = 0; j < RS_PASSES; j++)
+      if (okj[j])
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const float d0 = (float)keep[j][2 * q] - mu[q], d1 = (float)keep[j][2 * q + 1] - mu[q];
+          m4[q] += d0 * d0 + d1 * d1;
+        }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 4; q++) part4[t * 4 + q] = m4[q];
+  __syncthreads();
+  if (t < npair) {
+    float m2 = 0.f;
+    for (int u = 0; u < VP; u++) m2 += part4[(u * G8 + t / 4) * 4 + t % 4];
+    float* dst = p.stats + (((int64_t)b * p.schunks + k) * npair + t) * 3;
+    dst[0] = n; dst[1] = pmean[t]; dst[2] = m2;
   }
 }
 
@@ -1382,29 +1504,61 @@ static int run_dense(const ConvParams& p, hipStream_t st) {
   return launch_dense<2, 2, 1, 1>(p, st);
 }
 
-extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
+// Split-K finish: the plain reduce, or (stats) the reduce that also leaves the
+// GroupNorm moments of 32-voxel blocks.
+static int launch_reduce(ConvParams& p, hipStream_t st, const char* what) {
+  const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
+  const int64_t nvox = (int64_t)p.B * ovol;
+  if (p.stats) {
+    hipLaunchKernelGGL(conv_reduce_stats_kernel, dim3((unsigned)((ovol + 31) / 32), (unsigned)p.B), dim3(RS_THREADS), 0,
+                       st, p, (int)ovol);
+    return check_launch(what);
+  }
+  const int64_t n = nvox * p.O;
+  const unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
+  hipLaunchKernelGGL(conv_reduce_kernel, dim3(blocks), dim3(256), 0, st, p, nvox);
+  return check_launch(what);
+}
+
+// One conv, as planned for these arguments. stats: also the GroupNorm partial moments of
+// the output (null: none). With dry, nothing is launched: *chunks receives the voxel
+// blocks per batch item the moments are kept for (0: this plan keeps none).
+static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t* chunks, void* stream) {
   ConvParams p;
   Tile t;
   size_t lds;
   bool vec;
   int64_t ws = 0;
+  if (chunks) *chunks = 0;
   int rc = plan_conv(a, p, t, lds, vec, ws);
   if (rc != LDX_OK) return rc;
-  if (use_dense(a, vec)) return run_dense(p, as_stream(stream));
+  hipStream_t st = as_stream(stream);
+  const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
+  // Moments need the 16-byte epilogue; the split-K reduce keeps them for O <= 512.
+  const bool can_stats = p.O % 8 == 0 && p.ep_vec;
+  const int64_t reduce_chunks = can_stats && p.O <= 512 ? (ovol + 31) / 32 : 0;
+  if (use_dense(a, vec)) {
+    if (dry) return LDX_OK;
+    if (stats) return fail("conv3d_stats: pointwise convs keep no moments");
+    return run_dense(p, st);
+  }
   {
     StreamParams sp;
     if (conv3d_stream_plan(a, &sp)) {
-      rc = conv3d_stream_launch(sp, as_stream(stream));
+      const int64_t ch = sp.split == 1 ? (can_stats ? sp.schunks : 0) : reduce_chunks;
+      if (chunks) *chunks = ch;
+      if (dry) return LDX_OK;
+      if (stats && ch == 0) return fail("conv3d_stats: this conv keeps no moments");
+      sp.stats = stats;
+      rc = conv3d_stream_launch(sp, st);
       if (rc != LDX_OK || sp.split == 1) return rc;
       // Split over channel chunks: the same fixed-order reduce and epilogue as the general
       // kernel's split-K.
       p.split = sp.split;
       p.part = sp.part;
-      const int64_t nvox = (int64_t)p.B * p.OD * p.OH * p.OW;
-      const int64_t n = nvox * p.O;
-      const unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
-      hipLaunchKernelGGL(conv_reduce_kernel, dim3(blocks), dim3(256), 0, as_stream(stream), p, nvox);
-      return check_launch("conv3d (streamed): split reduce");
+      p.stats = stats;
+      p.schunks = (int)ch;
+      return launch_reduce(p, st, "conv3d (streamed): split reduce");
     }
   }
   if (p.split > 1 && (!a->workspace || a->workspace_bytes < (size_t)ws)) {
@@ -1413,8 +1567,16 @@ extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
     p.cps = (p.C + t.CC - 1) / t.CC;
   }
   p.part = p.split > 1 ? (float*)a->workspace : nullptr;
+  {
+    const int64_t ch = p.split == 1 ? (can_stats ? (int64_t)(p.upsample ? 8 : 1) * p.NBD * p.NBH * p.NBW * t.WV * t.FV : 0)
+                                    : reduce_chunks;
+    if (chunks) *chunks = ch;
+    if (dry) return LDX_OK;
+    if (stats && ch == 0) return fail("conv3d_stats: this conv keeps no moments");
+    p.stats = stats;
+    p.schunks = (int)ch;
+  }
   const int grid_z = p.B * (p.upsample ? 8 : 1) * p.split;
-  hipStream_t st = as_stream(stream);
 
 #define LDX_TILE(WO_, WV_, FO_, FV_, KSPL_)                                             \
   if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_ && t.KSPL == KSPL_) \
@@ -1430,11 +1592,23 @@ extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
   return fail("conv3d: no kernel for tile");
 #undef LDX_TILE
   if (rc != LDX_OK || p.split == 1) return rc;
-  const int64_t nvox = (int64_t)p.B * p.OD * p.OH * p.OW;
-  const int64_t n = nvox * p.O;
-  const unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
-  hipLaunchKernelGGL(conv_reduce_kernel, dim3(blocks), dim3(256), 0, st, p, nvox);
-  return check_launch("conv3d: split reduce");
+  return launch_reduce(p, st, "conv3d: split reduce");
+}
+
+extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
+  return conv3d_run(a, nullptr, false, nullptr, stream);
+}
+
+extern "C" int64_t ldx_conv3d_stats_chunks(const ldx_conv3d_args* a) {
+  int64_t ch = 0;
+  if (!a || conv3d_run(a, nullptr, true, &ch, nullptr) != LDX_OK) return 0;
+  return ch;
+}
+
+extern "C" int ldx_conv3d_stats(const ldx_conv3d_args* a, float* stats, void* stream) {
+  if (!stats) return fail("conv3d_stats: null moments buffer");
+  if ((uintptr_t)stats % 16) return fail("conv3d_stats: moments buffer must be 16-byte aligned");
+  return conv3d_run(a, stats, false, nullptr, stream);
 }
 
 extern "C" int ldx_dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps,

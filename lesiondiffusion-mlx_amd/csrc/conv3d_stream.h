@@ -26,6 +26,8 @@ struct StreamParams {
   const f16* res; int64_t resp;
   float scale;
   f16* y; int64_t yp;
+  float* stats;             // GroupNorm partial moments [B][schunks][O / 2][3], or null
+  int schunks;              // moment blocks per batch item: one per brick
 };
 
 // True (and *p planned) when the streamed kernel takes this conv. A plan that splits the

@@ -76,7 +76,8 @@ struct Shape {
   static constexpr int RP = 64 + 4;                   // floats per epilogue row (padded)
   static constexpr int EPI = 16 * 32 * RP * 4;        // epilogue rows: [w4][fv][group] x 32 voxels
   static constexpr int LDS_MAIN = RING + NSLOT * STAGE;
-  static constexpr int LDS = LDS_MAIN > EPI ? LDS_MAIN : EPI;
+  static constexpr int MST = 8 * 32 * 3 * 4;           // per-wave GroupNorm moments, past the rows
+  static constexpr int LDS = LDS_MAIN > EPI + MST ? LDS_MAIN : EPI + MST;
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert(HALO % 16 == 0 && STAGE % 1024 == 0, "alignment");
 };
@@ -421,6 +422,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   __syncthreads();
   // Rows fv = kg: (group 0 + group 1), then bias + shift, scale, residual, one rounding --
   // or, split over channel chunks, the fp32 sums of this range (the reduce finishes them).
+  f16x8 outv[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int ro = ((lane >> 3) + 8 * i) * S::RP + g8 * 8;
@@ -436,13 +438,35 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       }
       continue;
     }
-    f16x8 out;
+    f16x8& out = outv[i];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       out[e] = (f16)((s0[e] + (bv0[e] + (float)sv[e])) * p.scale + (float)res[i][e]);
       out[e + 4] = (f16)((s1[e] + (bv1[e] + (float)sv[e + 4])) * p.scale + (float)res[i][e + 4]);
     }
     if (okr[i]) *reinterpret_cast<f16x8*>(p.y + ovr[i] * p.yp + o8) = out;
+  }
+  // GroupNorm partial moments of the stored values, one block per brick: each wave's
+  // 32 voxels x 32 channel pairs (lanes l, l + 8, ... hold the same 8 channels) into LDS
+  // past the epilogue rows, then thread pp < BO / 2 merges pair pp over the waves of its
+  // 64-channel half in a fixed order (K-group, then voxel block).
+  if (p.stats && p.split == 1) {
+    float* mst = reinterpret_cast<float*>(smem + S::EPI);   // [8 waves][32 pairs][3]
+    pair_moments<4, 8>(outv, okr, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
+    __syncthreads();
+    if (tid < BO / 2) {
+      const int wo_p = tid >> 5, pp = tid & 31;
+      Moments m = {0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k2 = 0; k2 < 2; k2++)
+#pragma unroll
+        for (int v2 = 0; v2 < S::WV; v2++) {
+          const float* q = mst + ((k2 * 4 + wo_p * S::WV + v2) * 32 + pp) * 3;
+          m = merge(m, Moments{q[0], q[1], q[2]});
+        }
+      float* dst = p.stats + (((int64_t)b * p.schunks + brick) * (p.O / 2) + oblk * (BO / 2) + tid) * 3;
+      dst[0] = m.n; dst[1] = m.mean; dst[2] = m.m2;
+    }
   }
 }
 
@@ -572,6 +596,8 @@ bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out, bool check_
     if (check_ws && (!a->workspace || a->workspace_bytes < need)) return false;
     p.part = (float*)a->workspace;
   }
+  if (p.bo != 0)
+    p.schunks = (int)(ceil_div64(p.D, p.TD) * ceil_div64(p.H, p.TH) * ceil_div64(p.W, p.TW));
   return p.bo != 0;
 }
 

@@ -123,16 +123,6 @@ __global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
 // (count, mean, M2) partials; per-thread sums over a few voxels, converted to
 // (n, mean, M2) and merged (Chan et al.) in a fixed order, so results are
 // deterministic run to run.
-struct Moments { float n, mean, m2; };
-
-__device__ __forceinline__ Moments merge(Moments a, Moments b) {
-  const float n = a.n + b.n;
-  if (n == 0.0f) return a;
-  const float d = b.mean - a.mean;
-  const float fb = b.n / n;
-  return {n, a.mean + d * fb, a.m2 + b.m2 + d * d * a.n * fb};
-}
-
 template <int V>
 __global__ __launch_bounds__(256) void gn_partial_kernel(
     const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,
@@ -289,6 +279,61 @@ __global__ __launch_bounds__(256) void gn_small_kernel(
   const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
   const float rstd = 1.0f / sqrtf(var + eps);
   for (int c = c0 + t; c < c0 + gs; c += 256) {
+    const float sc = gamma[c] * rstd;
+    affine[((int64_t)b * C + c) * 2] = sc;
+    affine[((int64_t)b * C + c) * 2 + 1] = beta[c] - sc * mean;
+  }
+}
+
+// GroupNorm from moments a producer left (ldx_conv3d_stats): per channel pair and voxel
+// block, (count, mean, M2) in [batch][chunks][pairs][3]. One workgroup per (group, batch
+// item) merges its pairs' blocks -- pairs [0, c0 / 2) from m0, the rest from m1 (the
+// decoder's concat) -- in a fixed order (thread t takes items t, t + 256, ... of the
+// group's list, then a fixed tree), and writes the group's (scale, offset) pairs.
+__global__ __launch_bounds__(256) void gn_moments_kernel(
+    const float* __restrict__ m0, int64_t n0, int P0, const float* __restrict__ m1, int64_t n1, int P1,
+    int C, int G, const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
+    float* __restrict__ affine) {
+  __shared__ float sn[256], sm[256], s2[256];
+  const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int gs = C / G, u0 = g * gs / 2, nu = gs / 2;
+  Moments m = {0.f, 0.f, 0.f};
+  // The group's (pair, block) items in one list -- x0's pairs first, block-minor -- dealt
+  // to the threads round-robin; four items' moments requested before any is merged.
+  const int na = max(0, min(nu, P0 - u0));   // pairs of the group in x0
+  const unsigned items0 = (unsigned)(na * n0), items = items0 + (unsigned)((nu - na) * n1);
+  for (unsigned i0 = t; i0 < items; i0 += 4 * 256) {
+    float3 r[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const unsigned i = i0 + e * 256;
+      r[e] = make_float3(0.f, 0.f, 0.f);
+      if (i < items0) {
+        const unsigned u = u0 + i / (unsigned)n0, j = i % (unsigned)n0;
+        r[e] = *reinterpret_cast<const float3*>(m0 + (((int64_t)b * n0 + j) * P0 + u) * 3);
+      } else if (i < items) {
+        const unsigned ii = i - items0;
+        const unsigned u = u0 + na - P0 + ii / (unsigned)n1, j = ii % (unsigned)n1;
+        r[e] = *reinterpret_cast<const float3*>(m1 + (((int64_t)b * n1 + j) * P1 + u) * 3);
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      if (i0 + e * 256 < items) m = merge(m, Moments{r[e].x, r[e].y, r[e].z});
+  }
+  sn[t] = m.n; sm[t] = m.mean; s2[t] = m.m2;
+  __syncthreads();
+  for (int off = 128; off > 0; off >>= 1) {
+    if (t < off) {
+      const Moments r = merge(Moments{sn[t], sm[t], s2[t]}, Moments{sn[t + off], sm[t + off], s2[t + off]});
+      sn[t] = r.n; sm[t] = r.mean; s2[t] = r.m2;
+    }
+    __syncthreads();
+  }
+  const float mean = sm[0];
+  const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  for (int c = g * gs + t; c < (g + 1) * gs; c += 256) {
     const float sc = gamma[c] * rstd;
     affine[((int64_t)b * C + c) * 2] = sc;
     affine[((int64_t)b * C + c) * 2 + 1] = beta[c] - sc * mean;
@@ -518,6 +563,24 @@ extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, con
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, batch), dim3(256), 0, st, part, (int)nchunks, C,
                      groups, gamma, beta, eps, affine);
   return check_launch("group_norm_affine: finalize");
+}
+
+extern "C" int ldx_group_norm_affine_moments(const float* m0, int64_t chunks0, int32_t c0, const float* m1,
+                                             int64_t chunks1, int32_t c1, int32_t batch, int32_t groups,
+                                             const float* gamma, const float* beta, float eps, float* affine,
+                                             void* stream) {
+  if (!m0 || !gamma || !beta || !affine) return fail("group_norm_affine_moments: null pointer");
+  if (c1 > 0 && (!m1 || chunks1 < 1)) return fail("group_norm_affine_moments: c1 > 0 without moments");
+  const int C = c0 + (c1 > 0 ? c1 : 0);
+  if (batch < 1 || chunks0 < 1 || c0 < 2 || groups < 1 || C % groups || c0 % 2 || (c1 > 0 && c1 % 2) ||
+      (C / groups) % 2)
+    return fail("group_norm_affine_moments: bad shape (batch %d C %d (c0 %d) groups %d): moments are kept "
+                "per channel pair, so c0, c1 and C / groups must be even", batch, C, c0, groups);
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(gn_moments_kernel, dim3(groups, batch), dim3(256), 0, st, m0, chunks0, c0 / 2,
+                     c1 > 0 ? m1 : m0, c1 > 0 ? chunks1 : chunks0, c1 > 0 ? c1 / 2 : 1, C, groups, gamma, beta,
+                     eps, affine);
+  return check_launch("group_norm_affine_moments");
 }
 
 extern "C" int ldx_layer_norm(const void* x, int64_t xp, int64_t rows, int32_t F, const float* gamma,

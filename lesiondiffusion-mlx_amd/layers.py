@@ -70,18 +70,20 @@ class SourceLayers:
     def conv(self, x: torch.Tensor, key: str, *, stride: int = 1, residual: torch.Tensor | None = None,
              x1: torch.Tensor | None = None, affine: torch.Tensor | None = None, silu: bool = False,
              shift: torch.Tensor | None = None, output_scale: float = 1.0,
-             out: torch.Tensor | None = None) -> torch.Tensor:
+             out: torch.Tensor | None = None, moments: bool = False) -> torch.Tensor:
         """3x3x3 (padding 1, stride 1 or 2) or pointwise conv keyed ``key`` with the fused
-        prologue/epilogue of ``ops.nax_conv3d`` (mlx_model.py:159-202, 290-342)."""
+        prologue/epilogue of ``ops.nax_conv3d`` (mlx_model.py:159-202, 290-342);
+        ``moments``: keep the output's GroupNorm moments for the norm that reads it next."""
         return ops.nax_conv3d(x, self.packed[key], self.bias32.get(key), stride=stride, residual=residual,
                               x1=x1, affine=affine, silu=silu, shift=shift, output_scale=output_scale,
-                              out=out)
+                              out=out, moments=moments)
 
-    def upsample_conv(self, x: torch.Tensor, key: str, *, output_scale: float = 1.0) -> torch.Tensor:
+    def upsample_conv(self, x: torch.Tensor, key: str, *, output_scale: float = 1.0,
+                      moments: bool = False) -> torch.Tensor:
         """Conv of the nearest 2x upsampling of ``x`` from folded weights
         (mlx_model.py:272-288)."""
         return ops.nax_conv3d(x, self.packed[key], self.bias32.get(key), upsample=True,
-                              output_scale=output_scale)
+                              output_scale=output_scale, moments=moments)
 
     def dense(self, x: torch.Tensor, key: str, *, residual: torch.Tensor | None = None,
               act: str | None = None, affine: torch.Tensor | None = None,
@@ -105,12 +107,14 @@ class SourceLayers:
 
     def norm_silu_conv(self, x: torch.Tensor, norm_key: str, conv_key: str, *, groups: int, eps: float,
                        shift: torch.Tensor | None = None, residual: torch.Tensor | None = None,
-                       x1: torch.Tensor | None = None, output_scale: float = 1.0) -> torch.Tensor:
+                       x1: torch.Tensor | None = None, output_scale: float = 1.0,
+                       moments: bool = False) -> torch.Tensor:
         """``residual + conv(silu(GN(x))) + shift`` with the normalised input never stored
-        (mlx_model.py:290-342)."""
+        (mlx_model.py:290-342). GN's statistics come from the moments the conv that wrote
+        ``x`` (and ``x1``) kept, when it kept them; ``moments`` keeps this conv's."""
         aff = self.norm_affine(x, norm_key, groups=groups, eps=eps, x1=x1)
         return self.conv(x, conv_key, x1=x1, affine=aff, silu=True, shift=shift, residual=residual,
-                         output_scale=output_scale)
+                         output_scale=output_scale, moments=moments)
 
     def layer_norm(self, x: torch.Tensor, key: str, eps: float = 1e-5) -> torch.Tensor:
         return ops.layer_norm(x, self.vec32[key + ".weight"], self.vec32[key + ".bias"], eps)

@@ -178,7 +178,8 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
                residual: torch.Tensor | None = None, x1: torch.Tensor | None = None,
                act: str | None = None, out: torch.Tensor | None = None,
                shift: torch.Tensor | None = None,
-               ln: tuple[torch.Tensor, torch.Tensor, float] | None = None) -> torch.Tensor:
+               ln: tuple[torch.Tensor, torch.Tensor, float] | None = None,
+               moments: bool | str = False) -> torch.Tensor:
     """Fused conv of NDHWC ``x`` (optionally ``concat([x, x1], channels)``) with a packed
     weight: ``half((conv(prep(x)) + bias + shift) * output_scale + residual)``, ``prep`` =
     the per-(b, c) ``affine`` then SiLU, rounded to fp16 once (nax_conv3d,
@@ -186,6 +187,10 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     a wider tensor is fine). ``act="gelu"`` / ``"silu"`` additionally stores
     ``half(act(y))``. ``ln = (gamma, beta, eps)`` (pointwise convs of one input only)
     layer-normalizes each input row first, in the same launch (ldx_dense_ln).
+    ``moments=True`` also keeps the GroupNorm partial moments of the output, reduced in
+    the conv's epilogue (ldx_conv3d_stats), where the plan allows it and pays (not on
+    split-K plans; ``moments="always"`` keeps them there too): a later
+    ``group_norm_affine`` of the returned tensor then merges them instead of reading it.
 
     Returns NDHWC ``(B, D', H', W', O)`` fp16 (written into ``out`` when given, which may
     be a channel slice of a wider tensor).
@@ -269,9 +274,39 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
                 raise ValueError(f"{name} must be contiguous device float32 with {c0} values")
         check(lib.ldx_dense_ln(ctypes.byref(a), gamma.data_ptr(), beta.data_ptr(), float(eps), _stream()),
               "dense_ln")
+        _set_moments(out, None)
+        return out
+    # Split-K plans (a workspace was asked for) keep no moments here: on the small tensors
+    # that split, the reduce with moments (6.5 us) and their merge cost more than the
+    # plain reduce plus a one-launch GroupNorm pass (measured on MI355X, config 5).
+    want = moments == "always" or (moments is True and not ws_bytes)
+    chunks = lib.ldx_conv3d_stats_chunks(ctypes.byref(a)) if want else 0
+    if chunks > 0:
+        m = torch.empty((b, chunks, o // 2, 3), dtype=torch.float32, device=x.device)
+        check(lib.ldx_conv3d_stats(ctypes.byref(a), m.data_ptr(), _stream()), "conv3d_stats")
+        _set_moments(out, m)
         return out
     check(lib.ldx_conv3d(ctypes.byref(a), _stream()), "conv3d")
+    _set_moments(out, None)
     return out
+
+
+def _set_moments(t: torch.Tensor, m: torch.Tensor | None) -> None:
+    """Attach (or clear) the GroupNorm partial moments a conv kept of ``t`` as written."""
+    if m is None:
+        if hasattr(t, "_ldx_moments"):
+            del t._ldx_moments
+    else:
+        t._ldx_moments = m
+
+
+def moments_of(t: torch.Tensor | None) -> torch.Tensor | None:
+    """The ``(B, chunks, C / 2, 3)`` moments a conv kept of ``t`` (``nax_conv3d(...,
+    moments=True)``), or None."""
+    m = getattr(t, "_ldx_moments", None) if t is not None else None
+    if m is None or t.dim() != 5 or m.shape[0] != t.shape[0] or 2 * m.shape[2] != t.shape[4]:
+        return None
+    return m
 
 
 def conv3d(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None,
@@ -324,6 +359,15 @@ def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, 
         raise ValueError(f"groups {groups} must divide channels {c}")
     g32 = gamma.to(torch.float32).contiguous()
     b32 = beta.to(torch.float32).contiguous()
+    m0, m1 = moments_of(x), moments_of(x1)
+    if m0 is not None and (x1 is None or m1 is not None) and (c // groups) % 2 == 0 and c0 % 2 == 0 \
+            and c1 % 2 == 0:
+        # Moments the producing convs kept: no pass over x.
+        out = torch.empty((b, c, 2), dtype=torch.float32, device=x.device)
+        check(lib.ldx_group_norm_affine_moments(
+            _ptr(m0), int(m0.shape[1]), c0, _ptr(m1), int(m1.shape[1]) if m1 is not None else 0, c1, b, groups,
+            _ptr(g32), _ptr(b32), float(eps), _ptr(out), _stream()), "group_norm_affine_moments")
+        return out
     voxels = d * h * w
     ws = torch.empty(max(1, lib.ldx_group_norm_workspace_bytes(b, voxels, c, groups)),
                      dtype=torch.uint8, device=x.device)

@@ -86,7 +86,7 @@ class LdmUnet(SourceLayers):
             lo, hi = self.emb_slices[key]
             shift = shifts[:, lo:hi]
         h = self.norm_silu_conv(x, key + ".in_layers.0", key + ".in_layers.2", groups=groups_for(c),
-                                eps=1e-5, shift=shift, x1=x1)
+                                eps=1e-5, shift=shift, x1=x1, moments=True)
         if key + ".skip_connection" in self.packed:
             skip = self.conv(x, key + ".skip_connection", x1=x1)
         elif x1 is None:
@@ -94,7 +94,7 @@ class LdmUnet(SourceLayers):
         else:
             raise ValueError(f"{key}: concatenated input without a skip projection")
         return self.norm_silu_conv(h, key + ".out_layers.0", key + ".out_layers.3",
-                                   groups=groups_for(h.shape[-1]), eps=1e-5, residual=skip)
+                                   groups=groups_for(h.shape[-1]), eps=1e-5, residual=skip, moments=True)
 
     def _attend(self, tok: torch.Tensor, att: str, heads: int, kv: tuple[torch.Tensor, torch.Tensor] | None,
                 residual: torch.Tensor, ln: str) -> torch.Tensor:
@@ -149,7 +149,7 @@ class LdmUnet(SourceLayers):
         """``LdmUnet._forward`` (mlx_model.py:599-654) on NDHWC fp16 ``x``."""
         cfg = self.config
         shifts = self.time_shifts(timesteps)
-        x = self.conv(x, "input_blocks.0.0")
+        x = self.conv(x, "input_blocks.0.0", moments=True)
         skips = [x]
         block, resolution = 1, 1
         for level in range(len(cfg.channel_mult)):
@@ -161,7 +161,7 @@ class LdmUnet(SourceLayers):
                 skips.append(x)
                 block += 1
             if level < len(cfg.channel_mult) - 1:
-                x = self.conv(x, f"input_blocks.{block}.0.op", stride=2)
+                x = self.conv(x, f"input_blocks.{block}.0.op", stride=2, moments=True)
                 skips.append(x)
                 block += 1
                 resolution *= 2
@@ -177,7 +177,7 @@ class LdmUnet(SourceLayers):
                 if has_attn:
                     x = self.transformer(x, context_kv, key + ".1")
                 if level and i == cfg.num_res_blocks:
-                    x = self.upsample_conv(x, key + f".{2 if has_attn else 1}.conv")
+                    x = self.upsample_conv(x, key + f".{2 if has_attn else 1}.conv", moments=True)
                     resolution //= 2
                 block += 1
         return self.norm_silu_conv(x, "out.0", "out.2", groups=groups_for(x.shape[-1]), eps=1e-5)
@@ -187,14 +187,14 @@ class LdmUnet(SourceLayers):
         attention (the residual-block stack of the encoder)."""
         cfg = self.config
         shifts = self.time_shifts(timesteps)
-        x = self.conv(x, "input_blocks.0.0")
+        x = self.conv(x, "input_blocks.0.0", moments=True)
         block = 1
         for level in range(len(cfg.channel_mult)):
             for _ in range(cfg.num_res_blocks):
                 x = self.residual(x, shifts, f"input_blocks.{block}.0")
                 block += 1
             if level < len(cfg.channel_mult) - 1:
-                x = self.conv(x, f"input_blocks.{block}.0.op", stride=2)
+                x = self.conv(x, f"input_blocks.{block}.0.op", stride=2, moments=True)
                 block += 1
         return x
 

@@ -39,17 +39,19 @@ class VqDecoder(SourceLayers):
                 self.bias32[att + ".qkv"] = torch.cat([self.weights[f"{att}.{n}.bias"].float()
                                                        for n in ("q", "k", "v")]).contiguous()
 
-    def norm_silu_conv_vq(self, x, norm_key, conv_key, *, eps_scale=1.0, output_scale=1.0, residual=None):
+    def norm_silu_conv_vq(self, x, norm_key, conv_key, *, eps_scale=1.0, output_scale=1.0, residual=None,
+                          moments=False):
         return self.norm_silu_conv(x, norm_key, conv_key, groups=self.groups, eps=self.eps * eps_scale,
-                                   residual=residual, output_scale=output_scale)
+                                   residual=residual, output_scale=output_scale, moments=moments)
 
     def residual(self, x: torch.Tensor, key: str) -> torch.Tensor:
         """VQ ResBlock (mlx_model.py:720-727)."""
-        h = self.norm_silu_conv_vq(x, key + ".norm1", key + ".conv1", eps_scale=self._eps_scale(key + ".norm1"))
+        h = self.norm_silu_conv_vq(x, key + ".norm1", key + ".conv1", eps_scale=self._eps_scale(key + ".norm1"),
+                                   moments=True)
         if key + ".nin_shortcut" in self.packed:
             x = self.conv(x, key + ".nin_shortcut")
         return self.norm_silu_conv_vq(h, key + ".norm2", key + ".conv2",
-                                      output_scale=self._branch_scale(key + ".conv2"), residual=x)
+                                      output_scale=self._branch_scale(key + ".conv2"), residual=x, moments=True)
 
     def attn_block(self, x: torch.Tensor, key: str) -> torch.Tensor:
         """Single-head spatial self-attention: GN -> 1x1 q/k/v (one GEMM, GN applied in
@@ -73,7 +75,7 @@ class VqDecoder(SourceLayers):
     def decode(self, z: torch.Tensor) -> torch.Tensor:
         """NDHWC fp16 latent -> NDHWC fp16 volume at 2^(upsamplings) resolution."""
         x = self.conv(z, "post_quant_conv")
-        x = self.conv(x, "decoder.conv_in")
+        x = self.conv(x, "decoder.conv_in", moments=True)
         x = self.residual(x, "decoder.mid.block_1")
         if "decoder.mid.attn_1.qkv" in self.packed:
             x = self.attn_block(x, "decoder.mid.attn_1")
@@ -83,7 +85,7 @@ class VqDecoder(SourceLayers):
                 x = self.residual(x, f"decoder.up.{level}.block.{blk}")
             if level in self.upsample_levels:
                 key = f"decoder.up.{level}.upsample.conv"
-                x = self.upsample_conv(x, key, output_scale=self._upsample_scale(key))
+                x = self.upsample_conv(x, key, output_scale=self._upsample_scale(key), moments=True)
         return self.norm_silu_conv_vq(x, "decoder.norm_out", "decoder.conv_out",
                                       eps_scale=self._eps_scale("decoder.norm_out"))
 

@@ -329,3 +329,92 @@ def test_dense_layer_norm_matches_float64(pkg, dev, rows, c, o, act, with_res) -
     assert np.all(np.isfinite(yy))
     assert np.all(np.abs(yy - expected) <= bound)
     assert np.all(np.abs(yy - host(sep)) <= bound)
+
+
+def merged_moments(m: torch.Tensor) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """Chan's merge, in float64, of every block's (count, mean, M2) per channel pair."""
+    mm = m.double().cpu().numpy()
+    n, mean, m2 = mm[..., 0], mm[..., 1], mm[..., 2]
+    assert np.all(m2 >= 0) and np.all(n >= 0) and np.all(n % 2 == 0)
+    tot = n.sum(1)
+    mu = (n * mean).sum(1) / tot
+    return tot, mu, (m2.sum(1) + (n * (mean - mu[:, None]) ** 2).sum(1)) / tot
+
+
+def check_moments(pkg, dev, y: torch.Tensor, groups: int = 32, eps: float = 1e-5) -> None:
+    """The moments a conv kept of y: every output voxel counted once per channel pair, the
+    pairs' mean and variance those of the stored fp16 values (float64 reference), and
+    group_norm_affine from them equal to GroupNorm's (scale, offset) of y."""
+    m = pkg.ops.moments_of(y)
+    assert m is not None, "this conv kept no moments"
+    yv = host(y)
+    b, o = yv.shape[0], yv.shape[-1]
+    pairs = yv.reshape(b, -1, o // 2, 2)
+    tot, mu, var = merged_moments(m)
+    assert np.array_equal(tot, np.full((b, o // 2), 2.0 * pairs.shape[1]))
+    np.testing.assert_allclose(mu, pairs.mean(axis=(1, 3)), rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(var, pairs.var(axis=(1, 3)), rtol=1e-4, atol=1e-7)
+    rng = np.random.default_rng(o)
+    gamma = rng.normal(size=(o,)).astype(np.float32)
+    beta = rng.normal(size=(o,)).astype(np.float32)
+    aff = host(pkg.ops.group_norm_affine(y, to_dev(gamma, dev), to_dev(beta, dev), groups=groups, eps=eps))
+    grp = yv.reshape(b, -1, groups, o // groups)
+    gm, gv = grp.mean(axis=(1, 3)), grp.var(axis=(1, 3))
+    scale = gamma[None] / np.sqrt(np.repeat(gv, o // groups, axis=1) + eps)
+    offset = beta[None] - scale * np.repeat(gm, o // groups, axis=1)
+    np.testing.assert_allclose(aff[..., 0], scale, rtol=2e-5, atol=1e-6)
+    np.testing.assert_allclose(aff[..., 1], offset, rtol=2e-5, atol=2e-5)
+
+
+@pytest.mark.parametrize(("shape", "out_c", "stride", "upsample", "fused"), [
+    ((2, 64, 5, 9, 11), 64, 1, False, True),
+    ((1, 32, 6, 7, 18), 128, 1, False, False),
+    ((1, 96, 4, 6, 5), 256, 1, False, True),
+    ((1, 32, 9, 10, 12), 64, 2, False, False),
+    ((2, 64, 3, 5, 4), 64, 1, True, False),
+])
+def test_conv_keeps_group_norm_moments(pkg, dev, shape, out_c, stride, upsample, fused) -> None:
+    """ldx_conv3d_stats: the GroupNorm partial moments reduced in the conv's epilogue (or
+    its split-K reduce) -- every path of the parametrised kernel choice -- match the
+    stored output, and the output itself equals ldx_conv3d's."""
+    x, w, b = case(shape, out_c, 3, 41)
+    rng = np.random.default_rng(41)
+    res = rng.normal(size=(shape[0], *([2 * s for s in shape[2:]] if upsample else
+                                       [(s - 1) // stride + 1 for s in shape[2:]]), out_c)).astype(np.float16)
+    xt = to_dev(ndhwc(x), dev)
+    packed = pkg.ops.pack_upsample_weight(to_dev(w, dev)) if upsample else pkg.ops.pack_weight(to_dev(w, dev))
+    kw = dict(stride=stride, upsample=upsample, residual=to_dev(res, dev), output_scale=0.5)
+    if fused:
+        gamma = rng.normal(size=(shape[1],)).astype(np.float32)
+        beta = rng.normal(size=(shape[1],)).astype(np.float32)
+        kw.update(affine=pkg.ops.group_norm_affine(xt, to_dev(gamma, dev), to_dev(beta, dev), groups=32,
+                                                   eps=1e-5), silu=True)
+    y = pkg.ops.nax_conv3d(xt, packed, to_dev(b, dev), moments="always", **kw)
+    y_plain = pkg.ops.nax_conv3d(xt, packed, to_dev(b, dev), **kw)
+    torch.cuda.synchronize()
+    assert pkg.ops.moments_of(y_plain) is None
+    assert torch.equal(y, y_plain)
+    check_moments(pkg, dev, y)
+
+
+def test_group_norm_of_a_concat_from_moments(pkg, dev) -> None:
+    """The decoder's GroupNorm over concat([x, skip]) from both producers' moments, with
+    groups that straddle the two tensors (C = 96 + 64, 32 groups of 5 channels would not be
+    pairs: 16 groups of 10), against float64 GroupNorm of the concatenation."""
+    xa, wa, ba = case((1, 32, 5, 6, 7), 96, 3, 51)
+    xb, wb, bb = case((1, 32, 5, 6, 7), 64, 3, 52)
+    ya = pkg.ops.nax_conv3d(to_dev(ndhwc(xa), dev), pkg.ops.pack_weight(to_dev(wa, dev)), to_dev(ba, dev),
+                            moments="always")
+    yb = pkg.ops.nax_conv3d(to_dev(ndhwc(xb), dev), pkg.ops.pack_weight(to_dev(wb, dev)), to_dev(bb, dev),
+                            moments="always")
+    assert pkg.ops.moments_of(ya) is not None and pkg.ops.moments_of(yb) is not None
+    rng = np.random.default_rng(5)
+    gamma = rng.normal(size=(160,)).astype(np.float32)
+    beta = rng.normal(size=(160,)).astype(np.float32)
+    aff = host(pkg.ops.group_norm_affine(ya, to_dev(gamma, dev), to_dev(beta, dev), groups=16, eps=1e-5, x1=yb))
+    cat = np.concatenate([host(ya), host(yb)], axis=-1)
+    grp = cat.reshape(1, -1, 16, 10)
+    gm, gv = grp.mean(axis=(1, 3)), grp.var(axis=(1, 3))
+    scale = gamma[None] / np.sqrt(np.repeat(gv, 10, axis=1) + 1e-5)
+    np.testing.assert_allclose(aff[..., 0], scale, rtol=2e-5, atol=1e-6)
+    np.testing.assert_allclose(aff[..., 1], beta[None] - scale * np.repeat(gm, 10, axis=1), rtol=2e-5, atol=2e-5)
