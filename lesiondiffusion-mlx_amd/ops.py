@@ -172,6 +172,9 @@ def _bias32(bias: torch.Tensor | None, batch: int, out_c: int) -> tuple[torch.Te
 
 # ------------------------------------------------------------------ conv3d
 
+MOMENTS_MAX_BLOCKS = 2048
+
+
 def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = None, *,
                affine: torch.Tensor | None = None, silu: bool = False, stride: int = 1,
                upsample: bool = False, output_scale: float = 1.0,
@@ -279,8 +282,14 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     # Split-K plans (a workspace was asked for) keep no moments here: on the small tensors
     # that split, the reduce with moments (6.5 us) and their merge cost more than the
     # plain reduce plus a one-launch GroupNorm pass (measured on MI355X, config 5).
+    # Nor do outputs of more than MOMENTS_MAX_BLOCKS moment blocks per batch item (the
+    # VQ decoder's full-resolution levels): one workgroup per group merges the blocks, which
+    # there costs more (90 us) than the two-pass GroupNorm over the tensor, and the
+    # epilogue's extra work is paid on every block.
     want = moments == "always" or (moments is True and not ws_bytes)
     chunks = lib.ldx_conv3d_stats_chunks(ctypes.byref(a)) if want else 0
+    if moments != "always" and chunks > MOMENTS_MAX_BLOCKS:
+        chunks = 0
     if chunks > 0:
         m = torch.empty((b, chunks, o // 2, 3), dtype=torch.float32, device=x.device)
         check(lib.ldx_conv3d_stats(ctypes.byref(a), m.data_ptr(), _stream()), "conv3d_stats")
