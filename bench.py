@@ -288,7 +288,7 @@ def bench_config5(pkg, steps: int = 200) -> dict:
             "step_attention_gflop": round(fc.attention / 1e9, 2),
             "tflops": round(fc.total / per / 1e9, 1), "frac_peak": round(fc.total / per / 1e9 / PEAK_FP16_TFLOPS, 4),
             "config": "config 5: LINet-style UNet 9->4 ch at 32x40x40, 64/128/256/256, 2 ResBlocks/level, "
-                      "self+cross attention at 8x10x20.. levels (heads of 32), 77x768 context, fp16 random init, "
+                      "self+cross attention at the 8x10x10 and 4x5x5 levels (heads of 32), 77x768 context, fp16 random init, "
                       f"DDIM {prep.num_steps} steps, one HIP graph per step"}
 
 
@@ -367,6 +367,8 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 512 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    ap.add_argument("--only", type=int, choices=(3, 4, 5),
+                    help="run just model config 3, 4 or 5 and print its figures (profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -378,6 +380,11 @@ def main() -> int:
 
     pkg = __graft_entry__.load_package()
     torch.cuda.synchronize()
+    if args.only is not None:
+        run = {3: lambda: bench_config3(pkg, max(args.steps // 5, 5)), 4: lambda: bench_config4(pkg, 3),
+               5: lambda: bench_config5(pkg, args.steps)}[args.only]
+        print(json.dumps(run()))
+        return 0
     conv = bench_conv(pkg, args.steps, args.warmup)
     att = bench_attention(pkg, args.steps, args.warmup)
     if args.copy_calibration:
