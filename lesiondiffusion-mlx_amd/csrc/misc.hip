@@ -123,6 +123,25 @@ __global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
 // (count, mean, M2) partials; per-thread sums over a few voxels, converted to
 // (n, mean, M2) and merged (Chan et al.) in a fixed order, so results are
 // deterministic run to run.
+// Merge of a workgroup's 256 per-thread moments in a fixed order: a shfl-down tree in each
+// wave (lane l takes lane l + off, off = 32 .. 1; lane 0 ends with the wave's total), then
+// the four waves' totals in wave order through LDS (red: 12 floats). Every thread returns
+// the same total; results repeat bit for bit.
+__device__ __forceinline__ Moments block_merge256(Moments m, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const Moments o = {__shfl_down(m.n, off), __shfl_down(m.mean, off), __shfl_down(m.m2, off)};
+    m = merge(m, o);
+  }
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (lane == 0) { red[w * 3] = m.n; red[w * 3 + 1] = m.mean; red[w * 3 + 2] = m.m2; }
+  __syncthreads();
+  Moments r = {red[0], red[1], red[2]};
+#pragma unroll
+  for (int i = 1; i < 4; i++) r = merge(r, Moments{red[3 * i], red[3 * i + 1], red[3 * i + 2]});
+  return r;
+}
+
 template <int V>
 __global__ __launch_bounds__(256) void gn_partial_kernel(
     const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,
@@ -201,24 +220,16 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(
 __global__ __launch_bounds__(256) void gn_finalize_kernel(
     const float* __restrict__ partial, int nchunks, int C, int G, const float* __restrict__ gamma,
     const float* __restrict__ beta, float eps, float* __restrict__ affine) {
-  __shared__ float sn[256], sm[256], s2[256];
+  __shared__ float red[12];
   const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   Moments m = {0.f, 0.f, 0.f};
   for (int j = t; j < nchunks; j += 256) {
     const float* pp = partial + (((int64_t)b * nchunks + j) * G + g) * 3;
     m = merge(m, Moments{pp[0], pp[1], pp[2]});
   }
-  sn[t] = m.n; sm[t] = m.mean; s2[t] = m.m2;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) {
-      const Moments r = merge(Moments{sn[t], sm[t], s2[t]}, Moments{sn[t + off], sm[t + off], s2[t + off]});
-      sn[t] = r.n; sm[t] = r.mean; s2[t] = r.m2;
-    }
-    __syncthreads();
-  }
-  const float mean = sm[0];
-  const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
+  const Moments tot = block_merge256(m, red);
+  const float mean = tot.mean;
+  const float var = tot.n > 0.f ? tot.m2 / tot.n : 0.f;
   const float rstd = 1.0f / sqrtf(var + eps);
   const int gs = C / G;
   for (int c = g * gs + t; c < (g + 1) * gs; c += 256) {
@@ -236,7 +247,7 @@ __global__ __launch_bounds__(256) void gn_small_kernel(
     const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,
     int C, int G, int64_t S, const float* __restrict__ gamma, const float* __restrict__ beta,
     float eps, float* __restrict__ affine) {
-  __shared__ float sn[256], sm[256], s2[256];
+  __shared__ float red[12];
   const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int gs = C / G, c0 = g * gs;
   auto at = [&](int64_t v, int c) -> float {
@@ -262,21 +273,15 @@ __global__ __launch_bounds__(256) void gn_small_kernel(
     }
     cnt += gs;
   }
+  Moments mt;
   {
     const float n = (float)cnt;
     const float m = n > 0.f ? sum / n : 0.f;
-    sn[t] = n; sm[t] = K + m; s2[t] = n > 0.f ? fmaxf(sq - sum * m, 0.f) : 0.f;
+    mt = {n, K + m, n > 0.f ? fmaxf(sq - sum * m, 0.f) : 0.f};
   }
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) {
-      const Moments r = merge(Moments{sn[t], sm[t], s2[t]}, Moments{sn[t + off], sm[t + off], s2[t + off]});
-      sn[t] = r.n; sm[t] = r.mean; s2[t] = r.m2;
-    }
-    __syncthreads();
-  }
-  const float mean = sm[0];
-  const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
+  const Moments tot = block_merge256(mt, red);
+  const float mean = tot.mean;
+  const float var = tot.n > 0.f ? tot.m2 / tot.n : 0.f;
   const float rstd = 1.0f / sqrtf(var + eps);
   for (int c = c0 + t; c < c0 + gs; c += 256) {
     const float sc = gamma[c] * rstd;
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(256) void gn_moments_kernel(
     const float* __restrict__ m0, int64_t n0, int P0, const float* __restrict__ m1, int64_t n1, int P1,
     int C, int G, const float* __restrict__ gamma, const float* __restrict__ beta, float eps,
     float* __restrict__ affine) {
-  __shared__ float sn[256], sm[256], s2[256];
+  __shared__ float red[12];
   const int g = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
   const int gs = C / G, u0 = g * gs / 2, nu = gs / 2;
   Moments m = {0.f, 0.f, 0.f};
@@ -321,17 +326,9 @@ __global__ __launch_bounds__(256) void gn_moments_kernel(
     for (int e = 0; e < 4; e++)
       if (i0 + e * 256 < items) m = merge(m, Moments{r[e].x, r[e].y, r[e].z});
   }
-  sn[t] = m.n; sm[t] = m.mean; s2[t] = m.m2;
-  __syncthreads();
-  for (int off = 128; off > 0; off >>= 1) {
-    if (t < off) {
-      const Moments r = merge(Moments{sn[t], sm[t], s2[t]}, Moments{sn[t + off], sm[t + off], s2[t + off]});
-      sn[t] = r.n; sm[t] = r.mean; s2[t] = r.m2;
-    }
-    __syncthreads();
-  }
-  const float mean = sm[0];
-  const float var = sn[0] > 0.f ? s2[0] / sn[0] : 0.f;
+  const Moments tot = block_merge256(m, red);
+  const float mean = tot.mean;
+  const float var = tot.n > 0.f ? tot.m2 / tot.n : 0.f;
   const float rstd = 1.0f / sqrtf(var + eps);
   for (int c = g * gs + t; c < (g + 1) * gs; c += 256) {
     const float sc = gamma[c] * rstd;
