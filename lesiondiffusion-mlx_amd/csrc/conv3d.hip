@@ -1053,6 +1053,53 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
   }
 }
 
+// Split-K finish with 16-byte accesses (O a multiple of 8, aligned rows; B x voxels x O / 8
+// below 2^31): thread per (voxel, 8 channels), partial planes summed in split order, then
+// conv_reduce_kernel's epilogue.
+__global__ __launch_bounds__(256) void conv_reduce8_kernel(ConvParams p, int nvox) {
+  const int G8 = p.O >> 3;
+  const int n8 = nvox * G8;
+  const int vol = nvox / p.B;
+  const int64_t plane = (int64_t)nvox * p.O;
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n8; i += gridDim.x * 256) {
+    const int ov = i / G8;
+    const int o = (i - ov * G8) * 8;
+    const int b = ov / vol;
+    const float* src = p.part + (int64_t)ov * p.O + o;
+    f32x4 lo = *reinterpret_cast<const f32x4*>(src), hi = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll 4
+    for (int s2 = 1; s2 < p.split; s2++) {
+      lo += *reinterpret_cast<const f32x4*>(src + s2 * plane);
+      hi += *reinterpret_cast<const f32x4*>(src + s2 * plane + 4);
+    }
+    float add[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+      const float* bb = p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o;
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(bb), b1 = *reinterpret_cast<const f32x4*>(bb + 4);
+#pragma unroll
+      for (int r = 0; r < 4; r++) { add[r] = b0[r]; add[r + 4] = b1[r]; }
+    }
+    if (p.shift) {
+      const f16x8 sh = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o);
+#pragma unroll
+      for (int r = 0; r < 8; r++) add[r] += (float)sh[r];
+    }
+    f16x8 rs = {};
+    if (p.res) rs = *reinterpret_cast<const f16x8*>(p.res + (int64_t)ov * p.resp + o);
+    f16x8 out;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float v = (lo[r] + add[r]) * p.scale;
+      if (p.res) v += (float)rs[r];
+      out[r] = post_act((f16)v, p.act);
+      float w = (hi[r] + add[r + 4]) * p.scale;
+      if (p.res) w += (float)rs[r + 4];
+      out[r + 4] = post_act((f16)w, p.act);
+    }
+    *reinterpret_cast<f16x8*>(p.y + (int64_t)ov * p.yp + o) = out;
+  }
+}
+
 // Split-K finish that also leaves GroupNorm partial moments: workgroup (k, b) of 1024
 // threads finishes output voxels [32 k, 32 k + 32) of batch item b, thread t the 8
 // channels 8 (t % G8) .. (G8 = O / 8 <= 64) of voxels t / G8 + j * VP (VP = 1024 / G8 per
@@ -1515,6 +1562,12 @@ static int launch_reduce(ConvParams& p, hipStream_t st, const char* what) {
     return check_launch(what);
   }
   const int64_t n = nvox * p.O;
+  if (p.ep_vec && p.O % 8 == 0 && n / 8 < ((int64_t)1 << 31)) {
+    const int64_t n8 = n / 8;
+    const unsigned blocks = (unsigned)((n8 + 255) / 256 < 8192 ? (n8 + 255) / 256 : 8192);
+    hipLaunchKernelGGL(conv_reduce8_kernel, dim3(blocks), dim3(256), 0, st, p, (int)nvox);
+    return check_launch(what);
+  }
   const unsigned blocks = (unsigned)((n + 255) / 256 < 8192 ? (n + 255) / 256 : 8192);
   hipLaunchKernelGGL(conv_reduce_kernel, dim3(blocks), dim3(256), 0, st, p, nvox);
   return check_launch(what);
