@@ -1449,7 +1449,10 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   const int nchunks = (p.C + t.CC - 1) / t.CC;
   p.split = 1;
   p.cps = nchunks;
-  if (wgs < 192 && nchunks > 1 && p.taps > 1 && p.C >= 128) {
+  // LDX_CONV_SPLIT_WG moves the grid size below which the reduction splits (tuning sweeps).
+  int64_t split_below = 192;
+  if (const char* env = getenv("LDX_CONV_SPLIT_WG")) split_below = atoll(env);
+  if (wgs < split_below && nchunks > 1 && p.taps > 1 && p.C >= 128) {
     int want = (int)((512 + wgs - 1) / wgs);
     if (want > nchunks) want = nchunks;
     p.cps = (nchunks + want - 1) / want;
