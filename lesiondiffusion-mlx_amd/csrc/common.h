@@ -134,11 +134,27 @@ __device__ __forceinline__ Moments merge(Moments a, Moments b) {
   return {n, a.mean + d * fb, a.m2 + b.m2 + d * d * a.n * fb};
 }
 
+// Sum of v over the lanes that share lane % L (L = 4 or 8): rotations by 8 (and 4) inside
+// each 16-lane row (DPP), then v_permlane16_swap and v_permlane32_swap of v with itself
+// (each lane gets its own value and its partner's one row / half away). No LDS traffic;
+// the additions run in a fixed order on every lane.
+template <int L>
+__device__ __forceinline__ float lane_group_sum(float v) {
+  static_assert(L == 4 || L == 8, "lane groups of 4 or 8");
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xf, 0xf, false));  // row_ror:8
+  if constexpr (L == 4)
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xf, 0xf, false));  // row_ror:4
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_int(v), __float_as_int(v), false, false);
+  v = __int_as_float(r16[0]) + __int_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r32[0]) + __int_as_float(r32[1]);
+}
+
 // GroupNorm partial moments of one wave's block of finished outputs, per channel pair.
 // Each lane holds 8 consecutive channels (4 pairs) of NI voxels (ok[i]: the voxel is an
 // output); the lanes holding the same channels are L apart (L a power of two, <= 32).
 // Two passes over the values -- the pair's mean, then its squared deviations -- each
-// summed over those lanes by an xor butterfly (every lane ends with the same sums), so the
+// summed over those lanes (lane_group_sum: every lane ends with the same sums), so the
 // block's (count, mean, M2) carry no cancellation. With `store`, the lane writes its four
 // pairs' moments as 12 consecutive floats at dst (16-byte aligned).
 template <int NI, int L>
@@ -152,12 +168,9 @@ __device__ __forceinline__ void pair_moments(const f16x8 (&v)[NI], const bool (&
 #pragma unroll
       for (int q = 0; q < 4; q++) s[q] += (float)v[i][2 * q] + (float)v[i][2 * q + 1];
     }
+  cnt = lane_group_sum<L>(cnt);
 #pragma unroll
-  for (int m = L; m < 64; m <<= 1) {
-    cnt += __shfl_xor(cnt, m);
-#pragma unroll
-    for (int q = 0; q < 4; q++) s[q] += __shfl_xor(s[q], m);
-  }
+  for (int q = 0; q < 4; q++) s[q] = lane_group_sum<L>(s[q]);
   float mean[4], m2[4];
 #pragma unroll
   for (int q = 0; q < 4; q++) { mean[q] = cnt > 0.f ? s[q] / cnt : 0.f; m2[q] = 0.f; }
@@ -171,9 +184,7 @@ __device__ __forceinline__ void pair_moments(const f16x8 (&v)[NI], const bool (&
       }
     }
 #pragma unroll
-  for (int m = L; m < 64; m <<= 1)
-#pragma unroll
-    for (int q = 0; q < 4; q++) m2[q] += __shfl_xor(m2[q], m);
+  for (int q = 0; q < 4; q++) m2[q] = lane_group_sum<L>(m2[q]);
   if (store) {
     f32x4* d = reinterpret_cast<f32x4*>(dst);
     d[0] = (f32x4){cnt, mean[0], m2[0], cnt};
