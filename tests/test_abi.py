@@ -122,3 +122,23 @@ def test_ops_fail_loudly_on_cpu_tensors(pkg) -> None:
         pkg.ops.attention(torch.zeros(1, 1, 4, 64, dtype=torch.float16),
                           torch.zeros(1, 1, 4, 64, dtype=torch.float16),
                           torch.zeros(1, 1, 4, 64, dtype=torch.float16), 0.125)
+
+
+def test_group_norm_moments_travel_with_the_tensor_the_conv_wrote(pkg) -> None:
+    """Host logic of the GroupNorm-moments hand-off (no kernel runs): moments attach to the
+    conv's output, are found only for a tensor of matching batch and channel pairs, and are
+    cleared when that tensor is written again without them."""
+    import torch
+
+    t = torch.zeros(2, 3, 4, 5, 16)
+    m = torch.zeros(2, 7, 8, 3)
+    assert pkg.ops.moments_of(t) is None
+    pkg.ops._set_moments(t, m)
+    assert pkg.ops.moments_of(t) is m
+    assert pkg.ops.moments_of(t.view(2, 60, 16)) is None           # a view is another tensor
+    other = torch.zeros(2, 3, 4, 5, 8)
+    pkg.ops._set_moments(other, m)                                  # 8 channels != 2 * 8 pairs
+    assert pkg.ops.moments_of(other) is None
+    pkg.ops._set_moments(t, None)
+    assert pkg.ops.moments_of(t) is None
+    assert pkg.ops.moments_of(None) is None
