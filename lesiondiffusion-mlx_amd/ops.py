@@ -172,7 +172,7 @@ def _bias32(bias: torch.Tensor | None, batch: int, out_c: int) -> tuple[torch.Te
 
 # ------------------------------------------------------------------ conv3d
 
-MOMENTS_MAX_BLOCKS = 2048
+MOMENTS_MAX_BLOCKS = 16384
 
 
 def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = None, *,
@@ -282,10 +282,11 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     # Split-K plans (a workspace was asked for) keep no moments here: on the small tensors
     # that split, the reduce with moments (6.5 us) and their merge cost more than the
     # plain reduce plus a one-launch GroupNorm pass (measured on MI355X, config 5).
-    # Nor do outputs of more than MOMENTS_MAX_BLOCKS moment blocks per batch item (the
-    # VQ decoder's full-resolution levels): one workgroup per group merges the blocks, which
-    # there costs more (90 us) than the two-pass GroupNorm over the tensor, and the
-    # epilogue's extra work is paid on every block.
+    # Nor do outputs of more than MOMENTS_MAX_BLOCKS moment blocks per batch item (the VQ
+    # decoder's 32-channel full-resolution convs, 10^5 blocks): one workgroup per group
+    # merges the blocks, which there costs more (90 us) than the two-pass GroupNorm over
+    # the tensor (measured on MI355X, config 4: caps of 2048 / 4096 / 16384 blocks gave
+    # 19.67 / 19.70 / 19.59 ms).
     want = moments == "always" or (moments is True and not ws_bytes)
     chunks = lib.ldx_conv3d_stats_chunks(ctypes.byref(a)) if want else 0
     if moments != "always" and chunks > MOMENTS_MAX_BLOCKS:
