@@ -178,8 +178,9 @@ int ldx_layer_norm(const void* x, int64_t x_pitch, int64_t rows, int32_t feature
  * (B, H, L, D) are views of this. head_dim in {16, 32, 64, 128, 256}.
  * mask (optional) is additive fp32 with strides (batch, head, query, key), 0 for a
  * broadcast axis; -inf removes a key; a query row with every key removed gives 0.
- * workspace (ldx_attention_workspace_bytes) receives a key-contiguous copy of V
- * made at the start of the call, so the kernel stages V^T tiles with wide stores. */
+ * No scratch memory is used: V is read as it lies and transposed by the LDS reads.
+ * ldx_attention_workspace_bytes returns 0 and the workspace fields are ignored (they
+ * may be NULL / 0); they are kept so that callers sized by the query stay valid. */
 typedef struct ldx_attention_args {
   int32_t batch, heads, q_len, kv_len, head_dim;
   const void* q; int64_t q_stride[3];   /* batch, len, head strides (elements) */
@@ -188,7 +189,7 @@ typedef struct ldx_attention_args {
   void* o; int64_t o_stride[3];
   float scale;
   const float* mask; int64_t mask_stride[4];
-  void* workspace; size_t workspace_bytes;   /* device scratch, required */
+  void* workspace; size_t workspace_bytes;   /* unused; may be NULL / 0 */
 } ldx_attention_args;
 
 size_t ldx_attention_workspace_bytes(const ldx_attention_args* args);

@@ -82,7 +82,7 @@ __device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned
 // other waves read the data).
 __device__ __forceinline__ void dma_b128(const void* src, unsigned lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory");
+               : "memory", "m0");
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -105,7 +105,7 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void* base, unsigned bytes) {
 __device__ __forceinline__ void dma_buffer_b128(i32x4 rs, unsigned voff, unsigned soff, unsigned lds) {
   asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs),
                "s"(soff), "s"(lds)
-               : "memory");
+               : "memory", "m0");
 }
 
 // 16 bytes per lane from a buffer (byte offset voff + soff; out of range reads zeros) into
@@ -152,7 +152,7 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 
 // GroupNorm partial moments of one wave's block of finished outputs, per channel pair.
 // Each lane holds 8 consecutive channels (4 pairs) of NI voxels (ok[i]: the voxel is an
-// output); the lanes holding the same channels are L apart (L a power of two, <= 32).
+// output); the lanes holding the same channels are L apart (L = 4 or 8).
 // Two passes over the values -- the pair's mean, then its squared deviations -- each
 // summed over those lanes (lane_group_sum: every lane ends with the same sums), so the
 // block's (count, mean, M2) carry no cancellation. With `store`, the lane writes its four

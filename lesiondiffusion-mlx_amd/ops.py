@@ -17,6 +17,7 @@ import math
 from dataclasses import dataclass
 
 import torch
+from torch.autograd.graph import increment_version
 
 from . import _lib
 from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, check, lib
@@ -301,20 +302,35 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     return out
 
 
+def _wrote(t: torch.Tensor) -> None:
+    """Record that a kernel wrote ``t`` through its data pointer. Torch counts in-place
+    writes in a version counter shared by every view of the same storage, but a write by
+    a kernel launched through the C ABI is invisible to it; bumping the counter here
+    makes every write -- by this library or by torch -- invalidate moments kept of any
+    view of that storage."""
+    increment_version(t)
+
+
 def _set_moments(t: torch.Tensor, m: torch.Tensor | None) -> None:
-    """Attach (or clear) the GroupNorm partial moments a conv kept of ``t`` as written."""
+    """Attach (or clear) the GroupNorm partial moments a conv kept of ``t`` as written,
+    tagged with the storage's write version after that write."""
+    _wrote(t)
     if m is None:
         if hasattr(t, "_ldx_moments"):
             del t._ldx_moments
     else:
-        t._ldx_moments = m
+        t._ldx_moments = (m, t._version)
 
 
 def moments_of(t: torch.Tensor | None) -> torch.Tensor | None:
     """The ``(B, chunks, C / 2, 3)`` moments a conv kept of ``t`` (``nax_conv3d(...,
-    moments=True)``), or None."""
-    m = getattr(t, "_ldx_moments", None) if t is not None else None
-    if m is None or t.dim() != 5 or m.shape[0] != t.shape[0] or 2 * m.shape[2] != t.shape[4]:
+    moments=True)``), or None -- also when anything has written to ``t``'s storage since
+    (a torch in-place op, another op's ``out=``, a write through another view)."""
+    kept = getattr(t, "_ldx_moments", None) if t is not None else None
+    if kept is None:
+        return None
+    m, version = kept
+    if t._version != version or t.dim() != 5 or m.shape[0] != t.shape[0] or 2 * m.shape[2] != t.shape[4]:
         return None
     return m
 
@@ -403,6 +419,7 @@ def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: fl
                              _ptr(gamma.to(torch.float32).contiguous()),
                              _ptr(beta.to(torch.float32).contiguous()), float(eps),
                              _ptr(o2), o2.stride(0), _stream()), "layer_norm")
+    _wrote(out)
     return out
 
 
@@ -493,6 +510,7 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
     if count_flops.active is not None:
         count_flops.active.attention += 4.0 * b * heads * lq * lk * d
     check(lib.ldx_attention(ctypes.byref(a), _stream()), "attention")
+    _wrote(out)
     return out
 
 

@@ -23,13 +23,13 @@ def lesion_diffusion_timesteps(steps: int, total: int = 1000) -> tuple[int, ...]
     """``value + 1`` for ``value`` in ``range(0, total, total // steps)``; an index that
     would reach ``total`` is an error (_schedules.py:11-39)."""
     if not isinstance(steps, int) or isinstance(steps, bool) or steps < 1:
-        raise ValueError("LesionDiffusion DDIM steps must be a positive integer")
+        raise ValueError(f"DDIM step count must be an int >= 1, got {steps!r}")
     if not isinstance(total, int) or isinstance(total, bool) or total < steps:
-        raise ValueError("LesionDiffusion DDIM schedule must contain at least as many timesteps")
+        raise ValueError(f"a {total!r}-entry noise schedule cannot hold {steps} DDIM steps")
     timesteps = tuple(v + 1 for v in range(0, total, total // steps))
     if timesteps[-1] >= total:
-        raise ValueError(f"LesionDiffusion DDIM steps {steps} produce out-of-bounds indices for a "
-                         f"{total}-timestep schedule; choose another diffusion_steps value")
+        raise ValueError(f"{steps} DDIM steps would index timestep {timesteps[-1]}, past the end of the "
+                         f"{total}-entry schedule; pick a step count for which it stays below {total}")
     return timesteps
 
 
@@ -122,7 +122,11 @@ class PreparedDdim:
         if tuple(step_noise.shape) != (self.num_steps, *self.cond.shape):
             raise ValueError(f"step noise must be {(self.num_steps, *self.cond.shape)}")
         self.x.copy_(initial.to(self.x.device, torch.float32))
-        self.noise = step_noise.to(device=self.x.device, dtype=torch.float32).contiguous()
+        if self.noise is None:
+            self.noise = torch.empty(step_noise.shape, dtype=torch.float32, device=self.x.device)
+        # In place: a captured step graph holds this buffer's device address, so the table
+        # must never be rebound once it exists (any dtype / device / layout is copied in).
+        self.noise.copy_(step_noise)
 
     def capture(self) -> None:
         """Capture one step (the step counter advances inside it) as a HIP graph."""

@@ -112,7 +112,8 @@ class ScaledVqDecoder(VqDecoder):
 
     def _upsample_scale(self, key: str) -> float:
         if key != "decoder.up.1.upsample.conv":
-            raise ValueError("scaled fp16 decoding requires the trained decoder layout")
+            raise ValueError(f"{key}: the 0.25 output scale is defined only for decoder.up.1's "
+                             "upsampling conv of the three-level decoder")
         return self.SCALE
 
 

@@ -9,12 +9,12 @@ def lesion_diffusion_timesteps(steps: int, total: int = 1000) -> tuple[int, ...]
     """``value + 1`` for ``value`` in ``range(0, total, total // steps)``, rejecting an
     out-of-range last index (src/lesiondiffusion_mlx/_schedules.py:11-39)."""
     if not isinstance(steps, int) or isinstance(steps, bool) or steps < 1:
-        raise ValueError("DDIM steps must be a positive integer")
+        raise ValueError(f"step count {steps!r} is not an int >= 1")
     if not isinstance(total, int) or isinstance(total, bool) or total < steps:
-        raise ValueError("DDIM schedule must contain at least as many timesteps")
+        raise ValueError(f"schedule of {total!r} entries is shorter than {steps} steps")
     t = tuple(v + 1 for v in range(0, total, total // steps))
     if t[-1] >= total:
-        raise ValueError(f"DDIM steps {steps} produce out-of-bounds indices for {total}")
+        raise ValueError(f"last timestep {t[-1]} of {steps} steps is outside a {total}-entry schedule")
     return t
 
 

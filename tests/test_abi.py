@@ -142,3 +142,29 @@ def test_group_norm_moments_travel_with_the_tensor_the_conv_wrote(pkg) -> None:
     pkg.ops._set_moments(t, None)
     assert pkg.ops.moments_of(t) is None
     assert pkg.ops.moments_of(None) is None
+
+
+def test_group_norm_moments_are_dropped_after_any_later_write(pkg) -> None:
+    """Moments are tagged with the storage's write version: a torch in-place op on the
+    tensor, a write through another view of its storage, or a library op writing it via
+    ``out=`` (which bumps the shared counter) all make ``moments_of`` return None."""
+    import torch
+
+    m = torch.zeros(1, 3, 8, 3)
+    t = torch.zeros(1, 2, 2, 2, 16)
+    pkg.ops._set_moments(t, m)
+    assert pkg.ops.moments_of(t) is m
+    t.add_(1.0)
+    assert pkg.ops.moments_of(t) is None
+
+    base = torch.zeros(1, 2, 2, 2, 48)
+    t = base[..., 16:32]
+    pkg.ops._set_moments(t, m)
+    assert pkg.ops.moments_of(t) is m
+    base[..., 40:].fill_(2.0)                                   # another slice of the same storage
+    assert pkg.ops.moments_of(t) is None
+
+    t = torch.zeros(1, 2, 2, 2, 16)
+    pkg.ops._set_moments(t, m)
+    pkg.ops._wrote(t.view(1, 8, 16))                           # what every out= writer does
+    assert pkg.ops.moments_of(t) is None

@@ -366,14 +366,20 @@ def check_moments(pkg, dev, y: torch.Tensor, groups: int = 32, eps: float = 1e-5
     np.testing.assert_allclose(aff[..., 1], offset, rtol=2e-5, atol=2e-5)
 
 
-@pytest.mark.parametrize(("shape", "out_c", "stride", "upsample", "fused"), [
-    ((2, 64, 5, 9, 11), 64, 1, False, True),
-    ((1, 32, 6, 7, 18), 128, 1, False, False),
-    ((1, 96, 4, 6, 5), 256, 1, False, True),
-    ((1, 32, 9, 10, 12), 64, 2, False, False),
-    ((2, 64, 3, 5, 4), 64, 1, True, False),
+@pytest.mark.parametrize(("shape", "out_c", "stride", "upsample", "fused", "groups"), [
+    ((2, 64, 5, 9, 11), 64, 1, False, True, 32),
+    ((1, 32, 6, 7, 18), 128, 1, False, False, 32),
+    ((1, 96, 4, 6, 5), 256, 1, False, True, 32),
+    ((1, 32, 9, 10, 12), 64, 2, False, False, 32),
+    ((2, 64, 3, 5, 4), 64, 1, True, False, 32),
+    # More (pair, block) items per group than the merge's 256 threads take in one round of
+    # four (1,024), so its loop runs several rounds with all 256 threads loaded: 8 pairs per
+    # group on config 1's grid, and the VQ decoder's 64 x 80 x 80 level (1,600 .. 12,800
+    # blocks per pair, depending on the kernel path).
+    ((1, 64, 32, 40, 40), 64, 1, False, True, 4),
+    ((1, 64, 64, 80, 80), 64, 1, False, False, 32),
 ])
-def test_conv_keeps_group_norm_moments(pkg, dev, shape, out_c, stride, upsample, fused) -> None:
+def test_conv_keeps_group_norm_moments(pkg, dev, shape, out_c, stride, upsample, fused, groups) -> None:
     """ldx_conv3d_stats: the GroupNorm partial moments reduced in the conv's epilogue (or
     its split-K reduce) -- every path of the parametrised kernel choice -- match the
     stored output, and the output itself equals ldx_conv3d's."""
@@ -394,7 +400,7 @@ def test_conv_keeps_group_norm_moments(pkg, dev, shape, out_c, stride, upsample,
     torch.cuda.synchronize()
     assert pkg.ops.moments_of(y_plain) is None
     assert torch.equal(y, y_plain)
-    check_moments(pkg, dev, y)
+    check_moments(pkg, dev, y, groups=groups)
 
 
 def test_group_norm_of_a_concat_from_moments(pkg, dev) -> None:

@@ -206,3 +206,9 @@ def test_graph_captured_ddim_matches_oracle_loop(pkg, dev) -> None:
         r = prep.run(use_graph=True).clone()
         torch.cuda.synchronize()
         assert torch.equal(r, eager), "graph replay differs from the eager loop"
+    # Noise handed over as host tensors after the capture: copied into the buffer the graph
+    # reads, so replays still see it.
+    prep.set_noise(init.cpu(), noise.cpu())
+    r = prep.run(use_graph=True).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(r, eager), "graph replay after set_noise with host tensors differs"
