@@ -151,6 +151,23 @@ int ldx_group_norm_affine(const void* x0, int64_t x0_pitch, int32_t c0,
                           const float* gamma, const float* beta, float eps,
                           float* affine, void* workspace, void* stream);
 
+/* ldx_group_norm_affine without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference (its kernels allocate their outputs through
+ * MLX). Same kernels and same results as ldx_group_norm_affine; the two-pass path's
+ * partials go to a device array of LDX_GROUP_NORM_SCRATCH_BYTES that the library holds on
+ * each GPU it runs on until the process ends. Nothing is allocated. Returns LDX_EINVAL when
+ * ldx_group_norm_workspace_bytes() of the same shape exceeds that size (at 32 groups: up
+ * to batch * ceil(voxels / 8192) <= 10922, e.g. 4 volumes of 256^3). Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race
+ * and must be ordered by the caller. */
+#define LDX_GROUP_NORM_SCRATCH_BYTES (4u << 20)
+int ldx_group_norm_affine_noalloc(const void* x0, int64_t x0_pitch, int32_t c0,
+                                  const void* x1, int64_t x1_pitch, int32_t c1,
+                                  int32_t batch, int64_t voxels, int32_t groups,
+                                  const float* gamma, const float* beta, float eps,
+                                  float* affine, void* stream);
+
 /* group_norm_affine from moments a conv left (ldx_conv3d_stats) instead of a pass over x:
  * m0 holds x0's (chunks0 blocks, c0 / 2 pairs), m1 x1's for the concat (c1 = 0: none).
  * Merged per group in a fixed order (Chan's pairwise update); c0, c1 and C / groups

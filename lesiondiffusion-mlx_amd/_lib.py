@@ -19,6 +19,7 @@ LDX_EHIP = -2
 ACT_NONE = 0
 ACT_GELU = 1
 ACT_SILU = 2
+GROUP_NORM_SCRATCH_BYTES = 4 << 20   # LDX_GROUP_NORM_SCRATCH_BYTES
 
 c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
@@ -76,6 +77,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_pack_weight": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "ldx_pack_upsample_weight": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_group_norm_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i64, c_i32, c_i32]),
+    "ldx_group_norm_affine_noalloc": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
+                                              c_vp, c_vp, c_f32, c_vp, c_vp]),
     "ldx_group_norm_affine_moments": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32,
                                                c_vp, c_vp, c_f32, c_vp, c_vp]),
     "ldx_group_norm_affine": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,

@@ -5,6 +5,7 @@
 #include "common.h"
 
 #include <cmath>
+#include <mutex>
 
 namespace ldx {
 
@@ -548,11 +549,12 @@ extern "C" size_t ldx_group_norm_workspace_bytes(int32_t batch, int64_t voxels, 
   return (size_t)(batch * nchunks * groups * 3) * sizeof(float);
 }
 
-extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, const void* x1,
-                                     int64_t p1, int32_t c1, int32_t batch, int64_t voxels,
-                                     int32_t groups, const float* gamma, const float* beta,
-                                     float eps, float* affine, void* workspace, void* stream) {
-  if (!x0 || !gamma || !beta || !affine || !workspace) return fail("group_norm_affine: null pointer");
+// Both GroupNorm entry points: statistics of x0 (and x1) into affine, the per-chunk partials
+// of the two-pass path in `workspace` (every entry is written before it is read).
+static int group_norm_affine_impl(const void* x0, int64_t p0, int32_t c0, const void* x1, int64_t p1,
+                                  int32_t c1, int32_t batch, int64_t voxels, int32_t groups,
+                                  const float* gamma, const float* beta, float eps, float* affine,
+                                  void* workspace, hipStream_t st) {
   if (c1 > 0 && !x1) return fail("group_norm_affine: c1 > 0 but x1 is null");
   const int C = c0 + (c1 > 0 ? c1 : 0);
   if (batch < 1 || voxels < 1 || c0 < 1 || groups < 1 || C % groups)
@@ -566,7 +568,6 @@ extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, con
   const int64_t chunk = gn_chunk(voxels, batch);
   const int64_t nchunks = (voxels + chunk - 1) / chunk;
   if (nchunks > 0x7fffffff || batch > 65535 || groups > 65535) return fail("group_norm_affine: too large");
-  hipStream_t st = as_stream(stream);
   if (nchunks * batch <= 16) {
     // Few chunks: the one-launch per-group kernel.
     hipLaunchKernelGGL(gn_small_kernel, dim3(groups, batch), dim3(256), 0, st, (const f16*)x0, p0, c0,
@@ -587,6 +588,65 @@ extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, con
   hipLaunchKernelGGL(gn_finalize_kernel, dim3(groups, batch), dim3(256), 0, st, part, (int)nchunks, C,
                      groups, gamma, beta, eps, affine);
   return check_launch("group_norm_affine: finalize");
+}
+
+extern "C" int ldx_group_norm_affine(const void* x0, int64_t p0, int32_t c0, const void* x1,
+                                     int64_t p1, int32_t c1, int32_t batch, int64_t voxels,
+                                     int32_t groups, const float* gamma, const float* beta,
+                                     float eps, float* affine, void* workspace, void* stream) {
+  if (!x0 || !gamma || !beta || !affine || !workspace) return fail("group_norm_affine: null pointer");
+  return group_norm_affine_impl(x0, p0, c0, x1, p1, c1, batch, voxels, groups, gamma, beta, eps, affine,
+                                workspace, as_stream(stream));
+}
+
+// ------------------------------------------- GroupNorm without a caller workspace
+// The partials of ldx_group_norm_affine_noalloc live in this file-scope device array, one
+// copy per GPU for the life of the process. Host code never passes `gn_scratch` itself to
+// a kernel (on the host it names a stand-in, not device memory): it passes the device
+// address hipGetSymbolAddress returns, looked up once per device with that device current.
+static __device__ __align__(256) float gn_scratch[LDX_GROUP_NORM_SCRATCH_BYTES / sizeof(float)];
+
+static std::mutex g_scratch_mutex;
+static void* g_scratch_ptr[64];
+
+// Device address of this device's gn_scratch (looked up on the first call per device).
+static int scratch_for_current_device(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("group_norm_affine_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return LDX_EHIP;
+  }
+  if (dev < 0 || dev >= 64) return fail("group_norm_affine_noalloc: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(gn_scratch));
+    if (e != hipSuccess || !p) {
+      set_error("group_norm_affine_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+      return LDX_EHIP;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LDX_OK;
+}
+
+extern "C" int ldx_group_norm_affine_noalloc(const void* x0, int64_t p0, int32_t c0, const void* x1,
+                                             int64_t p1, int32_t c1, int32_t batch, int64_t voxels,
+                                             int32_t groups, const float* gamma, const float* beta,
+                                             float eps, float* affine, void* stream) {
+  if (!x0 || !gamma || !beta || !affine) return fail("group_norm_affine_noalloc: null pointer");
+  const size_t need = ldx_group_norm_workspace_bytes(batch, voxels, c0 + (c1 > 0 ? c1 : 0), groups);
+  if (need > LDX_GROUP_NORM_SCRATCH_BYTES)
+    return fail("group_norm_affine_noalloc: %zu bytes of partials (batch %d, %lld voxels, %d groups) exceed "
+                "the %d-byte device scratch; use ldx_group_norm_affine with a workspace",
+                need, batch, (long long)voxels, groups, (int)LDX_GROUP_NORM_SCRATCH_BYTES);
+  void* scratch = nullptr;
+  const int rc = scratch_for_current_device(&scratch);
+  if (rc) return rc;
+  return group_norm_affine_impl(x0, p0, c0, x1, p1, c1, batch, voxels, groups, gamma, beta, eps, affine,
+                                scratch, as_stream(stream));
 }
 
 extern "C" int ldx_group_norm_affine_moments(const float* m0, int64_t chunks0, int32_t c0, const float* m1,
