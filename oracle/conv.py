@@ -170,3 +170,73 @@ def pack_upsample_weight_reference_layout(w: np.ndarray) -> np.ndarray:
     folded = fold_upsample_weight(wp)        # (8, O', 2, 2, 2, C')
     rows = folded.transpose(0, 2, 3, 4, 5, 1).reshape(8, 8 * (c + cp), o + op)
     return rows.astype(np.float16)
+
+
+def conv3d_planes(plane, depth: int, w: np.ndarray, b: np.ndarray | None = None, *, stride: int = 1,
+                  planes: list[int]) -> np.ndarray:
+    """Output D-planes ``planes`` of ``conv3d(x, w, b, stride=stride)`` (3x3x3, padding 1)
+    for an input of ``depth`` planes that is only read plane by plane: ``plane(i)`` returns
+    input plane ``i`` as ``(B, C, H, W)``. Output plane ``od`` reads input planes
+    ``od * stride + kd - 1`` (zero outside ``[0, depth)``), the same sliding window as
+    ``conv3d``; this lets a full-size layer be checked on a few planes without forming it.
+    Returns ``(B, O, len(planes), H', W')`` float64."""
+    w = np.asarray(w, dtype=np.float64)
+    o, c = w.shape[:2]
+    out = None
+    for j, od in enumerate(planes):
+        for kd in range(3):
+            i = od * stride + kd - 1
+            if not 0 <= i < depth:
+                continue
+            xp = np.pad(np.asarray(plane(i), np.float64), [(0, 0), (0, 0), (1, 1), (1, 1)])
+            bsz, _, hp, wp = xp.shape
+            oh = (hp - 3) // stride + 1
+            ow = (wp - 3) // stride + 1
+            if out is None:
+                out = np.zeros((bsz, o, len(planes), oh, ow))
+            for kh in range(3):
+                for kw in range(3):
+                    xs = xp[:, :, kh:kh + stride * (oh - 1) + 1:stride, kw:kw + stride * (ow - 1) + 1:stride]
+                    out[:, :, j] += np.moveaxis(np.tensordot(w[:, :, kd, kh, kw], xs, axes=([1], [1])), 0, 1)
+    if out is None:
+        raise ValueError("no output plane reads an input plane")
+    if b is not None:
+        b = np.asarray(b, dtype=np.float64)
+        out += b[:, :, None, None, None] if b.ndim == 2 else b[None, :, None, None, None]
+    return out
+
+
+def upsample_conv_folded_planes(plane, depth: int, folded: np.ndarray, b: np.ndarray | None = None, *,
+                                planes: list[int]) -> np.ndarray:
+    """Output D-planes ``planes`` (of the 2x grid) of ``upsample_conv_folded``, reading the
+    source plane by plane (``plane(i)`` as in ``conv3d_planes``): output plane ``2 m + pd``
+    reads source planes ``m - 1 + pd + td``, td = 0, 1, through parity pd's folded taps
+    (_nax_conv.py:168-189, 246-253). Returns ``(B, O, len(planes), 2H, 2W)`` float64."""
+    folded = np.asarray(folded, dtype=np.float64)
+    o = folded.shape[1]
+    out = None
+    for j, od in enumerate(planes):
+        pd, m = od % 2, od // 2
+        for td in range(2):
+            i = m - 1 + pd + td
+            if not 0 <= i < depth:
+                continue
+            xp = np.pad(np.asarray(plane(i), np.float64), [(0, 0), (0, 0), (1, 1), (1, 1)])
+            bsz, _, hp, wp = xp.shape
+            h, wd = hp - 2, wp - 2
+            if out is None:
+                out = np.zeros((bsz, o, len(planes), 2 * h, 2 * wd))
+            for ph in range(2):
+                for pw in range(2):
+                    parity = pd * 4 + ph * 2 + pw
+                    for th in range(2):
+                        for tw in range(2):
+                            xs = xp[:, :, ph + th:ph + th + h, pw + tw:pw + tw + wd]
+                            out[:, :, j, ph::2, pw::2] += np.moveaxis(
+                                np.tensordot(folded[parity, :, td, th, tw, :], xs, axes=([1], [1])), 0, 1)
+    if out is None:
+        raise ValueError("no output plane reads a source plane")
+    if b is not None:
+        b = np.asarray(b, dtype=np.float64)
+        out += b[:, :, None, None, None] if b.ndim == 2 else b[None, :, None, None, None]
+    return out

@@ -167,6 +167,38 @@ def test_upsample_fold_equals_conv_of_nearest_upsampling() -> None:
     np.testing.assert_allclose(ours, ref, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("stride", [1, 2])
+def test_conv_plane_slabs_equal_torch_planes(stride) -> None:
+    """``conv3d_planes`` (input read plane by plane) gives torch's F.conv3d output planes,
+    boundary planes included, for odd and even depths."""
+    rng = np.random.default_rng(3)
+    for shape in ((2, 5, 7, 6, 5), (1, 3, 6, 5, 8)):
+        x = rng.standard_normal(shape)
+        w = rng.standard_normal((4, shape[1], 3, 3, 3))
+        b = rng.standard_normal((shape[0], 4))
+        ref = F.conv3d(torch.from_numpy(x), torch.from_numpy(w), None, stride=stride, padding=1).numpy()
+        ref = ref + b[:, :, None, None, None]
+        od = ref.shape[2]
+        planes = [0, od // 2, od - 1]
+        ours = ocv.conv3d_planes(lambda i: x[:, :, i], shape[2], w, b, stride=stride, planes=planes)
+        np.testing.assert_allclose(ours, ref[:, :, planes], rtol=1e-12, atol=1e-12)
+
+
+def test_upsample_plane_slabs_equal_conv_of_nearest_upsampling() -> None:
+    """``upsample_conv_folded_planes`` gives the planes of ``upsample_conv_folded`` exactly and
+    of conv(upsample(x)) to the fold's float32 rounding, for both parities at the borders."""
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((1, 3, 4, 3, 5))
+    w = rng.standard_normal((5, 3, 3, 3, 3)).astype(np.float32)
+    b = rng.standard_normal(5)
+    folded = ocv.fold_upsample_weight(w).astype(np.float64)
+    planes = [0, 1, 4, 7]
+    ours = ocv.upsample_conv_folded_planes(lambda i: x[:, :, i], 4, folded, b, planes=planes)
+    np.testing.assert_allclose(ours, ocv.upsample_conv_folded(x, folded, b)[:, :, planes], rtol=1e-12, atol=1e-12)
+    ref = ocv.conv3d(ocv.upsample_nearest2(x), w.astype(np.float64), b)[:, :, planes]
+    np.testing.assert_allclose(ours, ref, rtol=1e-5, atol=1e-5)
+
+
 def test_nearest_rules() -> None:
     x = np.arange(2 * 3 * 2).reshape(1, 1, 2, 3, 2).astype(np.float64)
     up = ocv.upsample_nearest2(x)
