@@ -32,10 +32,26 @@ sys.path.insert(0, str(REPO))
 METRIC = "conv3d & flash-attn TFLOP/s (% MFMA peak); ms per 3D-UNet denoise step"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
-# HBM bytes per config-1 conv launch: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over
-# this script with --copy-calibration, each divided by what the counter reports per byte
-# of a plain 512 MiB device copy (FETCH 0.5, WRITE 1.0); profiles/conv3d_config1.txt.
-CONV_CONFIG1_TRAFFIC_BYTES = 17.94e6
+# HBM bytes per config-1 conv launch come from the committed profile of the benched kernel:
+# rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over this script with --copy-calibration,
+# each divided by what the counter reports per byte of a plain 512 MiB device copy. The
+# profile states them on a line "roofline.traffic: <bytes> bytes per launch (revision <rev>)".
+CONV_PROFILE = REPO / "profiles" / "conv3d_config1.txt"
+
+
+def profiled_traffic() -> tuple[float | None, str | None]:
+    """(HBM bytes per config-1 launch, "profile @ revision") from CONV_PROFILE, or (None,
+    None) when the profile states none."""
+    import re
+
+    try:
+        text = CONV_PROFILE.read_text()
+    except OSError:
+        return None, None
+    m = re.search(r"roofline\.traffic:\s*([0-9.eE+]+) bytes per launch \(revision ([0-9a-f]+)\)", text)
+    if not m:
+        return None, None
+    return float(m.group(1)), f"{CONV_PROFILE.relative_to(REPO)} @ {m.group(2)}"
 
 
 # Each timed region is one replay of the K captured launches; the reported figure is the
@@ -43,6 +59,8 @@ CONV_CONFIG1_TRAFFIC_BYTES = 17.94e6
 # microseconds while the host is still submitting its packets (seen in kernel traces as a
 # run of idle gaps inside one replay), and the median keeps that out of the per-launch time.
 TIMED_REPLAYS = 3
+# The 200-step config-5 loop is timed this many times; the median is reported.
+CONFIG5_RUNS = 5
 
 
 def _graph_time(launch, steps: int, warmup: int) -> float:
@@ -272,28 +290,80 @@ def bench_config5(pkg, steps: int = 200) -> dict:
     prep.set_noise(init, noise)
     prep.run()  # warm replay
     torch.cuda.synchronize()
-    prep.set_noise(init, noise)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    out = prep.run()
-    end.record()
-    torch.cuda.synchronize()
-    total = start.elapsed_time(end)
-    assert bool(torch.isfinite(out).all())
+    totals = []
+    for _ in range(CONFIG5_RUNS):
+        prep.set_noise(init, noise)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record()
+        out = prep.run()
+        end.record()
+        torch.cuda.synchronize()
+        totals.append(start.elapsed_time(end))
+        assert bool(torch.isfinite(out).all())
+    total = float(np.median(totals))
     per = total / prep.num_steps
     return {"ms_per_step": round(per, 4), "total_ms": round(total, 2), "steps": prep.num_steps,
+            "total_ms_runs": [round(t, 2) for t in totals],
             "step_gflop": round(fc.total / 1e9, 1), "step_conv_gflop": round(fc.conv / 1e9, 1),
             "step_attention_gflop": round(fc.attention / 1e9, 2),
             "tflops": round(fc.total / per / 1e9, 1), "frac_peak": round(fc.total / per / 1e9 / PEAK_FP16_TFLOPS, 4),
             "config": "config 5: LINet-style UNet 9->4 ch at 32x40x40, 64/128/256/256, 2 ResBlocks/level, "
                       "self+cross attention at the 8x10x10 and 4x5x5 levels (heads of 32), 77x768 context, fp16 random init, "
-                      f"DDIM {prep.num_steps} steps, one HIP graph per step"}
+                      f"DDIM {prep.num_steps} steps, one HIP graph per step; total_ms is the median of "
+                      f"{CONFIG5_RUNS} runs"}
 
 
-def cpu_baseline_conv(x, w, b, budget_s: float = 15.0) -> dict:
-    """The float64 oracle conv (oracle/conv.py) on the host cores, on a bounded sample:
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_threads() -> int:
+    import torch
+
+    n = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(n)
+    return torch.get_num_threads()
+
+
+def cpu_baseline_conv(x, w, b, budget_s: float = 10.0) -> dict:
+    """The headline CPU baseline: torch CPU fp32 ``F.conv3d`` (channels-last-3d input) of the
+    same seeded config-1 tensors on the host cores -- the stand-in for the reference's
+    ``mx.cpu`` path, which needs macOS arm64 -- repeated full config-1 convolutions until
+    ``budget_s`` seconds have elapsed."""
+    import torch
+    import torch.nn.functional as F
+
+    cores = _cpu_threads()
+    xc = x.float().cpu().permute(0, 4, 1, 2, 3).contiguous(memory_format=torch.channels_last_3d)
+    wc, bc = w.float().cpu(), b.float().cpu()
+    n = 0
+    with torch.no_grad():
+        F.conv3d(xc, wc, bc, padding=1)
+        t0 = time.perf_counter()
+        while True:
+            F.conv3d(xc, wc, bc, padding=1)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+    flop = 2.0 * 51200 * 64 * 64 * 27
+    return {"value": round(flop * n / el / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{n} full config-1 convolutions in {el:.1f} s: torch {torch.__version__} CPU fp32 F.conv3d "
+                      f"(channels_last_3d) on {cores} threads of a {cpu_model()}; a stand-in for the reference's "
+                      "MLX mx.cpu path, which needs macOS arm64"}
+
+
+def cpu_oracle_conv(x, w, b, budget_s: float = 5.0) -> dict:
+    """The float64 oracle conv (oracle/conv.py, per-tap BLAS products) on the host cores,
     repeated full config-1 convolutions until ``budget_s`` seconds have elapsed."""
     from oracle import conv as ocv
 
@@ -310,38 +380,84 @@ def cpu_baseline_conv(x, w, b, budget_s: float = 15.0) -> dict:
             break
     flop = 2.0 * 51200 * 64 * 64 * 27
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": flop * n / el / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{n} full config-1 convolutions (float64 NumPy oracle, per-tap BLAS products) in {el:.1f} s"}
+    return {"value": round(flop * n / el / 1e12, 4), "unit": "TFLOP/s", "threads": threads,
+            "sample": f"{n} full config-1 convolutions (float64 NumPy oracle) in {el:.1f} s"}
 
 
-def cpu_torch_fp32(x, w, b, qkv) -> dict:
-    """torch CPU fp32 on the same seeded tensors (F.conv3d on channels_last_3d input,
-    F.scaled_dot_product_attention): median of 5 timed calls after one warm-up."""
+def cpu_torch_attention(qkv) -> dict:
+    """torch CPU fp32 ``F.scaled_dot_product_attention`` on config 2's self-attention
+    tensors: median of 5 timed calls after one warm-up."""
     import torch
     import torch.nn.functional as F
 
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    torch.set_num_threads(cores)
-    xc = x.float().cpu().permute(0, 4, 1, 2, 3).contiguous(memory_format=torch.channels_last_3d)
-    wc, bc = w.float().cpu(), b.float().cpu()
+    cores = _cpu_threads()
     q, k, v = (t.float().cpu() for t in qkv)
-
-    def med(fn):
-        fn()
+    with torch.no_grad():
+        F.scaled_dot_product_attention(q, k, v, scale=0.125)
         ts = []
         for _ in range(5):
             t0 = time.perf_counter()
-            fn()
+            F.scaled_dot_product_attention(q, k, v, scale=0.125)
             ts.append(time.perf_counter() - t0)
-        return float(np.median(ts))
+    ta = float(np.median(ts))
+    return {"self_attention_tflops": round(4.0 * 8 * 1600 * 1600 * 64 / ta / 1e12, 4),
+            "self_attention_ms": round(ta * 1e3, 2), "cores": cores}
 
-    with torch.no_grad():
-        tc = med(lambda: F.conv3d(xc, wc, bc, padding=1))
-        ta = med(lambda: F.scaled_dot_product_attention(q, k, v, scale=0.125))
-    return {"conv3d_tflops": round(2.0 * 51200 * 64 * 64 * 27 / tc / 1e12, 4), "conv3d_ms": round(tc * 1e3, 2),
-            "self_attention_tflops": round(4.0 * 8 * 1600 * 1600 * 64 / ta / 1e12, 4),
-            "self_attention_ms": round(ta * 1e3, 2), "cores": cores,
-            "note": "CPU baseline (torch, not MLX): the reference's mx.cpu path needs macOS arm64"}
+
+def cpu_models(pkg) -> dict:
+    """Configs 3, 4 and 5 on the host cores in torch CPU fp32 (oracle/torch_cpu.py: the same
+    layer graphs, the same seeded weights and inputs as the GPU runs): config 3 the median
+    of 3 runs, config 5 two UNet forwards (the DDIM update's elementwise work is left out)
+    extrapolated to 200 steps, config 4 one decode."""
+    import torch
+
+    from oracle import torch_cpu as tcpu
+    from oracle import unet as oun
+
+    cores = _cpu_threads()
+    out = {"cores": cores, "cpu": cpu_model(),
+           "note": "torch CPU fp32 (not MLX: the reference's mx.cpu path needs macOS arm64)"}
+    rng = np.random.default_rng(0)
+    cfg3 = oun.UnetConfig(64, 2, (), (1, 2, 4, 4), 32, True)
+    w3 = _half(pkg.unet.unet_state_dict(pkg.unet.UnetConfig(64, 2, (), (1, 2, 4, 4), 32, True), in_channels=4,
+                                        out_channels=4, context_dim=None, seed=0))
+    net3 = tcpu.TorchUnet(w3, cfg3)
+    x3 = rng.standard_normal((1, 4, 32, 40, 40)).astype(np.float32)
+    t = np.array([500], np.int32)
+    net3.encoder_stack(x3, t)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        net3.encoder_stack(x3, t)
+        ts.append(time.perf_counter() - t0)
+    out["config3_ms"] = round(1e3 * float(np.median(ts)), 1)
+
+    cfg5 = oun.UnetConfig(64, 2, (4, 8), (1, 2, 4, 4), 32, False)
+    w5 = _half(pkg.unet.unet_state_dict(pkg.unet.UnetConfig(64, 2, (4, 8), (1, 2, 4, 4), 32, False), in_channels=9,
+                                        out_channels=4, context_dim=768, seed=0))
+    net5 = tcpu.TorchUnet(w5, cfg5)
+    x5 = rng.standard_normal((1, 9, 32, 40, 40)).astype(np.float32)
+    ctx = rng.standard_normal((1, 77, 768)).astype(np.float32)
+    net5.forward(x5, np.array([996], np.int32), ctx)
+    t0 = time.perf_counter()
+    for step_t in (996, 991):
+        net5.forward(x5, np.array([step_t], np.int32), ctx)
+    per = (time.perf_counter() - t0) / 2
+    out["config5_ms_per_step"] = round(per * 1e3, 1)
+    out["config5_200_steps_s_extrapolated"] = round(per * 200, 1)
+
+    w4, kw = pkg.vq.vq_decoder_state_dict(latent_channels=8, levels=[(3, 256, True), (2, 128, True), (1, 64, False),
+                                                                     (0, 32, False)],
+                                          mid_channels=256, mid_attention=True, seed=0)
+    dec = tcpu.TorchVqDecoder(_half(w4), levels=kw["levels"], upsample_levels=kw["upsample_levels"])
+    z = rng.standard_normal((1, 8, 32, 40, 40)).astype(np.float32)
+    t0 = time.perf_counter()
+    y = dec.decode(z)
+    out["config4_ms"] = round((time.perf_counter() - t0) * 1e3, 1)
+    assert tuple(y.shape) == (1, 1, 128, 160, 160)
+    del y
+    torch.set_num_threads(cores)
+    return out
 
 
 def copy_calibration(mib: int = 512, reps: int = 3) -> None:
@@ -386,6 +502,7 @@ def main() -> int:
         print(json.dumps(run()))
         return 0
     conv = bench_conv(pkg, args.steps, args.warmup)
+    traffic, traffic_src = profiled_traffic()
     att = bench_attention(pkg, args.steps, args.warmup)
     if args.copy_calibration:
         copy_calibration()
@@ -406,7 +523,7 @@ def main() -> int:
                                "D x H x W = 32 x 40 x 40, seed 0", "global_batch": 1},
         "roofline": {"bound": "mfma", "achieved": round(conv["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(conv["tflops"] / PEAK_FP16_TFLOPS, 4),
-                     "traffic": CONV_CONFIG1_TRAFFIC_BYTES},
+                     "traffic": traffic, "traffic_source": traffic_src},
         "attention": {
             "self_tflops": round(att["self"]["tflops"], 2), "self_ms": round(att["self"]["ms"], 5),
             "self_frac_peak": round(att["self"]["frac_peak"], 4),
@@ -421,7 +538,10 @@ def main() -> int:
         line["denoise_step"] = bench_config5(pkg, 200)
     if not args.skip_cpu:
         line["cpu_baseline"] = cpu_baseline_conv(conv["x"], conv["w"], conv["b"])
-        line["cpu_torch_fp32"] = cpu_torch_fp32(conv["x"], conv["w"], conv["b"], att["_tensors"])
+        line["cpu_baseline_attention"] = cpu_torch_attention(att["_tensors"])
+        line["cpu_oracle_float64"] = cpu_oracle_conv(conv["x"], conv["w"], conv["b"])
+        if not args.skip_model:
+            line["cpu_models"] = cpu_models(pkg)
     print(json.dumps(line))
     return 0
 

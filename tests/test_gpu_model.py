@@ -41,6 +41,10 @@ def assert_matches_recording(got: np.ndarray, recorded: np.ndarray, oracle_half:
     relative per element and the fp16 parity bar against the recording, and 2e-3 against
     the oracle evaluated with the fused path's storage points."""
     rec = recorded.astype(np.float64)
+    excess = lambda a: float(np.max(np.abs(a - rec) - (2e-3 + 2e-3 * np.abs(rec))))
+    print(f"vs recording: max abs {np.abs(got - rec).max():.3e}, excess over 2e-3 + 2e-3|rec| {excess(got):.3e}; "
+          f"reference rounding (oracle): max abs {np.abs(oracle_half - rec).max():.3e}, excess "
+          f"{excess(oracle_half):.3e}")
     np.testing.assert_allclose(got, rec, atol=3e-3, rtol=2e-3)
     assert_fp16_bar(got, rec, rel_l2=1e-2)
     np.testing.assert_allclose(got, oracle_half, atol=2e-3, rtol=2e-3)

@@ -320,3 +320,50 @@ def test_timestep_embedding_closed_form() -> None:
     np.testing.assert_allclose(e[0], [1, 1, 1, 1, 0, 0, 0, 0], atol=0)
     f = np.exp(-math.log(10000) * np.arange(4) / 4)
     np.testing.assert_allclose(e[1], np.concatenate([np.cos(17 * f), np.sin(17 * f)]), rtol=1e-5, atol=1e-6)
+
+
+# -------------------------------------------------- torch fp32 CPU baseline networks
+
+def test_torch_cpu_unet_matches_float64_oracle() -> None:
+    """The benchmark's torch-fp32 CPU network (oracle/torch_cpu.py) computes the oracle
+    network: the recorded ``unet_mask`` architecture with cross attention to a context (both
+    attentions, the concat decoder, upsampling) and its encoder stack agree with the float64
+    oracle to fp32 accuracy."""
+    import importlib
+    import json
+
+    from oracle import fixture_weights as ofw
+    from oracle import unet as oun
+
+    tcpu = importlib.import_module("oracle.torch_cpu")
+    z = load_fixture("unet_mask")
+    c = json.loads(z["config"].item())
+    cfg = oun.UnetConfig(c["model_channels"], c["num_res_blocks"], tuple(c["attention_resolutions"]),
+                         tuple(c["channel_mult"]), c["num_head_channels"], False)
+    w = ofw.unet_fixture_weights(101, skip_context=False)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((1, 4, 8, 8, 8))
+    ctx = rng.standard_normal((1, 3, 6))
+    t = np.array([417], np.int32)
+    want = oun.Unet(w, cfg, half=False).forward(x, t, ctx)
+    got = tcpu.TorchUnet(w, cfg).forward(x, t, ctx).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+    want_e = oun.Unet(w, cfg, half=False).encoder_stack(x, t)
+    got_e = tcpu.TorchUnet(w, cfg).encoder_stack(x, t).numpy()
+    np.testing.assert_allclose(got_e, want_e, rtol=1e-4, atol=1e-5)
+
+
+def test_torch_cpu_vq_decoder_matches_float64_oracle() -> None:
+    """The torch-fp32 CPU VQ decoder (mid attention, two upsamplings) against the oracle."""
+    import importlib
+
+    lay = importlib.import_module("oracle.torch_cpu")
+    from oracle import fixture_weights as ofw
+    from oracle import unet as oun
+
+    w = ofw.vq_fixture_weights(201)
+    rng = np.random.default_rng(10)
+    z = rng.standard_normal((1, 4, 2, 3, 2))
+    want = oun.VqDecoder(w, half=False).decode(z)
+    got = lay.TorchVqDecoder(w).decode(z).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
