@@ -32,6 +32,11 @@ extern "C" {
 #define LDX_EINVAL (-1)
 #define LDX_EHIP (-2)
 
+/* Element types of the entry points that take a `dtype` argument. */
+#define LDX_DTYPE_F16 0
+#define LDX_DTYPE_F32 1
+#define LDX_DTYPE_BF16 2
+
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
 /* ABI version (4); bumped on any change to the structs below. */
@@ -260,6 +265,29 @@ int ldx_ddim_update(float* x, const void* net_out, int64_t net_pitch, const floa
 int ldx_ddim_timestep(const int32_t* step, const int32_t* t_table, int32_t batch,
                       int32_t* t_out, void* stream);
 int ldx_step_advance(int32_t* step, void* stream);
+
+/* ------------------------------------------------------- VQ codebook search -------
+ * Replaces the native four-channel nearest-codebook search nearest_codebook4
+ * (src/lesiondiffusion_mlx/_vq.py:12-82) and the quantize step of VqAutoencoder
+ * (mlx_model.py:742-803). Element type T = dtype (LDX_DTYPE_F16 or LDX_DTYPE_F32) for
+ * every array but the int32 indices; vectors are rows of 4 contiguous values.
+ *
+ * ldx_vq_squared_norms4: out[i] = T(sum_c float(T(x[i,c] * x[i,c]))), the four squares
+ * rounded to T, summed in fp32 in channel order, the sum rounded to T.
+ *
+ * ldx_vq_nearest4: for each of `positions` latent vectors z[p], the code index chosen over
+ * the `entries` codebook rows with the reference's distance and rounding points:
+ *   dot = fma(z3, c3, fma(z2, c2, fma(z1, c1, z0 * c0)))            (fp32)
+ *   distance = T(T(z_norm[p] + codebook_norm[c]) - T(2 * T(dot)))
+ * the lowest index with a NaN distance if there is one, else the lowest index of the
+ * smallest distance (MLX argmin's order; exact, independent of the scan). z_norm may be
+ * NULL (computed as in ldx_vq_squared_norms4); codebook_norm is required (computed once per
+ * codebook by the caller). quantized (may be NULL) receives the straight-through value
+ * z + (selected - z), each operation rounded to T. */
+int ldx_vq_squared_norms4(const void* x, int64_t n, int32_t dtype, void* out, void* stream);
+int ldx_vq_nearest4(const void* z, const void* z_norm, const void* codebook, const void* codebook_norm,
+                    int64_t positions, int32_t entries, int32_t dtype, int32_t* indices,
+                    void* quantized, void* stream);
 
 #ifdef __cplusplus
 }

@@ -6,6 +6,6 @@ Importing this package loads ``libldx.so`` (built by ``__graft_entry__.build()``
 fails if it is missing: every op runs a hand-written HIP kernel, there is no CPU path.
 """
 
-from . import _lib, layers, ops, sampling, unet, vq  # noqa: F401  (loads libldx.so)
+from . import _lib, layers, ops, sampling, unet, vq, weights  # noqa: F401  (loads libldx.so)
 
-__all__ = ["ops", "layers", "unet", "vq", "sampling"]
+__all__ = ["ops", "layers", "unet", "vq", "sampling", "weights"]

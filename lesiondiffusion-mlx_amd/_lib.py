@@ -19,6 +19,9 @@ LDX_EHIP = -2
 ACT_NONE = 0
 ACT_GELU = 1
 ACT_SILU = 2
+DTYPE_F16 = 0
+DTYPE_F32 = 1
+DTYPE_BF16 = 2
 GROUP_NORM_SCRATCH_BYTES = 4 << 20   # LDX_GROUP_NORM_SCRATCH_BYTES
 
 c_i32 = ctypes.c_int32
@@ -94,6 +97,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_ddim_update": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp]),
     "ldx_ddim_timestep": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp]),
     "ldx_step_advance": (c_i32, [c_vp, c_vp]),
+    "ldx_vq_squared_norms4": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_vp]),
+    "ldx_vq_nearest4": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
 }
 
 ABI_VERSION = 4

@@ -25,7 +25,8 @@ from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, check, lib
 __all__ = [
     "PackedWeight", "pack_weight", "pack_upsample_weight", "nax_conv3d", "conv3d", "dense",
     "group_norm_affine", "layer_norm", "attention", "flash_attention", "timestep_embedding",
-    "silu", "upsample_nearest2", "resize_nearest", "output_extent", "count_flops",
+    "silu", "upsample_nearest2", "resize_nearest", "output_extent", "count_flops", "squared_norms4",
+    "nearest_codebook4",
 ]
 
 
@@ -554,3 +555,52 @@ def resize_nearest(x: torch.Tensor, shape: tuple[int, int, int]) -> torch.Tensor
     if tuple(shape) == tuple(2 * int(s) for s in x.shape[1:4]):
         return upsample_nearest2(x)
     raise ValueError("only nearest 2x resizing is supported")
+
+
+# ------------------------------------------------------------ VQ codebook search
+
+_VQ_DTYPES = {torch.float16: _lib.DTYPE_F16, torch.float32: _lib.DTYPE_F32}
+
+
+def _vq_rows(t: torch.Tensor, name: str) -> int:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor; there is no CPU path")
+    if t.dtype not in _VQ_DTYPES:
+        raise ValueError(f"{name} must be float16 or float32, got {t.dtype}")
+    if t.dim() != 2 or t.shape[1] != 4 or not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous (rows, 4), got {tuple(t.shape)}")
+    if t.shape[0] < 1:
+        raise ValueError(f"{name} is empty")
+    return int(t.shape[0])
+
+
+def squared_norms4(x: torch.Tensor) -> torch.Tensor:
+    """Per-row ``T(sum float32(T(x * x)))`` of ``(rows, 4)`` vectors, the squared norm the
+    reference keeps per codebook entry (mlx_model.py:775-778)."""
+    n = _vq_rows(x, "x")
+    out = torch.empty(n, dtype=x.dtype, device=x.device)
+    check(lib.ldx_vq_squared_norms4(_ptr(x), n, _VQ_DTYPES[x.dtype], _ptr(out), _stream()), "vq_squared_norms4")
+    return out
+
+
+def nearest_codebook4(z: torch.Tensor, codebook: torch.Tensor, codebook_norm: torch.Tensor, *,
+                      quantized: torch.Tensor | None = None) -> torch.Tensor:
+    """int32 index of the nearest codebook row for each ``(positions, 4)`` latent row:
+    the reference's distance and rounding points, the first NaN distance else the first
+    smallest (nearest_codebook4, _vq.py:63-82). ``quantized`` (same shape and dtype as
+    ``z``), when given, receives the straight-through ``z + (selected - z)``."""
+    p = _vq_rows(z, "z")
+    e = _vq_rows(codebook, "codebook")
+    if codebook.dtype != z.dtype or codebook_norm.dtype != z.dtype:
+        raise ValueError("z, codebook and codebook_norm must share one dtype")
+    if not codebook_norm.is_cuda or tuple(codebook_norm.shape) != (e,) or not codebook_norm.is_contiguous():
+        raise ValueError(f"codebook_norm must be a contiguous device vector of {e} values")
+    if quantized is not None and (tuple(quantized.shape) != (p, 4) or quantized.dtype != z.dtype
+                                  or not quantized.is_contiguous() or not quantized.is_cuda):
+        raise ValueError("quantized must be a contiguous device tensor shaped and typed like z")
+    idx = torch.empty(p, dtype=torch.int32, device=z.device)
+    check(lib.ldx_vq_nearest4(_ptr(z), None, _ptr(codebook), _ptr(codebook_norm), p, e, _VQ_DTYPES[z.dtype],
+                              _ptr(idx), _ptr(quantized), _stream()), "vq_nearest4")
+    if quantized is not None:
+        _wrote(quantized)
+    return idx

@@ -1,10 +1,11 @@
 """3-D VQ-GAN decoder on the HIP ops, channels-last (src/lesiondiffusion_mlx/mlx_model.py:
 657-819) and its scaled-fp16 variant (_scaled_vq.py:27-118).
 
-``VqDecoder`` decodes an un-quantized latent (``decode(z, quantize=False)`` of the
-reference; the nearest-codebook search is not part of this build). Its level list
-generalises the reference's three-level layout so the full-resolution configuration --
-two upsamplings and a single-head mid-block attention -- uses the same code.
+``VqDecoder.decode(z)`` quantizes the latent to its nearest codebook entries first (the
+four-channel native search, ``ops.nearest_codebook4``) unless ``quantize=False``, as the
+reference's ``decode(z, quantize=True)`` does. Its level list generalises the reference's
+three-level layout so the full-resolution configuration -- two upsamplings and a
+single-head mid-block attention -- uses the same code.
 """
 
 from __future__ import annotations
@@ -27,9 +28,11 @@ class VqDecoder(SourceLayers):
     def __init__(self, weights: Mapping[str, object], *, levels: tuple[int, ...] = (2, 1, 0),
                  upsample_levels: tuple[int, ...] = (1,), blocks: int = 2, groups: int = 16,
                  eps: float = 1e-6, device="cuda"):
-        super().__init__(weights, device=device)
+        codebook = weights.get(self.CODEBOOK)
+        super().__init__({k: v for k, v in weights.items() if k != self.CODEBOOK}, device=device)
         self.levels, self.upsample_levels, self.blocks = levels, upsample_levels, blocks
         self.groups, self.eps = groups, eps
+        self.set_codebook(codebook)
         for k in list(self.weights):
             if k.endswith(".attn_1.q.weight"):
                 att = k[: -len(".q.weight")]
@@ -38,6 +41,41 @@ class VqDecoder(SourceLayers):
                 self.packed[att + ".qkv"] = ops.pack_weight(torch.cat([w.reshape(c, -1) for w in ws]).contiguous())
                 self.bias32[att + ".qkv"] = torch.cat([self.weights[f"{att}.{n}.bias"].float()
                                                        for n in ("q", "k", "v")]).contiguous()
+
+    CODEBOOK = "quantize.embedding.weight"
+    QUANTIZE_DTYPE = torch.float16
+
+    def set_codebook(self, codebook) -> None:
+        """Use ``codebook`` ``(entries, 4)`` (host or device, any float dtype; None: none) from
+        now on; its squared norms are recomputed on first use (the reference keeps them until
+        the codebook is replaced, mlx_model.py:771-778)."""
+        self._codebook = None
+        if codebook is not None:
+            t = codebook if isinstance(codebook, torch.Tensor) else torch.as_tensor(np.asarray(codebook))
+            self._codebook = t.detach().to(device=self.device, dtype=torch.float32).contiguous()
+        self._codebook_cache: dict[torch.dtype, tuple[torch.Tensor, torch.Tensor]] = {}
+
+    def codebook(self, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        """(codebook, its squared norms) in ``dtype``."""
+        if self._codebook is None:
+            raise ValueError(f"no codebook: the weights have no {self.CODEBOOK}")
+        if dtype not in self._codebook_cache:
+            cb = self._codebook.to(dtype).contiguous()
+            self._codebook_cache[dtype] = (cb, ops.squared_norms4(cb))
+        return self._codebook_cache[dtype]
+
+    def quantize(self, z: torch.Tensor, dtype: torch.dtype | None = None) -> torch.Tensor:
+        """Nearest-codebook straight-through quantization of an NDHWC four-channel latent, in
+        ``dtype`` (default: the decoder's quantization type), returned in that dtype
+        (VqAutoencoder.quantize, mlx_model.py:742-803)."""
+        dtype = dtype or self.QUANTIZE_DTYPE
+        if z.shape[-1] != 4:
+            raise ValueError(f"the native search takes four-channel latents, got {z.shape[-1]} channels")
+        flat = z.to(dtype).reshape(-1, 4).contiguous()
+        cb, norms = self.codebook(dtype)
+        out = torch.empty_like(flat)
+        ops.nearest_codebook4(flat, cb, norms, quantized=out)
+        return out.view(z.shape)
 
     def norm_silu_conv_vq(self, x, norm_key, conv_key, *, eps_scale=1.0, output_scale=1.0, residual=None,
                           moments=False):
@@ -72,9 +110,13 @@ class VqDecoder(SourceLayers):
     def _upsample_scale(self, key: str) -> float:
         return 1.0
 
-    def decode(self, z: torch.Tensor) -> torch.Tensor:
-        """NDHWC fp16 latent -> NDHWC fp16 volume at 2^(upsamplings) resolution."""
-        x = self.conv(z, "post_quant_conv")
+    def decode(self, z: torch.Tensor, *, quantize: bool = True) -> torch.Tensor:
+        """NDHWC latent -> NDHWC fp16 volume at 2^(upsamplings) resolution; the latent is
+        quantized first unless ``quantize`` is False (VqAutoencoder.decode,
+        mlx_model.py:805-819)."""
+        if quantize:
+            z = self.quantize(z)
+        x = self.conv(z.to(torch.float16), "post_quant_conv")
         x = self.conv(x, "decoder.conv_in", moments=True)
         x = self.residual(x, "decoder.mid.block_1")
         if "decoder.mid.attn_1.qkv" in self.packed:
@@ -89,9 +131,12 @@ class VqDecoder(SourceLayers):
         return self.norm_silu_conv_vq(x, "decoder.norm_out", "decoder.conv_out",
                                       eps_scale=self._eps_scale("decoder.norm_out"))
 
-    def __call__(self, z: torch.Tensor) -> torch.Tensor:
+    def __call__(self, z: torch.Tensor, *, quantize: bool = True) -> torch.Tensor:
         """Channels-first latent in, channels-first volume out."""
-        return ndhwc_to_ncdhw(self.decode(ncdhw_to_ndhwc(z.to(device=self.device, dtype=torch.float16))))
+        zz = ncdhw_to_ndhwc(z.to(device=self.device))
+        if not quantize:
+            zz = zz.to(torch.float16)
+        return ndhwc_to_ncdhw(self.decode(zz, quantize=quantize))
 
 
 class ScaledVqDecoder(VqDecoder):
@@ -101,6 +146,8 @@ class ScaledVqDecoder(VqDecoder):
     eps * 0.25^2, which leaves the normalised value unchanged."""
 
     SCALE = 0.25
+    # The latent is quantized in fp32 before the half decode (_scaled_vq.py:45-49).
+    QUANTIZE_DTYPE = torch.float32
 
     def _eps_scale(self, norm_key: str) -> float:
         scaled = norm_key == "decoder.norm_out" or (

@@ -16,6 +16,10 @@ This package restates, in float64 NumPy, what the reference
                    mlx_sampling.py:27-200).
 * ``fixture_weights`` -- the seeded weight recipes behind the reference's recorded
                    Torch-CPU fixtures (tests/_fixture_models.py:31-157).
+* ``vq``        -- the four-channel nearest-codebook search with its rounding points and
+                   the straight-through quantize (_vq.py:12-82, mlx_model.py:742-803).
+* ``torch_cpu`` -- the UNet and VQ decoder in torch fp32 on the CPU: ``bench.py``'s CPU
+                   baseline for configs 3-5 (the same layer graphs as ``unet``).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
 may import this package, and only as the checker. The product path (the HIP library

@@ -14,6 +14,7 @@ import torch
 from oracle import fixture_weights as ofw
 from oracle import sampling as osm
 from oracle import unet as oun
+from oracle import vq as ovq
 from tests.conftest import assert_fp16_bar, load_fixture
 
 pytestmark = pytest.mark.gpu
@@ -120,25 +121,56 @@ def test_linet_style_unet_matches_oracle(pkg, dev) -> None:
 
 @pytest.mark.parametrize("dtype", ["float16"])
 def test_vq_decoder_matches_recorded_torch(pkg, dev, dtype) -> None:
-    """decode(z, quantize=False) and decode(quantized) of the fixture decoder
-    (tests/test_equivalence.py:151-166), held as in ``assert_matches_recording``."""
+    """decode(z) (nearest-codebook quantization, then the decoder) and decode(z,
+    quantize=False) of the fixture decoder (tests/test_equivalence.py:151-166), held as in
+    ``assert_matches_recording``."""
     z = load_fixture("vq_" + dtype)
     w16 = {k: v.astype(np.float16) for k, v in ofw.vq_fixture_weights(int(z["weight_seed"])).items()}
     dec = pkg.vq.VqDecoder(w16)
     ora = oun.VqDecoder(w16, half=True)
-    for key, inp in (("decoded_unquantized", z["z"].astype(np.float16)), ("decoded", z["quantized"])):
-        got = dec(torch.from_numpy(inp).to(dev))
+    z16 = z["z"].astype(np.float16)
+    _, q = ovq.quantize4(z16.transpose(0, 2, 3, 4, 1).reshape(-1, 4), w16["quantize.embedding.weight"], np.float16)
+    q = q.reshape(1, 2, 2, 2, 4).transpose(0, 4, 1, 2, 3)
+    for key, quantize, oracle_in in (("decoded_unquantized", False, z16), ("decoded", True, q)):
+        got = dec(torch.from_numpy(z16).to(dev), quantize=quantize)
         torch.cuda.synchronize()
-        assert_matches_recording(got.float().cpu().numpy(), z[key], ora.decode(inp))
+        assert_matches_recording(got.float().cpu().numpy(), z[key], ora.decode(oracle_in))
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_vq_quantize_matches_recorded_torch_bit_for_bit(pkg, dev, dtype) -> None:
+    """The quantize step on the GPU equals the recorded source quantize bit for bit
+    (tests/test_equivalence.py:164, ``assert_bits``), in fp16 and in fp32."""
+    z = load_fixture("vq_" + dtype)
+    t = getattr(torch, dtype)
+    w = ofw.vq_fixture_weights(int(z["weight_seed"]))
+    dec = pkg.vq.VqDecoder({k: v.astype(np.float16) for k, v in w.items()})
+    dec.set_codebook(w["quantize.embedding.weight"].astype(dtype))
+    zz = torch.from_numpy(z["z"].transpose(0, 2, 3, 4, 1).copy()).to(dev)
+    got = dec.quantize(zz, t)
+    torch.cuda.synchronize()
+    assert got.dtype == t
+    want = z["quantized"].transpose(0, 2, 3, 4, 1)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16 if dtype == "float16" else np.uint32),
+                                  want.view(np.uint16 if dtype == "float16" else np.uint32))
 
 
 def test_scaled_vq_decoder_matches_fp32_decoder(pkg, dev) -> None:
-    """The scaled fp16 decoder (_scaled_vq.py) against the recorded fp32 decoder output."""
+    """The scaled fp16 decoder (_scaled_vq.py) against the recorded fp32 decoder outputs: the
+    unquantized decode, and decode(z) with the latent quantized in fp32 against an fp32
+    codebook first (_scaled_vq.py:45-49)."""
     z = load_fixture("vq_float32")
-    w16 = {k: v.astype(np.float16) for k, v in ofw.vq_fixture_weights(int(z["weight_seed"])).items()}
-    got = pkg.vq.ScaledVqDecoder(w16)(torch.from_numpy(z["z"].astype(np.float16)).to(dev))
+    w = ofw.vq_fixture_weights(int(z["weight_seed"]))
+    w16 = {k: v.astype(np.float16) for k, v in w.items()}
+    dec = pkg.vq.ScaledVqDecoder(w16)
+    dec.set_codebook(w["quantize.embedding.weight"].astype(np.float32))
+    zt = torch.from_numpy(z["z"]).to(dev)
+    got = dec(zt.half(), quantize=False)
     torch.cuda.synchronize()
     np.testing.assert_allclose(got.float().cpu().numpy(), z["decoded_unquantized"], atol=2e-3, rtol=2e-3)
+    got = dec(zt)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(got.float().cpu().numpy(), z["decoded"], atol=2e-3, rtol=2e-3)
 
 
 def test_vq_decoder_with_mid_attention_matches_oracle(pkg, dev) -> None:
@@ -149,7 +181,7 @@ def test_vq_decoder_with_mid_attention_matches_oracle(pkg, dev) -> None:
     w16 = {k: v.astype(np.float16) for k, v in w.items()}
     rng = np.random.default_rng(8)
     zz = rng.standard_normal((1, 8, 4, 5, 6)).astype(np.float16)
-    got = pkg.vq.VqDecoder(w16, **kw)(torch.from_numpy(zz).to(dev))
+    got = pkg.vq.VqDecoder(w16, **kw)(torch.from_numpy(zz).to(dev), quantize=False)
     torch.cuda.synchronize()
     ora = oun.VqDecoder(w16, half=True, levels=kw["levels"], upsample_levels=kw["upsample_levels"]).decode(zz)
     assert got.shape == ora.shape == (1, 1, 16, 20, 24)

@@ -367,3 +367,72 @@ def test_torch_cpu_vq_decoder_matches_float64_oracle() -> None:
     want = oun.VqDecoder(w, half=False).decode(z)
     got = lay.TorchVqDecoder(w).decode(z).numpy()
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-5)
+
+
+# ---------------------------------------------------------------- VQ codebook search
+
+def _round_fraction_f32(x) -> np.float32:
+    """The float32 nearest the exact rational ``x`` (ties to even), by comparing neighbours."""
+    from fractions import Fraction
+
+    f = np.float32(float(x))
+    cands = [f, np.nextafter(f, np.float32(-np.inf)), np.nextafter(f, np.float32(np.inf))]
+    best = min(cands, key=lambda c: (abs(Fraction(float(c)) - x),
+                                     int(np.frombuffer(np.float32(c).tobytes(), np.uint32)[0]) & 1))
+    return np.float32(best)
+
+
+def test_fma32_is_correctly_rounded() -> None:
+    """``oracle.vq.fma32`` equals the exactly rounded a * b + c: on random operands of mixed
+    magnitudes and on hand-built cases whose product is a float32 midpoint and whose addend
+    is too small for the float64 sum (plain float64 evaluation rounds those the wrong way)."""
+    from fractions import Fraction
+
+    from oracle import vq as ovq
+
+    rng = np.random.default_rng(21)
+    a = (rng.standard_normal(400) * 2.0 ** rng.integers(-20, 20, 400)).astype(np.float32)
+    b = (rng.standard_normal(400) * 2.0 ** rng.integers(-20, 20, 400)).astype(np.float32)
+    c = (-(a.astype(np.float64) * b) * (1 + rng.standard_normal(400) * 1e-6)).astype(np.float32)
+    # a * b = 24929 * (673 / 2^24) = 1 + 2^-24 exactly, halfway between 1 and 1 + 2^-23.
+    ma, mb = np.float32(24929.0), np.float32(673.0 * 2.0 ** -24)
+    a = np.concatenate([a, [ma, ma, ma]]).astype(np.float32)
+    b = np.concatenate([b, [mb, mb, mb]]).astype(np.float32)
+    c = np.concatenate([c, [2.0 ** -80, -(2.0 ** -80), 0.0]]).astype(np.float32)
+    got = ovq.fma32(a, b, c)
+    want = np.array([_round_fraction_f32(Fraction(float(x)) * Fraction(float(y)) + Fraction(float(z)))
+                     for x, y, z in zip(a, b, c)], np.float32)
+    np.testing.assert_array_equal(got, want)
+    assert got[-3] == np.float32(1 + 2.0 ** -23) and got[-2] == np.float32(1.0) and got[-1] == np.float32(1.0)
+
+
+def test_vq_selection_rule_closed_forms() -> None:
+    """The selection is the first NaN, else the first smallest distance: ties keep the lower
+    index, -0 equals +0, +inf rows give index 0."""
+    from oracle import vq as ovq
+
+    d = np.array([[3, 1, 1, 2], [3, np.nan, 1, np.nan], [np.inf, np.inf, np.inf, np.inf],
+                  [0.0, -0.0, -1, -1], [5, 4, 3, np.nan]], np.float32)
+    assert np.argmin(d, axis=1).tolist() == [1, 1, 0, 2, 3]
+    # a two-code book where the latent sits exactly between the codes: a tie, index 0
+    cb = np.array([[0, 0, 0, 0], [2, 0, 0, 0]], np.float32)
+    for t in (np.float16, np.float32):
+        assert ovq.nearest_codebook4(np.array([[1, 0, 0, 0]], t), cb, t).tolist() == [0]
+        assert ovq.nearest_codebook4(np.array([[1.75, 0, 0, 0]], t), cb, t).tolist() == [1]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_vq_oracle_matches_recorded_quantize_bit_for_bit(dtype: str) -> None:
+    """The recorded source quantize of the fixture latent (tests/test_equivalence.py:164,
+    ``assert_bits``) with the fixture codebook, reproduced exactly."""
+    from oracle import vq as ovq
+
+    z = load_fixture("vq_" + dtype)
+    t = np.dtype(dtype)
+    cb = ofw.vq_fixture_weights(int(z["weight_seed"]))["quantize.embedding.weight"].astype(t)
+    flat = z["z"].astype(t).transpose(0, 2, 3, 4, 1).reshape(-1, 4)
+    _, q = ovq.quantize4(flat, cb, t)
+    want = z["quantized"].transpose(0, 2, 3, 4, 1).reshape(-1, 4)
+    assert q.dtype == want.dtype
+    np.testing.assert_array_equal(q.view(np.uint16 if t == np.float16 else np.uint32),
+                                  want.view(np.uint16 if t == np.float16 else np.uint32))
