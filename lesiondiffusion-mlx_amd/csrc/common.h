@@ -75,6 +75,11 @@ __device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigne
 // flat address).
 __device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned)(uintptr_t)p; }
 
+// The two LDS-DMA helpers below write M0. M0 is a reserved register on gfx9: the
+// compiler keeps no value of its own in it across code it did not generate (it sets M0
+// right before each instruction of its own that reads it), and clang rejects M0 in a
+// clobber list (a reserved register there is undefined behaviour), so none is given.
+//
 // 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
 // (global_load_lds_dwordx4). Issued as asm so that the compiler's wait insertion,
 // which cannot tell these writes from the halo, does not drain all of them before
@@ -82,7 +87,7 @@ __device__ __forceinline__ unsigned lds_offset(const void* p) { return (unsigned
 // other waves read the data).
 __device__ __forceinline__ void dma_b128(const void* src, unsigned lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds)
-               : "memory", "m0");
+               : "memory");
 }
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -105,7 +110,7 @@ __device__ __forceinline__ i32x4 dma_rsrc(const void* base, unsigned bytes) {
 __device__ __forceinline__ void dma_buffer_b128(i32x4 rs, unsigned voff, unsigned soff, unsigned lds) {
   asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(rs),
                "s"(soff), "s"(lds)
-               : "memory", "m0");
+               : "memory");
 }
 
 // 16 bytes per lane from a buffer (byte offset voff + soff; out of range reads zeros) into
