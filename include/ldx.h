@@ -4,7 +4,8 @@
  * LayerNorm, weight packing and the DDIM step.
  *
  * Conventions
- *  - Activations are channels-last NDHWC float16 ("voxels x channels"); every
+ *  - Activations are channels-last NDHWC float16 ("voxels x channels"), or bfloat16 where
+ *    an entry point takes a dtype (conv3d, attention, the weight packers); every
  *    activation pointer comes with a voxel pitch in elements (>= channels), so a
  *    kernel can read or write a channel slice of a wider tensor (zero-copy concat).
  *  - All pointers are device pointers owned by the caller; no entry point allocates
@@ -39,7 +40,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (4); bumped on any change to the structs below. */
+/* ABI version (5); bumped on any change to the structs below. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -91,6 +92,8 @@ typedef struct ldx_conv3d_args {
   void* y; int64_t y_pitch;          /* fp16 NDHWC output */
   void* workspace;                   /* optional device scratch for split-K partial sums */
   size_t workspace_bytes;
+  int32_t dtype;                     /* LDX_DTYPE_F16 (0) or LDX_DTYPE_BF16: the type of x0, x1,
+                                        weight, shift, residual and y (bias and affine stay fp32) */
 } ldx_conv3d_args;
 
 /* Bytes of workspace with which ldx_conv3d splits the reduction over channel chunks
@@ -121,8 +124,9 @@ int ldx_conv3d_stats(const ldx_conv3d_args* args, float* moments, void* stream);
 int ldx_dense_ln(const ldx_conv3d_args* args, const float* gamma, const float* beta, float eps,
                  void* stream);
 
-/* Pack a Torch-layout fp16 weight (O, C, K, K, K) (K = 3 or 1; a dense (O, C)
- * weight is K = 1) into the kernel's fragment-major layout of
+/* Pack a Torch-layout fp16 or bf16 weight (O, C, K, K, K) (K = 3 or 1; a dense (O, C)
+ * weight is K = 1; a pure rearrangement of 16-bit values, the same for both types) into
+ * the kernel's fragment-major layout of
  * ldx_packed_weight_elems(O, C, K, 0) halves: with NOB = 4*ceil(O/128), NKC =
  * 4*ceil(C/64), tap = kd*9 + kh*3 + kw, fragment ((ob*K^3 + tap)*NKC + kc) holds 512
  * halves, lane l's eight at offset l*8 being W[ob*32 + l%32, kc*16 + 8*(l/32) + e,
@@ -133,12 +137,13 @@ size_t ldx_packed_weight_elems(int32_t out_c, int32_t in_c, int32_t ksize, int32
 int ldx_pack_weight(const void* weight, int32_t out_c, int32_t in_c, int32_t ksize,
                     void* packed, void* stream);
 
-/* Fold a Torch-layout fp16 (O, C, 3, 3, 3) weight into the 8 parity 2x2x2 filters
- * of a nearest-2x-upsampled conv (pack_upsample_weight, _nax_conv.py:367-405):
- * merged taps summed in fp32 in the reference's order and rounded to fp16 once,
+/* Fold a Torch-layout (O, C, 3, 3, 3) weight of type dtype (LDX_DTYPE_F16 or
+ * LDX_DTYPE_BF16) into the 8 parity 2x2x2 filters of a nearest-2x-upsampled conv
+ * (pack_upsample_weight, _nax_conv.py:367-405): merged taps summed in fp32 in the
+ * reference's order and rounded to dtype once,
  * stored fragment-major as above with parity = pd*4+ph*2+pw leading and tap =
  * td*4+th*2+tw: fragment (((parity*NOB + ob)*8 + tap)*NKC + kc). */
-int ldx_pack_upsample_weight(const void* weight, int32_t out_c, int32_t in_c,
+int ldx_pack_upsample_weight(const void* weight, int32_t out_c, int32_t in_c, int32_t dtype,
                              void* packed, void* stream);
 
 /* ------------------------------------------------------------- group norm -------
@@ -212,6 +217,7 @@ typedef struct ldx_attention_args {
   float scale;
   const float* mask; int64_t mask_stride[4];
   void* workspace; size_t workspace_bytes;   /* unused; may be NULL / 0 */
+  int32_t dtype;                        /* LDX_DTYPE_F16 (0) or LDX_DTYPE_BF16: q, k, v and o */
 } ldx_attention_args;
 
 size_t ldx_attention_workspace_bytes(const ldx_attention_args* args);

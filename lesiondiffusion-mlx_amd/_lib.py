@@ -48,6 +48,7 @@ class ConvArgs(ctypes.Structure):
         ("output_scale", c_f32), ("act", c_i32),
         ("y", c_vp), ("y_pitch", c_i64),
         ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
+        ("dtype", c_i32),
     ]
 
 
@@ -64,6 +65,7 @@ class AttnArgs(ctypes.Structure):
         ("scale", c_f32),
         ("mask", c_vp), ("mask_stride", c_i64 * 4),
         ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
+        ("dtype", c_i32),
     ]
 
 
@@ -78,7 +80,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_dense_ln": (c_i32, [ctypes.POINTER(ConvArgs), c_vp, c_vp, c_f32, c_vp]),
     "ldx_packed_weight_elems": (ctypes.c_size_t, [c_i32, c_i32, c_i32, c_i32]),
     "ldx_pack_weight": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
-    "ldx_pack_upsample_weight": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
+    "ldx_pack_upsample_weight": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
     "ldx_group_norm_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i64, c_i32, c_i32]),
     "ldx_group_norm_affine_noalloc": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
                                               c_vp, c_vp, c_f32, c_vp, c_vp]),
@@ -101,7 +103,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_vq_nearest4": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 def _load() -> ctypes.CDLL:

@@ -29,28 +29,27 @@
 // (:105-113); plus the additive mask of mx.fast.scaled_dot_product_attention
 // (mlx_model.py:843-847, 860-862).
 
-#include "common.h"
+#include "elem.h"
 
 #include <cstdlib>
 #include <type_traits>
 
 namespace ldx {
+namespace LDX_ELEM_NS {
 
 struct AttnParams {
   int B, H, L, LK;
-  const f16* q; int64_t qs0, qs1, qs2;
-  const f16* k; int64_t ks0, ks1, ks2;
-  const f16* v; int64_t vs0, vs1, vs2;
-  f16* o; int64_t os0, os1, os2;
+  const E* q; int64_t qs0, qs1, qs2;
+  const E* k; int64_t ks0, ks1, ks2;
+  const E* v; int64_t vs0, vs1, vs2;
+  E* o; int64_t os0, os1, os2;
   float c;  // scale * log2(e)
   const float* mask; int64_t ms0, ms1, ms2, ms3;
 };
 
-__device__ __forceinline__ f32x16 mfma32x(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma32x(E8 a, E8 b, f32x16 c) {
+  return mfma_e(a, b, c);
 }
-
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 
 
@@ -90,7 +89,7 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // Pointer into this workgroup's LDS as the address-space-3 pointer that the transposing
 // read takes.
-__device__ __forceinline__ lds_s16x4* lds_v4(const f16* p) {
+__device__ __forceinline__ lds_s16x4* lds_v4(const E* p) {
   return (lds_s16x4*)((__attribute__((address_space(3))) char*)(p));
 }
 
@@ -132,7 +131,7 @@ void attention_kernel(AttnParams p) {
   constexpr int LDS_H = NTILE * TILE > MERGE * 2 ? NTILE * TILE : MERGE * 2;
   // (+64 halves: for D = 16 the transposing V reads of the unused O^T rows 16..31 run
   // up to 8 halves past the last tile.)
-  __shared__ __attribute__((aligned(16))) f16 smem[LDS_H + 64];
+  __shared__ __attribute__((aligned(16))) E smem[LDS_H + 64];
 
   // The wave index is uniform; readfirstlane lets the compiler keep block indices,
   // tile bases and loop conditions in scalar registers.
@@ -150,21 +149,21 @@ void attention_kernel(AttnParams p) {
   const int nqb = (p.L + QPW - 1) / QPW;
   const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
   const int q0 = SPLIT == 1 ? qblk * 128 + wave * 32 : qblk * 32;
-  f16* Ks = smem + (SPLIT == 1 ? 0 : wave) * TILE;  // SPLIT > 1: this wave's tile
+  E* Ks = smem + (SPLIT == 1 ? 0 : wave) * TILE;  // SPLIT > 1: this wave's tile
   const int ltid = SPLIT == 1 ? threadIdx.x : lane;
 
-  const f16* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
-  const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
-  const f16* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+  const E* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
+  const E* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
+  const E* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
 
   // Q^T fragments: lane holds query q0 + col, dims 16*dk + 8*hf .. +7.
   const int qi = min(q0 + col, p.L - 1);
-  f16x8 qf[DK];
+  E8 qf[DK];
 #pragma unroll
   for (int dk = 0; dk < DK; dk++) {
     const int d = dk * 16 + 8 * hf;
-    f16x8 v = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (d < D) v = *reinterpret_cast<const f16x8*>(qb + (int64_t)qi * p.qs1 + d);
+    E8 v = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (d < D) v = *reinterpret_cast<const E8*>(qb + (int64_t)qi * p.qs1 + d);
     qf[dk] = v;
   }
   const float* mrow = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi * p.ms2 : nullptr;
@@ -201,7 +200,7 @@ void attention_kernel(AttnParams p) {
   // where the register budget must allow four waves per SIMD): the next tile loads
   // while the current one is multiplied.
   constexpr int PF = (SPLIT == 8 || D >= 128) ? 1 : 2;
-  f16x8 kst[PF][KPT], vst[PF][KPT];
+  E8 kst[PF][KPT], vst[PF][KPT];
   // Tile loads through buffer resources whose extent ends at the last valid key:
   // addresses need no per-lane arithmetic and rows past the key length read as zero.
   // (V^T reads past a row's padded end wrap into the next row: finite values whose
@@ -213,21 +212,21 @@ void attention_kernel(AttnParams p) {
     const auto vr = make_rsrc(vb_ + (int64_t)kbase * p.vs1, (unsigned)(((rows - 1) * p.vs1 + D) * 2));
 #pragma unroll
     for (int i = 0; i < KPT; i++)
-      if (KALL || ltid + i * TPT < KCH) kst[S][i] = buffer_load16(kr, koff0, i * kstep);
+      if (KALL || ltid + i * TPT < KCH) kst[S][i] = buffer_load16<E8>(kr, koff0, i * kstep);
 #pragma unroll
     for (int i = 0; i < KPT; i++)
-      if (KALL || ltid + i * TPT < KCH) vst[S][i] = buffer_load16(vr, voff0, i * vstep);
+      if (KALL || ltid + i * TPT < KCH) vst[S][i] = buffer_load16<E8>(vr, voff0, i * vstep);
   };
-  auto store_tile = [&](auto set_c, f16* kd) {
+  auto store_tile = [&](auto set_c, E* kd) {
     constexpr int S = decltype(set_c)::value;
-    f16* vd = kd + KB * KP;
+    E* vd = kd + KB * KP;
 #pragma unroll
     for (int i = 0; i < KPT; i++)
       if (KALL || ltid + i * TPT < KCH)
-        *reinterpret_cast<f16x8*>(kd + kst0 + key_row((i * KST) & 31) * KP) = kst[S][i];
+        *reinterpret_cast<E8*>(kd + kst0 + key_row((i * KST) & 31) * KP) = kst[S][i];
 #pragma unroll
     for (int i = 0; i < KPT; i++)
-      if (KALL || ltid + i * TPT < KCH) *reinterpret_cast<f16x8*>(vd + vst0 + ((i * KST) & 31) * KP) = vst[S][i];
+      if (KALL || ltid + i * TPT < KCH) *reinterpret_cast<E8*>(vd + vst0 + ((i * KST) & 31) * KP) = vst[S][i];
   };
 
   const int nblk = (p.LK + KB - 1) / KB;
@@ -242,7 +241,7 @@ void attention_kernel(AttnParams p) {
     if (nit > 1) load_tile(S1(), blk_of(1) * KB);
   }
   if constexpr (SPLIT == 1) __syncthreads();
-  const f16x2 ones = {(f16)1, (f16)1};
+  const E2 ones = {(E)1, (E)1};
 
   // One key block: block it is in LDS, block it + 1 in register set NEXT (stored after
   // the multiply), block it + 2 is loaded into the other set.
@@ -255,8 +254,8 @@ void attention_kernel(AttnParams p) {
     } else {
       if (it + 1 < nit) load_tile(NXC(), blk_of(it + 1) * KB);
     }
-    const f16* Kc = tile_k(it);
-    const f16* Vc = Kc + KB * KP;
+    const E* Kc = tile_k(it);
+    const E* Vc = Kc + KB * KP;
 
     // S^T = K Q^T: rows = keys (permuted by key_row), columns = queries.
     f32x16 s;
@@ -265,8 +264,8 @@ void attention_kernel(AttnParams p) {
 #pragma unroll
     for (int dk = 0; dk < DK; dk++) {
       const int d = dk * 16 + 8 * hf;
-      f16x8 kf = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (d < D) kf = *reinterpret_cast<const f16x8*>(Kc + col * KP + d);
+      E8 kf = {0, 0, 0, 0, 0, 0, 0, 0};
+      if (d < D) kf = *reinterpret_cast<const E8*>(Kc + col * KP + d);
       s = mfma32x(kf, qf[dk], s);
     }
     // Lane holds keys kbase + 16*(e/8) + 8*hf + e%8 of query q0 + col. Exponents are
@@ -302,14 +301,14 @@ void attention_kernel(AttnParams p) {
     }
     const float alpha = __builtin_amdgcn_exp2f(m - base);
     m = mn;
-    f16x8 pf[2];
+    E8 pf[2];
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
-      const f16x2 pr = {(f16)__builtin_amdgcn_exp2f(s[e]), (f16)__builtin_amdgcn_exp2f(s[e + 1])};
+      const E2 pr = {(E)__builtin_amdgcn_exp2f(s[e]), (E)__builtin_amdgcn_exp2f(s[e + 1])};
       pf[e >> 3][e & 7] = pr[0];
       pf[e >> 3][(e & 7) + 1] = pr[1];
-      sum = __builtin_amdgcn_fdot2(pr, ones, sum, false);
+      sum = dot2_e(pr, ones, sum);
     }
     l = l * alpha + sum;
     // Rescale only when some query's running max moved (wave-uniform test).
@@ -323,10 +322,10 @@ void attention_kernel(AttnParams p) {
     for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
       for (int db = 0; db < DB; db++) {
-        const f16* va = Vc + vtr0 + ks * 16 * KP + db * 32;
+        const E* va = Vc + vtr0 + ks * 16 * KP + db * 32;
         const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(va));
         const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(va + 4 * KP));
-        const f16x8 vf = __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+        const E8 vf = __builtin_bit_cast(E8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
         o[db] = mfma32x(vf, pf[ks], o[db]);
       }
     }
@@ -351,22 +350,22 @@ void attention_kernel(AttnParams p) {
   }
   l = halves_sum(l);
 
-  f16* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
+  E* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
   const int qo = q0 + col;
   if constexpr (SPLIT == 1) {
     if (qo < p.L) {
       const float inv = l > 0.f ? 1.0f / l : 0.f;
-      f16* orow = ob + (int64_t)qo * p.os1;
+      E* orow = ob + (int64_t)qo * p.os1;
 #pragma unroll
       for (int db = 0; db < DB; db++)
 #pragma unroll
         for (int j = 0; j < 4; j++) {
           const int d = db * 32 + j * 8 + 4 * hf;
           if (d < D) {
-            f16x4 out;
+            E4 out;
 #pragma unroll
-            for (int r = 0; r < 4; r++) out[r] = (f16)(o[db][j * 4 + r] * inv);
-            *reinterpret_cast<f16x4*>(orow + d) = out;
+            for (int r = 0; r < 4; r++) out[r] = (E)(o[db][j * 4 + r] * inv);
+            *reinterpret_cast<E4*>(orow + d) = out;
           }
         }
     }
@@ -397,15 +396,15 @@ void attention_kernel(AttnParams p) {
       const float inv = den > 0.f ? 1.0f / den : 0.f;
       const int qg = q0 + qq;
       if (qg < p.L) {
-        f16x4 out;
+        E4 out;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           float acc = 0.f;
 #pragma unroll
           for (int w = 0; w < SPLIT; w++) acc += f[w] * mo[(w * D + d4 + r) * 32 + qq];
-          out[r] = (f16)(acc * inv);
+          out[r] = (E)(acc * inv);
         }
-        *reinterpret_cast<f16x4*>(ob + (int64_t)qg * p.os1 + d4) = out;
+        *reinterpret_cast<E4*>(ob + (int64_t)qg * p.os1 + d4) = out;
       }
     }
   }
@@ -442,7 +441,7 @@ void attention_pipe_kernel(AttnParams p) {
   constexpr int NH = HT * 2 / 1024;           // 1 KB DMA instructions per K or V tile
   constexpr int RPD = 1024 / (D * 2);
   static_assert(D == 32 || D == 64, "DMA tiles for head widths 32 and 64");
-  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  extern __shared__ __attribute__((aligned(16))) E smem[];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hf = lane >> 5, col = lane & 31;
@@ -454,13 +453,13 @@ void attention_pipe_kernel(AttnParams p) {
   const int nqb = (p.L + 32 * QB - 1) / (32 * QB);
   const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
   const int q0 = qblk * 32 * QB;
-  f16* kbuf = smem + wave * 5 * HT;           // three K tiles, then two V tiles
-  f16* vbuf = kbuf + 3 * HT;
+  E* kbuf = smem + wave * 5 * HT;           // three K tiles, then two V tiles
+  E* vbuf = kbuf + 3 * HT;
   const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
 
-  const f16* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
-  const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
-  const f16* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+  const E* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
+  const E* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
+  const E* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
 
   int qi[QB];
   const float* mrow[QB];
@@ -509,24 +508,24 @@ void attention_pipe_kernel(AttnParams p) {
   const int vd0 = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   auto vaddr = [&](int r, int d) { return r * D + (((d >> 3) ^ (r % KG)) << 3) + (d & 7); };
 
-  f16x8 qf[QB][DK];
+  E8 qf[QB][DK];
   float m[QB];   // exponent base of each query (log2 units), -inf before its first key
 #pragma unroll
   for (int j = 0; j < QB; j++) m[j] = -INFINITY;
   // S^T = K Q^T of block it (rows = keys permuted by key_row, columns = queries).
   auto compute_s = [&](int it, f32x16 (&s)[QB]) {
-    const f16* Kc = kbuf + (it % 3) * HT;
+    const E* Kc = kbuf + (it % 3) * HT;
 #pragma unroll
     for (int j = 0; j < QB; j++) s[j] = (f32x16){};
 #pragma unroll
     for (int dk = 0; dk < DK; dk++) {
       const int c = 2 * dk + hf;
-      const f16x8 kf = *reinterpret_cast<const f16x8*>(Kc + col * D + ((c ^ (col % KG)) << 3));
+      const E8 kf = *reinterpret_cast<const E8*>(Kc + col * D + ((c ^ (col % KG)) << 3));
 #pragma unroll
       for (int j = 0; j < QB; j++) s[j] = mfma32x(kf, qf[j][dk], s[j]);
     }
   };
-  const f16x2 ones = {(f16)1, (f16)1};
+  const E2 ones = {(E)1, (E)1};
   // V^T read addresses (halves, in the first V buffer; the second is HT further).
   int va[2][DB][2];
 #pragma unroll
@@ -542,22 +541,22 @@ void attention_pipe_kernel(AttnParams p) {
   auto softmax_pv = [&](int it, auto vpar_c, auto full_c, f32x16 (&s)[QB]) {
     constexpr int VP = decltype(vpar_c)::value;
     constexpr bool FULL = decltype(full_c)::value;
-    const f16* Vc = vbuf + VP * HT;
+    const E* Vc = vbuf + VP * HT;
     auto read_v = [&](int ks, int db) {
       const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][0]));
       const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][1]));
-      return __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+      return __builtin_bit_cast(E8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
     };
     // One query block: the V^T operands first, so their LDS latency runs under the softmax
     // (two query blocks have no registers to spare for that).
-    f16x8 vf[2][DB];
+    E8 vf[2][DB];
     if constexpr (QB == 1) {
 #pragma unroll
       for (int ks = 0; ks < 2; ks++)
 #pragma unroll
         for (int db = 0; db < DB; db++) vf[ks][db] = read_v(ks, db);
     }
-    f16x8 pf[QB][2];
+    E8 pf[QB][2];
     float alpha[QB];
 #pragma unroll
     for (int j = 0; j < QB; j++) {
@@ -600,10 +599,10 @@ void attention_pipe_kernel(AttnParams p) {
       float sum = 0.f;
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const f16x2 pr = {(f16)__builtin_amdgcn_exp2f(s[j][e]), (f16)__builtin_amdgcn_exp2f(s[j][e + 1])};
+        const E2 pr = {(E)__builtin_amdgcn_exp2f(s[j][e]), (E)__builtin_amdgcn_exp2f(s[j][e + 1])};
         pf[j][e >> 3][e & 7] = pr[0];
         pf[j][e >> 3][(e & 7) + 1] = pr[1];
-        sum = __builtin_amdgcn_fdot2(pr, ones, sum, false);
+        sum = dot2_e(pr, ones, sum);
       }
       l[j] = l[j] * alpha[j] + sum;
     }
@@ -677,7 +676,7 @@ void attention_pipe_kernel(AttnParams p) {
   // exp2(m_w - M) / den (M and den over the waves) and stores it as [wave][query][d] fp32
   // rows padded to D + 4 (16-byte writes free of bank conflicts); each thread then sums
   // the SPLIT partials of 8 consecutive d of one query into one 16-byte store.
-  f16* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
+  E* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
   constexpr int RP = D + 4;
   float* mo = reinterpret_cast<float*>(smem);            // [QB][SPLIT][32][RP] scaled partial O
   float* ml = mo + QB * SPLIT * 32 * RP;                  // [QB][32][SPLIT] m, then the same for l
@@ -724,8 +723,8 @@ void attention_pipe_kernel(AttnParams p) {
       a0 += *reinterpret_cast<const f32x4*>(r);
       a1 += *reinterpret_cast<const f32x4*>(r + 4);
     }
-    const f16x8 out = {(f16)a0[0], (f16)a0[1], (f16)a0[2], (f16)a0[3], (f16)a1[0], (f16)a1[1], (f16)a1[2], (f16)a1[3]};
-    *reinterpret_cast<f16x8*>(ob + (int64_t)qg * p.os1 + d8) = out;
+    const E8 out = {(E)a0[0], (E)a0[1], (E)a0[2], (E)a0[3], (E)a1[0], (E)a1[1], (E)a1[2], (E)a1[3]};
+    *reinterpret_cast<E8*>(ob + (int64_t)qg * p.os1 + d8) = out;
   }
 }
 
@@ -782,7 +781,7 @@ void attention_wide_kernel(AttnParams p) {
   constexpr int RPD = 1024 / (D * 2);         // tile rows per DMA instruction
   constexpr bool QL = AttnWideLds<D>::QL;
   static_assert(D == 128 || D == 256, "wide heads");
-  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  extern __shared__ __attribute__((aligned(16))) E smem[];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hf = lane >> 5, col = lane & 31;
@@ -794,25 +793,25 @@ void attention_wide_kernel(AttnParams p) {
   const int nqb = (p.L + 127) / 128;
   const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
   const int q0 = qblk * 128 + wave * 32;
-  f16* kbuf = smem;                 // K tiles 0..2, then V tiles 0..2
-  f16* vbuf = smem + 3 * (TB / 2);
+  E* kbuf = smem;                 // K tiles 0..2, then V tiles 0..2
+  E* vbuf = smem + 3 * (TB / 2);
   const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
 
-  const f16* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
-  const f16* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
-  const f16* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+  const E* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
+  const E* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
+  const E* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
   const int qi = min(q0 + col, p.L - 1);
   const float* mrow = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi * p.ms2 : nullptr;
 
   // Q^T fragments: in registers (D = 128), or (D = 256, where O^T alone takes 128
   // registers) in this wave's LDS block, laid out like a K tile without the row
   // permutation and read with the K fragments.
-  f16x8 qf[QL ? 1 : DK];
+  E8 qf[QL ? 1 : DK];
   if constexpr (!QL) {
 #pragma unroll
-    for (int dk = 0; dk < DK; dk++) qf[dk] = *reinterpret_cast<const f16x8*>(qb_ + (int64_t)qi * p.qs1 + dk * 16 + 8 * hf);
+    for (int dk = 0; dk < DK; dk++) qf[dk] = *reinterpret_cast<const E8*>(qb_ + (int64_t)qi * p.qs1 + dk * 16 + 8 * hf);
   }
-  f16* qbuf = smem + 6 * (TB / 2) + wave * (TB / 2);
+  E* qbuf = smem + 6 * (TB / 2) + wave * (TB / 2);
   f32x16 o[DB];
 #pragma unroll
   for (int i = 0; i < DB; i++)
@@ -832,7 +831,7 @@ void attention_wide_kernel(AttnParams p) {
   const int nblk = (p.LK + KB - 1) / KB;
   // Block it's tile through a buffer resource that ends at the sequence's last key (none
   // past it: a block beyond the last reads zeros).
-  auto issue = [&](const f16* base, int64_t rs1, const unsigned (&off)[NHW], unsigned dst_base, int it) {
+  auto issue = [&](const E* base, int64_t rs1, const unsigned (&off)[NHW], unsigned dst_base, int it) {
     const int kbase = it * KB;
     const int rows = min(KB, p.LK - kbase);
     const i32x4 rs = dma_rsrc(rows > 0 ? base + (int64_t)kbase * rs1 : base,
@@ -873,13 +872,13 @@ void attention_wide_kernel(AttnParams p) {
     s = (f32x16){};
 #pragma unroll
     for (int g = 0; g < DK; g += 4) {
-      f16x8 kf[4];
+      E8 kf[4];
 #pragma unroll
-      for (int u = 0; u < 4; u++) kf[u] = *reinterpret_cast<const f16x8*>(kbase_p + (ka ^ kconst(g + u)));
+      for (int u = 0; u < 4; u++) kf[u] = *reinterpret_cast<const E8*>(kbase_p + (ka ^ kconst(g + u)));
       if constexpr (QL) {
-        f16x8 qg[4];
+        E8 qg[4];
 #pragma unroll
-        for (int u = 0; u < 4; u++) qg[u] = *reinterpret_cast<const f16x8*>(qbase_p + (ka_lane ^ kconst(g + u)));
+        for (int u = 0; u < 4; u++) qg[u] = *reinterpret_cast<const E8*>(qbase_p + (ka_lane ^ kconst(g + u)));
 #pragma unroll
         for (int u = 0; u < 4; u++) s = mfma32x(kf[u], qg[u], s);
       } else {
@@ -889,7 +888,7 @@ void attention_wide_kernel(AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  const f16x2 ones = {(f16)1, (f16)1};
+  const E2 ones = {(E)1, (E)1};
   constexpr float RB = 8.f;
   auto softmax_pv = [&](int it, auto full_c, f32x16& s) {
     constexpr bool FULL = decltype(full_c)::value;
@@ -927,14 +926,14 @@ void attention_wide_kernel(AttnParams p) {
 #pragma unroll
       for (int e = 0; e < 16; e++) s[e] -= base;
     }
-    f16x8 pf[2];
+    E8 pf[2];
     float sum = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
-      const f16x2 pr = {(f16)__builtin_amdgcn_exp2f(s[e]), (f16)__builtin_amdgcn_exp2f(s[e + 1])};
+      const E2 pr = {(E)__builtin_amdgcn_exp2f(s[e]), (E)__builtin_amdgcn_exp2f(s[e + 1])};
       pf[e >> 3][e & 7] = pr[0];
       pf[e >> 3][(e & 7) + 1] = pr[1];
-      sum = __builtin_amdgcn_fdot2(pr, ones, sum, false);
+      sum = dot2_e(pr, ones, sum);
     }
     l = l * alpha + sum;
     // (Plain multiplies: the accumulators may live in AGPRs, which the rescale reaches
@@ -950,14 +949,14 @@ void attention_wide_kernel(AttnParams p) {
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
       for (int g = 0; g < DB; g += 4) {
-        f16x8 vf[4];
+        E8 vf[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-          const f16* a0 = reinterpret_cast<const f16*>(vbase_p + (va ^ vconst(ks, 0, g + u)));
-          const f16* a1 = reinterpret_cast<const f16*>(vbase_p + (va ^ vconst(ks, 1, g + u)));
+          const E* a0 = reinterpret_cast<const E*>(vbase_p + (va ^ vconst(ks, 0, g + u)));
+          const E* a1 = reinterpret_cast<const E*>(vbase_p + (va ^ vconst(ks, 1, g + u)));
           const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(a0));
           const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(a1));
-          vf[u] = __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+          vf[u] = __builtin_bit_cast(E8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) o[g + u] = mfma32x(vf[u], pf[ks], o[g + u]);
@@ -1013,16 +1012,16 @@ void attention_wide_kernel(AttnParams p) {
   l = halves_sum(l);
   const int qo = q0 + col;
   if (qo < p.L) {
-    f16* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
+    E* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
     const float inv = l > 0.f ? 1.0f / l : 0.f;
 #pragma unroll
     for (int db = 0; db < DB; db++)
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        f16x4 out;
+        E4 out;
 #pragma unroll
-        for (int r = 0; r < 4; r++) out[r] = (f16)(o[db][j * 4 + r] * inv);
-        *reinterpret_cast<f16x4*>(orow + db * 32 + j * 8 + 4 * hf) = out;
+        for (int r = 0; r < 4; r++) out[r] = (E)(o[db][j * 4 + r] * inv);
+        *reinterpret_cast<E4*>(orow + db * 32 + j * 8 + 4 * hf) = out;
       }
   }
 }
@@ -1072,9 +1071,6 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
   return launch_attn<D, 1>(p, st);
 }
 
-}  // namespace ldx
-
-using namespace ldx;
 
 static int check_attention_args(const ldx_attention_args* a) {
   if (!a) return fail("attention: null args");
@@ -1102,21 +1098,21 @@ static int check_attention_args(const ldx_attention_args* a) {
 
 // No scratch memory is needed (V is transposed by the LDS reads); the workspace fields
 // of the argument struct are accepted and ignored.
-extern "C" size_t ldx_attention_workspace_bytes(const ldx_attention_args* a) {
+size_t attention_workspace_bytes(const ldx_attention_args* a) {
   (void)a;
   return 0;
 }
 
-extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
+int attention_entry(const ldx_attention_args* a, void* stream) {
   int rc = check_attention_args(a);
   if (rc != LDX_OK) return rc;
   const int D = a->head_dim;
   AttnParams p{};
   p.B = a->batch; p.H = a->heads; p.L = a->q_len; p.LK = a->kv_len;
-  p.q = (const f16*)a->q; p.qs0 = a->q_stride[0]; p.qs1 = a->q_stride[1]; p.qs2 = a->q_stride[2];
-  p.k = (const f16*)a->k; p.ks0 = a->k_stride[0]; p.ks1 = a->k_stride[1]; p.ks2 = a->k_stride[2];
-  p.v = (const f16*)a->v; p.vs0 = a->v_stride[0]; p.vs1 = a->v_stride[1]; p.vs2 = a->v_stride[2];
-  p.o = (f16*)a->o; p.os0 = a->o_stride[0]; p.os1 = a->o_stride[1]; p.os2 = a->o_stride[2];
+  p.q = (const E*)a->q; p.qs0 = a->q_stride[0]; p.qs1 = a->q_stride[1]; p.qs2 = a->q_stride[2];
+  p.k = (const E*)a->k; p.ks0 = a->k_stride[0]; p.ks1 = a->k_stride[1]; p.ks2 = a->k_stride[2];
+  p.v = (const E*)a->v; p.vs0 = a->v_stride[0]; p.vs1 = a->v_stride[1]; p.vs2 = a->v_stride[2];
+  p.o = (E*)a->o; p.os0 = a->o_stride[0]; p.os1 = a->o_stride[1]; p.os2 = a->o_stride[2];
   p.c = a->scale * 1.44269504088896341f;
   p.mask = a->mask;
   p.ms0 = a->mask_stride[0]; p.ms1 = a->mask_stride[1]; p.ms2 = a->mask_stride[2]; p.ms3 = a->mask_stride[3];
@@ -1129,3 +1125,28 @@ extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
     default: return launch_d<256>(p, st);
   }
 }
+
+}  // namespace LDX_ELEM_NS
+}  // namespace ldx
+
+#if !defined(LDX_ELEM_BF16)
+namespace ldx {
+namespace bf16_path {
+size_t attention_workspace_bytes(const ldx_attention_args* a);
+int attention_entry(const ldx_attention_args* a, void* stream);
+}  // namespace bf16_path
+}  // namespace ldx
+
+// The C entry points (in the fp16 unit only): the kernels of the args' dtype.
+extern "C" size_t ldx_attention_workspace_bytes(const ldx_attention_args* a) {
+  (void)a;
+  return 0;
+}
+
+extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
+  if (a && a->dtype == LDX_DTYPE_BF16) return ldx::bf16_path::attention_entry(a, stream);
+  if (a && a->dtype != LDX_DTYPE_F16)
+    return ldx::fail("attention: dtype %d is not LDX_DTYPE_F16 or LDX_DTYPE_BF16", a->dtype);
+  return ldx::f16_path::attention_entry(a, stream);
+}
+#endif

@@ -11,8 +11,13 @@
 #include "ldx.h"
 
 typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16;
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -65,8 +70,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, un
 }
 
 // 16 bytes at byte offset off + soff (soff wave-uniform) of a buffer resource.
-__device__ __forceinline__ f16x8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned soff = 0) {
-  return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
+template <typename V8 = f16x8>
+__device__ __forceinline__ V8 buffer_load16(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned soff = 0) {
+  return __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
 }
 
 // ---------------------------------------------------------------- LDS DMA
@@ -117,8 +123,9 @@ __device__ __forceinline__ void dma_buffer_b128(i32x4 rs, unsigned voff, unsigne
 // registers, by asm: the compiler's wait insertion does not see it (and so drains nothing
 // on its account). The caller awaits it with vmcnt_wait and then passes the value through
 // pin_value before its first use.
-__device__ __forceinline__ f16x8 buffer_load16_asm(i32x4 rs, unsigned voff, unsigned soff = 0) {
-  f16x8 v;
+template <typename V8 = f16x8>
+__device__ __forceinline__ V8 buffer_load16_asm(i32x4 rs, unsigned voff, unsigned soff = 0) {
+  V8 v;
   asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(rs), "s"(soff) : "memory");
   return v;
 }
@@ -162,8 +169,8 @@ __device__ __forceinline__ float lane_group_sum(float v) {
 // summed over those lanes (lane_group_sum: every lane ends with the same sums), so the
 // block's (count, mean, M2) carry no cancellation. With `store`, the lane writes its four
 // pairs' moments as 12 consecutive floats at dst (16-byte aligned).
-template <int NI, int L>
-__device__ __forceinline__ void pair_moments(const f16x8 (&v)[NI], const bool (&ok)[NI], float* dst,
+template <int NI, int L, typename V8>
+__device__ __forceinline__ void pair_moments(const V8 (&v)[NI], const bool (&ok)[NI], float* dst,
                                              bool store) {
   float cnt = 0.f, s[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll

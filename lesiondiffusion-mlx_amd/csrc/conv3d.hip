@@ -23,7 +23,7 @@
 // prologue _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421),
 // stride-2 / upsample window rule :185-189, 251-253.
 
-#include "common.h"
+#include "elem.h"
 #include "conv3d_stream.h"
 
 #include <algorithm>
@@ -31,6 +31,7 @@
 #include <type_traits>
 
 namespace ldx {
+namespace LDX_ELEM_NS {
 
 struct ConvParams {
   int B, D, H, W;          // input / source grid
@@ -49,15 +50,15 @@ struct ConvParams {
   int NOB;                 // 32-row output blocks of the packed weight
   int split, cps;          // split-K: channel-chunk ranges of cps chunks each
   float* part;             // split > 1: fp32 partial sums [split][B * output voxels][O]
-  const f16* x0; int64_t x0p;
-  const f16* x1; int64_t x1p;
-  const f16* w;
+  const E* x0; int64_t x0p;
+  const E* x1; int64_t x1p;
+  const E* w;
   const float* bias; int bias_batched;
-  const f16* shift; int64_t shiftp;
+  const E* shift; int64_t shiftp;
   const float* affine; int silu;
-  const f16* res; int64_t resp;
+  const E* res; int64_t resp;
   float scale; int act;
-  f16* y; int64_t yp; int yvec;
+  E* y; int64_t yp; int yvec;
   int ep_vec;              // 16-byte epilogue accesses: y, residual, shift, bias, partials aligned
   int nh;                  // planned halo: register slots per thread (0: generic staging loop)
   int stg_off;             // > 0: LDS offset (floats) of the epilogue staging, past the halo
@@ -75,15 +76,15 @@ __device__ __forceinline__ float gelu_erf(float v) {
 }
 
 // Epilogue activation applied to the stored half value (a second rounding).
-__device__ __forceinline__ f16 post_act(f16 h, int act) {
-  if (act == LDX_ACT_GELU) return (f16)gelu_erf((float)h);
-  if (act == LDX_ACT_SILU) return (f16)silu_f((float)h);
+__device__ __forceinline__ E post_act(E h, int act) {
+  if (act == LDX_ACT_GELU) return (E)gelu_erf((float)h);
+  if (act == LDX_ACT_SILU) return (E)silu_f((float)h);
   return h;
 }
 template <int ACT>
-__device__ __forceinline__ f16 post_act_t(f16 h) {
-  if constexpr (ACT == LDX_ACT_GELU) return (f16)gelu_erf((float)h);
-  else if constexpr (ACT == LDX_ACT_SILU) return (f16)silu_f((float)h);
+__device__ __forceinline__ E post_act_t(E h) {
+  if constexpr (ACT == LDX_ACT_GELU) return (E)gelu_erf((float)h);
+  else if constexpr (ACT == LDX_ACT_SILU) return (E)silu_f((float)h);
   else return h;
 }
 
@@ -96,7 +97,7 @@ __device__ __forceinline__ int fdiv(int t, float rcp) { return (int)(((float)t +
 // affine + SiLU prologue and zero padding. Global loads are issued NB at a time before
 // any of them is consumed, so their latencies overlap.
 template <int CC, bool VEC, int NT>
-__device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b, int c0,
+__device__ __forceinline__ void load_halo(const ConvParams& p, E* halo, int b, int c0,
                                           int gd0, int gh0, int gw0) {
   constexpr int PITCH = CC + 8;
   const int hvox = p.HD * p.HH * p.HW;
@@ -126,12 +127,12 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
     // through a buffer resource over the batch item, so padding voxels and channels
     // past C read as zero without a branch.
     const bool in0 = c0 < p.C0;
-    const f16* base = in0 ? p.x0 + bvox * p.x0p : p.x1 + bvox * p.x1p;
+    const E* base = in0 ? p.x0 + bvox * p.x0p : p.x1 + bvox * p.x1p;
     const int64_t pitch = in0 ? p.x0p : p.x1p;
     const auto rs = make_rsrc(base, (unsigned)(vol * pitch * 2));
     const unsigned cofs = (unsigned)((in0 ? c : c - p.C0) * 2);
     for (int v0 = threadIdx.x / G; v0 < hvox; v0 += VPI * NB) {
-      f16x8 val[NB];
+      E8 val[NB];
       bool ok[NB];
 #pragma unroll
       for (int j = 0; j < NB; j++) {
@@ -144,23 +145,23 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
         ok[j] = vox < hvox && cval && id >= 0 && id < p.D && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W;
         const unsigned off = ok[j] ? (unsigned)(((id * p.H + ih) * p.W + iw) * (unsigned)pitch * 2u) + cofs
                                    : 0xfffffff0u;
-        val[j] = buffer_load16(rs, off);
+        val[j] = buffer_load16<E8>(rs, off);
       }
 #pragma unroll
       for (int j = 0; j < NB; j++) {
         const int vox = v0 + j * VPI;
         if (vox >= hvox) break;
-        f16x8 v = val[j];
+        E8 v = val[j];
         if (xf) {
 #pragma unroll
           for (int e = 0; e < 8; e++) {
             float yv = (float)v[e] * sc[e] + of[e];
             if (silu) yv = silu_f(yv);
-            v[e] = ok[j] ? (f16)yv : (f16)0;
+            v[e] = ok[j] ? (E)yv : (E)0;
           }
         }
         const int t2 = fdiv(vox, p.rHW);
-        *reinterpret_cast<f16x8*>(halo + t2 * p.RS + (vox - t2 * p.HW) * PITCH + cg * 8) = v;
+        *reinterpret_cast<E8*>(halo + t2 * p.RS + (vox - t2 * p.HW) * PITCH + cg * 8) = v;
       }
     }
   } else {
@@ -172,15 +173,15 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
       const int hh = t - hd * p.HH;
       const int id = gd0 + hd, ih = gh0 + hh, iw = gw0 + hw;
       const int c = c0 + cc;
-      f16 v = 0;
+      E v = 0;
       if (c < p.C && id >= 0 && id < p.D && ih >= 0 && ih < p.H && iw >= 0 && iw < p.W) {
         const int64_t vi = bvox + ((int64_t)id * p.H + ih) * p.W + iw;
-        const f16* src = c < p.C0 ? p.x0 + vi * p.x0p + c : p.x1 + vi * p.x1p + (c - p.C0);
+        const E* src = c < p.C0 ? p.x0 + vi * p.x0p + c : p.x1 + vi * p.x1p + (c - p.C0);
         if (p.affine || p.silu) {
           float yv = (float)*src;
           if (p.affine) yv = yv * p.affine[((int64_t)b * p.C + c) * 2] + p.affine[((int64_t)b * p.C + c) * 2 + 1];
           if (p.silu) yv = silu_f(yv);
-          v = (f16)yv;
+          v = (E)yv;
         } else {
           v = *src;
         }
@@ -190,11 +191,11 @@ __device__ __forceinline__ void load_halo(const ConvParams& p, f16* halo, int b,
   }
 }
 
-// One 32x32x16 f16 MFMA, D(32x32) += A(32x16) * B(16x32). Lane l: A row l%32 and
+// One 32x32x16 E MFMA, D(32x32) += A(32x16) * B(16x32). Lane l: A row l%32 and
 // B column l%32, k = 8*(l/32) + e; D column l%32, rows (e/4)*8 + 4*(l/32) + e%4.
 // On gfx950 this shape sustains twice the throughput of 16x16x32 in a dense loop.
-__device__ __forceinline__ f32x16 mfma32(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma32(E8 a, E8 b, f32x16 c) {
+  return mfma_e(a, b, c);
 }
 
 // Weight ring: WRING slots, loads issued WPF = WRING - 1 stages ahead.
@@ -222,7 +223,7 @@ __device__ __forceinline__ EpiConst epi_const(const ConvParams& p, int lane, int
 #pragma unroll
   for (int r = 0; r < 8; r++) e.add8[r] = 0.f;
   const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) : nullptr;
-  const f16* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
+  const E* shb = p.shift ? p.shift + (int64_t)b * p.shiftp : nullptr;
   if (e.nch > 0) {
     if (e.vec8) {
       if (bias) {
@@ -232,7 +233,7 @@ __device__ __forceinline__ EpiConst epi_const(const ConvParams& p, int lane, int
         for (int r = 0; r < 4; r++) { e.add8[r] = b0[r]; e.add8[r + 4] = b1[r]; }
       }
       if (shb) {
-        const f16x8 s8 = *reinterpret_cast<const f16x8*>(shb + e.o);
+        const E8 s8 = *reinterpret_cast<const E8*>(shb + e.o);
 #pragma unroll
         for (int r = 0; r < 8; r++) e.add8[r] += (float)s8[r];
       }
@@ -290,7 +291,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
     __builtin_amdgcn_wave_barrier();  // (LDS operations of a wave complete in order)
     int ov[NI];
     bool ok[NI];
-    f16x8 re8[NI];
+    E8 re8[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
       const int v = lane / G8 + i * (64 / G8);
@@ -308,17 +309,17 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
     if (pref_res) {
 #pragma unroll
       for (int i = 0; i < NI; i++)
-        re8[i] = ok[i] ? *reinterpret_cast<const f16x8*>(p.res + (int64_t)ov[i] * p.resp + o)
-                       : (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+        re8[i] = ok[i] ? *reinterpret_cast<const E8*>(p.res + (int64_t)ov[i] * p.resp + o)
+                       : (E8){0, 0, 0, 0, 0, 0, 0, 0};
     } else {
 #pragma unroll
-      for (int i = 0; i < NI; i++) re8[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < NI; i++) re8[i] = (E8){0, 0, 0, 0, 0, 0, 0, 0};
     }
     f32x4 lo[NI], hi[NI];
-    f16x8 outv[NI];
+    E8 outv[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) {
-      outv[i] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+      outv[i] = (E8){0, 0, 0, 0, 0, 0, 0, 0};
       const int v = lane / G8 + i * (64 / G8);
       lo[i] = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8);
       hi[i] = *reinterpret_cast<const f32x4*>(stg + v * EPW + g * 8 + 4);
@@ -340,20 +341,20 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
         }
         continue;
       }
-      f16* yrow = p.y + (int64_t)ov[i] * p.yp + o;
+      E* yrow = p.y + (int64_t)ov[i] * p.yp + o;
       if (vec8) {
-        f16x8& out = outv[i];
+        E8& out = outv[i];
 #pragma unroll
-        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((f16)((r8[r] + ec.add8[r]) * p.scale + (float)re8[i][r]));
-        *reinterpret_cast<f16x8*>(yrow) = out;
+        for (int r = 0; r < 8; r++) out[r] = post_act_t<ACT>((E)((r8[r] + ec.add8[r]) * p.scale + (float)re8[i][r]));
+        *reinterpret_cast<E8*>(yrow) = out;
       } else {
-        const f16* rrow = p.res ? p.res + (int64_t)ov[i] * p.resp + o : nullptr;
+        const E* rrow = p.res ? p.res + (int64_t)ov[i] * p.resp + o : nullptr;
 #pragma unroll
         for (int r = 0; r < 8; r++) {
           if (r >= nch) break;
           float t = (r8[r] + ec.add8[r]) * p.scale;
           if (rrow) t += (float)rrow[r];
-          yrow[r] = post_act_t<ACT>((f16)t);
+          yrow[r] = post_act_t<ACT>((E)t);
         }
       }
     }
@@ -419,14 +420,14 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   // Tap of each chunk after whose weight load the next chunk's halo is requested: the
   // loads then have the last WPF - 1 taps of the chunk to land.
   constexpr int TPF = TAPS - WPF;
-  extern __shared__ __attribute__((aligned(16))) f16 smem[];
-  f16* halo = smem + KSPL * WRING * WSTAGE;
+  extern __shared__ __attribute__((aligned(16))) E smem[];
+  E* halo = smem + KSPL * WRING * WSTAGE;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = wave >> 2, w4 = wave & 3;
   const int wo = w4 / WV, wv = w4 - wo * WV;
-  f16* wring = smem + kg * WRING * WSTAGE;    // this K-group's weight ring
+  E* wring = smem + kg * WRING * WSTAGE;    // this K-group's weight ring
   // Workgroup -> (output block, brick, z) with the output blocks of a brick adjacent and
   // the bricks each XCD receives (workgroups are dealt to the 8 XCDs round-robin)
   // contiguous, so neighbouring halos meet in the same L2.
@@ -479,7 +480,7 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   const int nst = (c_end - c_begin + CC - 1) / CC * TAPS;
   const unsigned ring_lds = lds_offset(wring);
   // This wave's fragment sources at (tap 0, chunk 0); a stage adds (tap * NKC + kc0) * 512.
-  const f16* wsrc[LW];
+  const E* wsrc[LW];
 #pragma unroll
   for (int i = 0; i < LW; i++) {
     const int f = (w4 + 4 * i) % NFRAG;
@@ -506,7 +507,7 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   const int cg = tid % G;
   unsigned hvi[NHMAX];
   int hlo[NHMAX];
-  f16x8 hval[NHMAX];
+  E8 hval[NHMAX];
   f32x4 haff[4];   // the chunk's (scale, offset) pairs of this thread's 8 channels
   if constexpr (PLAN) {
     const int hvox = p.HD * p.HH * p.HW;
@@ -531,7 +532,7 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
     if constexpr (PLAN) {
       const bool in0 = c0 < p.C0;
       const int64_t vol = (int64_t)p.D * p.H * p.W;
-      const f16* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
+      const E* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
       const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
       const auto rs = make_rsrc(base, (unsigned)(vol * pitch2));
       const int c = c0 + cg * 8;
@@ -540,13 +541,13 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
 #pragma unroll
       for (int j = 0; j < NHMAX; j++) {
         const unsigned off = (hvi[j] != ~0u && cval) ? hvi[j] * pitch2 + cofs : 0xfffffff0u;
-        hval[j] = buffer_load16(rs, off);
+        hval[j] = buffer_load16<E8>(rs, off);
       }
       const auto ra = make_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr,
                                 p.affine ? (unsigned)(p.C * 8) : 0u);
 #pragma unroll
       for (int q = 0; q < 4; q++)
-        haff[q] = __builtin_bit_cast(f32x4, buffer_load16(ra, (unsigned)(c * 8 + q * 16)));
+        haff[q] = __builtin_bit_cast(f32x4, buffer_load16<E8>(ra, (unsigned)(c * 8 + q * 16)));
     }
   };
   // Write hval to the halo, with the affine + SiLU prologue and one fp16 rounding;
@@ -566,17 +567,17 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
 #pragma unroll
       for (int j = 0; j < NHMAX; j++) {
         if (hlo[j] < 0) continue;
-        f16x8 v = hval[j];
+        E8 v = hval[j];
         if (xf) {
           const bool ok = cval && hvi[j] != ~0u;
 #pragma unroll
           for (int e = 0; e < 8; e++) {
             float yv = (float)v[e] * sc[e] + of[e];
             if (p.silu) yv = silu_f(yv);
-            v[e] = ok ? (f16)yv : (f16)0;
+            v[e] = ok ? (E)yv : (E)0;
           }
         }
-        *reinterpret_cast<f16x8*>(halo + hlo[j]) = v;
+        *reinterpret_cast<E8*>(halo + hlo[j]) = v;
       }
     }
   };
@@ -598,19 +599,19 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
 
   // Operand fragments double-buffered in registers: while the MFMAs of tap t run, the
   // A (weight ring) and B (halo) fragments of tap t + 1 are read from LDS.
-  f16x8 ra[2][FO][KSG], rb[2][FV][KSG];
+  E8 ra[2][FO][KSG], rb[2][FV][KSG];
   auto load_frags = [&](int set, int stage, int tap) {
     const int kd = tap / (KSZ * KSZ), kh = (tap / KSZ) % KSZ, kw = tap % KSZ;
     const int toff = kd * sd + kh * sh + kw * PITCH;
-    const f16* wst = wring + (stage % WRING) * WSTAGE + lane * 8;
+    const E* wst = wring + (stage % WRING) * WSTAGE + lane * 8;
 #pragma unroll
     for (int kk = 0; kk < KSG; kk++) {
 #pragma unroll
       for (int fo = 0; fo < FO; fo++)
-        ra[set][fo][kk] = *reinterpret_cast<const f16x8*>(wst + ((wo * FO + fo) * KSG + kk) * 512);
+        ra[set][fo][kk] = *reinterpret_cast<const E8*>(wst + ((wo * FO + fo) * KSG + kk) * 512);
 #pragma unroll
       for (int fv = 0; fv < FV; fv++)
-        rb[set][fv][kk] = *reinterpret_cast<const f16x8*>(halo + lbase[fv] + toff + kk * 16);
+        rb[set][fv][kk] = *reinterpret_cast<const E8*>(halo + lbase[fv] + toff + kk * 16);
     }
   };
   auto mfma_frags = [&](int set) {
@@ -731,7 +732,7 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
   constexpr int BO = WO * FO * 32, BV = WV * FV * 32;
   constexpr int PD = 4;                       // k-steps of operands in flight
   constexpr int EPW = FO * 32 + 4;
-  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  extern __shared__ __attribute__((aligned(16))) E smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wo = wave / WV, wv = wave - wo * WV;
@@ -765,16 +766,16 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
   const float* aff = p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr;
   const EpiConst ec = epi_const<FO>(p, lane, ob0, b);
 
-  f16x8 ra[PD][FO], rb[PD][FV];
+  E8 ra[PD][FO], rb[PD][FV];
   auto load = [&](int set, int kc) {
 #pragma unroll
     for (int fo = 0; fo < FO; fo++)
-      ra[set][fo] = buffer_load16(rw, aoff, (unsigned)((ob0 + fo) * p.NKC + kc) * 1024u);
+      ra[set][fo] = buffer_load16<E8>(rw, aoff, (unsigned)((ob0 + fo) * p.NKC + kc) * 1024u);
     const bool in0 = kc < nk0;
 #pragma unroll
     for (int fv = 0; fv < FV; fv++)
-      rb[set][fv] = in0 ? buffer_load16(r0, boff0[fv], (unsigned)kc * 32u)
-                        : buffer_load16(r1, boff1[fv], (unsigned)(kc - nk0) * 32u);
+      rb[set][fv] = in0 ? buffer_load16<E8>(r0, boff0[fv], (unsigned)kc * 32u)
+                        : buffer_load16<E8>(r1, boff1[fv], (unsigned)(kc - nk0) * 32u);
   };
   auto prep = [&](int set, int kc) {
     // Channels past C (C % 16 != 0) meet zero weights; zero them so stray values cannot
@@ -785,7 +786,7 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
       for (int fv = 0; fv < FV; fv++)
 #pragma unroll
         for (int e = 0; e < 8; e++)
-          if (c + e >= p.C) rb[set][fv][e] = (f16)0;
+          if (c + e >= p.C) rb[set][fv][e] = (E)0;
     }
     if (aff || p.silu) {
       float sc[8], of[8];
@@ -801,7 +802,7 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
         for (int e = 0; e < 8; e++) {
           float y = (float)rb[set][fv][e] * sc[e] + of[e];
           if (p.silu) y = silu_f(y);
-          rb[set][fv][e] = c + e < p.C ? (f16)y : (f16)0;
+          rb[set][fv][e] = c + e < p.C ? (E)y : (E)0;
         }
     }
   };
@@ -850,7 +851,7 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
   constexpr int PD = 8;                       // k-steps of operands in flight per wave
   constexpr int EPW = FO * 32 + 4;
   constexpr int PART = FO * FV * 1024;        // floats of one wave's partial block
-  extern __shared__ __attribute__((aligned(16))) f16 smem[];
+  extern __shared__ __attribute__((aligned(16))) E smem[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hf = lane >> 5;
@@ -882,16 +883,16 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
   const float* aff = p.affine ? p.affine + (int64_t)b * p.C * 2 : nullptr;
   const EpiConst ec = epi_const<FO>(p, lane, ob0, b);
 
-  f16x8 ra[PD][FO], rb[PD][FV];
+  E8 ra[PD][FO], rb[PD][FV];
   auto load = [&](int set, int kc) {
 #pragma unroll
     for (int fo = 0; fo < FO; fo++)
-      ra[set][fo] = buffer_load16(rw, aoff, (unsigned)((ob0 + fo) * p.NKC + kc) * 1024u);
+      ra[set][fo] = buffer_load16<E8>(rw, aoff, (unsigned)((ob0 + fo) * p.NKC + kc) * 1024u);
     const bool in0 = kc < nk0;
 #pragma unroll
     for (int fv = 0; fv < FV; fv++)
-      rb[set][fv] = in0 ? buffer_load16(r0, boff0[fv], (unsigned)kc * 32u)
-                        : buffer_load16(r1, boff1[fv], (unsigned)(kc - nk0) * 32u);
+      rb[set][fv] = in0 ? buffer_load16<E8>(r0, boff0[fv], (unsigned)kc * 32u)
+                        : buffer_load16<E8>(r1, boff1[fv], (unsigned)(kc - nk0) * 32u);
   };
   auto prep = [&](int set, int kc) {
     const int c = kc * 16 + hf * 8;
@@ -900,7 +901,7 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
       for (int fv = 0; fv < FV; fv++)
 #pragma unroll
         for (int e = 0; e < 8; e++)
-          if (c + e >= p.C) rb[set][fv][e] = (f16)0;
+          if (c + e >= p.C) rb[set][fv][e] = (E)0;
     }
     if (aff || p.silu) {
       float sc[8], of[8];
@@ -916,7 +917,7 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
         for (int e = 0; e < 8; e++) {
           float y = (float)rb[set][fv][e] * sc[e] + of[e];
           if (p.silu) y = silu_f(y);
-          rb[set][fv][e] = c + e < p.C ? (f16)y : (f16)0;
+          rb[set][fv][e] = c + e < p.C ? (E)y : (E)0;
         }
     }
   };
@@ -978,8 +979,8 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
         const f32x4 b1 = *reinterpret_cast<const f32x4*>(lng + 512 + c + 4);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          rb[j][0][e] = (f16)(((float)rb[j][0][e] - mean) * rstd * g0[e] + b0[e]);
-          rb[j][0][e + 4] = (f16)(((float)rb[j][0][e + 4] - mean) * rstd * g1[e] + b1[e]);
+          rb[j][0][e] = (E)(((float)rb[j][0][e] - mean) * rstd * g0[e] + b0[e]);
+          rb[j][0][e + 4] = (E)(((float)rb[j][0][e + 4] - mean) * rstd * g1[e] + b1[e]);
         }
         acc[0][0] = mfma32(ra[j][0], rb[j][0], acc[0][0]);
       }
@@ -1049,7 +1050,7 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
     if (p.shift) add += (float)p.shift[(int64_t)b * p.shiftp + o];
     v = (v + add) * p.scale;
     if (p.res) v += (float)p.res[ov * p.resp + o];
-    p.y[ov * p.yp + o] = post_act((f16)v, p.act);
+    p.y[ov * p.yp + o] = post_act((E)v, p.act);
   }
 }
 
@@ -1080,23 +1081,23 @@ __global__ __launch_bounds__(256) void conv_reduce8_kernel(ConvParams p, int nvo
       for (int r = 0; r < 4; r++) { add[r] = b0[r]; add[r + 4] = b1[r]; }
     }
     if (p.shift) {
-      const f16x8 sh = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o);
+      const E8 sh = *reinterpret_cast<const E8*>(p.shift + (int64_t)b * p.shiftp + o);
 #pragma unroll
       for (int r = 0; r < 8; r++) add[r] += (float)sh[r];
     }
-    f16x8 rs = {};
-    if (p.res) rs = *reinterpret_cast<const f16x8*>(p.res + (int64_t)ov * p.resp + o);
-    f16x8 out;
+    E8 rs = {};
+    if (p.res) rs = *reinterpret_cast<const E8*>(p.res + (int64_t)ov * p.resp + o);
+    E8 out;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       float v = (lo[r] + add[r]) * p.scale;
       if (p.res) v += (float)rs[r];
-      out[r] = post_act((f16)v, p.act);
+      out[r] = post_act((E)v, p.act);
       float w = (hi[r] + add[r + 4]) * p.scale;
       if (p.res) w += (float)rs[r + 4];
-      out[r + 4] = post_act((f16)w, p.act);
+      out[r + 4] = post_act((E)w, p.act);
     }
-    *reinterpret_cast<f16x8*>(p.y + (int64_t)ov * p.yp + o) = out;
+    *reinterpret_cast<E8*>(p.y + (int64_t)ov * p.yp + o) = out;
   }
 }
 
@@ -1117,10 +1118,10 @@ __global__ __launch_bounds__(RS_THREADS) void conv_reduce_stats_kernel(ConvParam
   const int k = blockIdx.x, b = blockIdx.y;
   const int nv = min(32, ovol - k * 32);
   const int64_t plane = (int64_t)p.B * ovol * p.O;
-  f16x8 keep[RS_PASSES];
+  E8 keep[RS_PASSES];
   bool okj[RS_PASSES];
   f32x4 lo[RS_PASSES], hi[RS_PASSES];
-  f16x8 rs[RS_PASSES];
+  E8 rs[RS_PASSES];
   int64_t ov[RS_PASSES];
   // Every pass's operands requested before any is summed.
 #pragma unroll
@@ -1130,8 +1131,8 @@ __global__ __launch_bounds__(RS_THREADS) void conv_reduce_stats_kernel(ConvParam
     ov[j] = (int64_t)b * ovol + k * 32 + (okj[j] ? v : 0);
     lo[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
     hi[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    rs[j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-    if (okj[j] && p.res) rs[j] = *reinterpret_cast<const f16x8*>(p.res + ov[j] * p.resp + o);
+    rs[j] = (E8){0, 0, 0, 0, 0, 0, 0, 0};
+    if (okj[j] && p.res) rs[j] = *reinterpret_cast<const E8*>(p.res + ov[j] * p.resp + o);
   }
 #pragma unroll 4
   for (int s2 = 0; s2 < p.split; s2++)
@@ -1147,23 +1148,23 @@ __global__ __launch_bounds__(RS_THREADS) void conv_reduce_stats_kernel(ConvParam
     const float* bias = p.bias ? p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o : nullptr;
     f32x4 b0 = {0.f, 0.f, 0.f, 0.f}, b1 = {0.f, 0.f, 0.f, 0.f};
     if (bias && vs < VP) { b0 = *reinterpret_cast<const f32x4*>(bias); b1 = *reinterpret_cast<const f32x4*>(bias + 4); }
-    f16x8 sh = {};
-    if (p.shift && vs < VP) sh = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o);
+    E8 sh = {};
+    if (p.shift && vs < VP) sh = *reinterpret_cast<const E8*>(p.shift + (int64_t)b * p.shiftp + o);
 #pragma unroll
     for (int r = 0; r < 4; r++) { add[r] = b0[r] + (float)sh[r]; add[r + 4] = b1[r] + (float)sh[r + 4]; }
   }
   float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < RS_PASSES; j++) {
-    keep[j] = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
+    keep[j] = (E8){0, 0, 0, 0, 0, 0, 0, 0};
     if (!okj[j]) continue;
-    f16x8 out;
+    E8 out;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      out[r] = post_act((f16)((lo[j][r] + add[r]) * p.scale + (float)rs[j][r]), p.act);
-      out[r + 4] = post_act((f16)((hi[j][r] + add[r + 4]) * p.scale + (float)rs[j][r + 4]), p.act);
+      out[r] = post_act((E)((lo[j][r] + add[r]) * p.scale + (float)rs[j][r]), p.act);
+      out[r + 4] = post_act((E)((hi[j][r] + add[r + 4]) * p.scale + (float)rs[j][r + 4]), p.act);
     }
-    *reinterpret_cast<f16x8*>(p.y + ov[j] * p.yp + o) = out;
+    *reinterpret_cast<E8*>(p.y + ov[j] * p.yp + o) = out;
     keep[j] = out;
 #pragma unroll
     for (int q = 0; q < 4; q++) s4[q] += (float)out[2 * q] + (float)out[2 * q + 1];
@@ -1315,9 +1316,6 @@ static int dispatch_k(ConvParams& p, int cc, bool vec, int grid_z, hipStream_t s
   return dispatch_cc<WO, WV, FO, FV, 1, KSPL>(p, cc, false, grid_z, stream, lds);
 }
 
-}  // namespace ldx
-
-using namespace ldx;
 
 // Validate the arguments and choose tile, brick, channel chunk and split for them.
 static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& lds, bool& vec,
@@ -1356,15 +1354,15 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
     p.OD = p.D; p.OH = p.H; p.OW = p.W;
     p.RD = p.D; p.RH = p.H; p.RW = p.W;
   }
-  p.x0 = (const f16*)a->x0; p.x0p = a->x0_pitch;
-  p.x1 = (const f16*)a->x1; p.x1p = a->x1_pitch;
-  p.w = (const f16*)a->weight;
+  p.x0 = (const E*)a->x0; p.x0p = a->x0_pitch;
+  p.x1 = (const E*)a->x1; p.x1p = a->x1_pitch;
+  p.w = (const E*)a->weight;
   p.bias = a->bias; p.bias_batched = a->bias_batched ? 1 : 0;
-  p.shift = (const f16*)a->shift; p.shiftp = a->shift_pitch;
+  p.shift = (const E*)a->shift; p.shiftp = a->shift_pitch;
   p.affine = a->affine; p.silu = a->silu ? 1 : 0;
-  p.res = (const f16*)a->residual; p.resp = a->residual_pitch;
+  p.res = (const E*)a->residual; p.resp = a->residual_pitch;
   p.scale = a->output_scale; p.act = a->act;
-  p.y = (f16*)a->y; p.yp = a->y_pitch;
+  p.y = (E*)a->y; p.yp = a->y_pitch;
   p.yvec = (p.yp % 4 == 0) && ((uintptr_t)a->y % 8 == 0);
   p.ep_vec = p.yp % 8 == 0 && (uintptr_t)a->y % 16 == 0 &&
              (!a->residual || (p.resp % 8 == 0 && (uintptr_t)a->residual % 16 == 0)) &&
@@ -1425,7 +1423,7 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
       const int pad_units = ((target - base_units) % 16 + 16) % 16;
       p.RS = (base_units + pad_units) * 8;
     }
-    lds = (size_t)p.HD * p.HH * p.RS * sizeof(f16);
+    lds = (size_t)p.HD * p.HH * p.RS * sizeof(E);
     const size_t wbytes = (size_t)WRING * (t.BO() / 32) * (t.CC / 16) * 1024;
     if (lds + wbytes <= (forced ? 160u * 1024 : 80u * 1024) || (t.CC == 32 && t.FV == 1)) break;
     if (t.CC == 64) t.CC = 32;
@@ -1471,7 +1469,7 @@ static bool use_dense(const ldx_conv3d_args* a, bool vec) {
   return a->ksize == 1 && vec && (a->c1 == 0 || a->c0 % 16 == 0);
 }
 
-extern "C" size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* a) {
+size_t conv3d_workspace_bytes(const ldx_conv3d_args* a) {
   ConvParams p;
   Tile t;
   size_t lds;
@@ -1651,23 +1649,23 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
   return launch_reduce(p, st, "conv3d: split reduce");
 }
 
-extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
+int conv3d_entry(const ldx_conv3d_args* a, void* stream) {
   return conv3d_run(a, nullptr, false, nullptr, stream);
 }
 
-extern "C" int64_t ldx_conv3d_stats_chunks(const ldx_conv3d_args* a) {
+int64_t conv3d_stats_chunks(const ldx_conv3d_args* a) {
   int64_t ch = 0;
   if (!a || conv3d_run(a, nullptr, true, &ch, nullptr) != LDX_OK) return 0;
   return ch;
 }
 
-extern "C" int ldx_conv3d_stats(const ldx_conv3d_args* a, float* stats, void* stream) {
+int conv3d_stats(const ldx_conv3d_args* a, float* stats, void* stream) {
   if (!stats) return fail("conv3d_stats: null moments buffer");
   if ((uintptr_t)stats % 16) return fail("conv3d_stats: moments buffer must be 16-byte aligned");
   return conv3d_run(a, stats, false, nullptr, stream);
 }
 
-extern "C" int ldx_dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps,
+int dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps,
                             void* stream) {
   if (!a || !gamma || !beta) return fail("dense_ln: null pointer");
   if (a->ksize != 1 || a->c1 != 0 || a->affine || a->silu || a->stride != 1 || a->upsample)
@@ -1688,3 +1686,55 @@ extern "C" int ldx_dense_ln(const ldx_conv3d_args* a, const float* gamma, const 
   p.ln_eps = eps;
   return launch_dense_ksplit<1, 1, true>(p, as_stream(stream));
 }
+
+}  // namespace LDX_ELEM_NS
+}  // namespace ldx
+
+#if !defined(LDX_ELEM_BF16)
+// The C entry points (in the fp16 unit only): argument checks shared by both element
+// types, then the planner and kernels of the args' dtype.
+namespace ldx {
+namespace bf16_path {
+size_t conv3d_workspace_bytes(const ldx_conv3d_args* a);
+int conv3d_entry(const ldx_conv3d_args* a, void* stream);
+int64_t conv3d_stats_chunks(const ldx_conv3d_args* a);
+int conv3d_stats(const ldx_conv3d_args* a, float* stats, void* stream);
+int dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps, void* stream);
+}  // namespace bf16_path
+}  // namespace ldx
+
+static bool conv_is_bf16(const ldx_conv3d_args* a) { return a && a->dtype == LDX_DTYPE_BF16; }
+static int conv_dtype_ok(const ldx_conv3d_args* a) {
+  if (a && a->dtype != LDX_DTYPE_F16 && a->dtype != LDX_DTYPE_BF16)
+    return ldx::fail("conv3d: dtype %d is not LDX_DTYPE_F16 or LDX_DTYPE_BF16", a->dtype);
+  return LDX_OK;
+}
+
+extern "C" size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* a) {
+  if (conv_dtype_ok(a) != LDX_OK) return 0;
+  return conv_is_bf16(a) ? ldx::bf16_path::conv3d_workspace_bytes(a) : ldx::f16_path::conv3d_workspace_bytes(a);
+}
+
+extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
+  if (int rc = conv_dtype_ok(a)) return rc;
+  return conv_is_bf16(a) ? ldx::bf16_path::conv3d_entry(a, stream) : ldx::f16_path::conv3d_entry(a, stream);
+}
+
+extern "C" int64_t ldx_conv3d_stats_chunks(const ldx_conv3d_args* a) {
+  if (conv_dtype_ok(a) != LDX_OK) return 0;
+  return conv_is_bf16(a) ? ldx::bf16_path::conv3d_stats_chunks(a) : ldx::f16_path::conv3d_stats_chunks(a);
+}
+
+extern "C" int ldx_conv3d_stats(const ldx_conv3d_args* a, float* stats, void* stream) {
+  if (int rc = conv_dtype_ok(a)) return rc;
+  return conv_is_bf16(a) ? ldx::bf16_path::conv3d_stats(a, stats, stream)
+                         : ldx::f16_path::conv3d_stats(a, stats, stream);
+}
+
+extern "C" int ldx_dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps,
+                            void* stream) {
+  if (int rc = conv_dtype_ok(a)) return rc;
+  return conv_is_bf16(a) ? ldx::bf16_path::dense_ln(a, gamma, beta, eps, stream)
+                         : ldx::f16_path::dense_ln(a, gamma, beta, eps, stream);
+}
+#endif

@@ -2,9 +2,10 @@
 // by ldx_conv3d.
 #pragma once
 
-#include "common.h"
+#include "elem.h"
 
 namespace ldx {
+namespace LDX_ELEM_NS {
 
 struct StreamParams {
   int B, D, H, W;
@@ -17,15 +18,15 @@ struct StreamParams {
   int split, cps;           // split-K: workgroup ranges of cps channel chunks (split > 1)
   int g1;                   // workgroups per split: bricks x output blocks x batch items
   float* part;              // split > 1: fp32 partial sums [split][B * D * H * W][O]
-  const f16* x0; int64_t x0p;
-  const f16* x1; int64_t x1p;
-  const f16* w;
+  const E* x0; int64_t x0p;
+  const E* x1; int64_t x1p;
+  const E* w;
   const float* bias; int bias_batched;
-  const f16* shift; int64_t shiftp;
+  const E* shift; int64_t shiftp;
   const float* affine; int silu;
-  const f16* res; int64_t resp;
+  const E* res; int64_t resp;
   float scale;
-  f16* y; int64_t yp;
+  E* y; int64_t yp;
   float* stats;             // GroupNorm partial moments [B][schunks][O / 2][3], or null
   int schunks;              // moment blocks per batch item: one per brick
 };
@@ -36,4 +37,5 @@ struct StreamParams {
 bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* p, bool check_ws = true);
 int conv3d_stream_launch(StreamParams& p, hipStream_t st);
 
+}  // namespace LDX_ELEM_NS
 }  // namespace ldx

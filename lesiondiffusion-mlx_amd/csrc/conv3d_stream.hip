@@ -28,12 +28,13 @@
 // Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619), prologue
 // _nax_conv.py:128-136, epilogue :265-270 (+ scaled variant :418-421).
 
-#include "common.h"
+#include "elem.h"
 #include "conv3d_stream.h"
 
 #include <type_traits>
 
 namespace ldx {
+namespace LDX_ELEM_NS {
 namespace cs {
 
 constexpr int CC = 32;            // channels per chunk (two k-steps, one per K-group)
@@ -82,8 +83,8 @@ struct Shape {
   static_assert(HALO % 16 == 0 && STAGE % 1024 == 0, "alignment");
 };
 
-__device__ __forceinline__ f32x16 mfma(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma(E8 a, E8 b, f32x16 c) {
+  return mfma_e(a, b, c);
 }
 
 template <int I>
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     hlo[j] = vox < S::HVOX ? ((hd * S::HH + hh) * S::RS + hw * PITCH + cg * 8) * 2 : -1;
   }
   const int64_t vol = (int64_t)p.D * p.H * p.W;
-  f16x8 hval[S::NHS];
+  E8 hval[S::NHS];
   f32x4 haff[4];
   // Request chunk ch's halo (NHS 16-byte loads) and the affine of this thread's 8
   // channels (4 loads): exactly NHL loads, zeros where a buffer range ends (padding
@@ -155,13 +156,13 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     const int c0 = ch * CC;
     const bool live = ch < ce;
     const bool in0 = c0 < p.C0;
-    const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
+    const E* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
     const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
     const i32x4 rs = dma_rsrc(base, live ? (unsigned)(vol * pitch2) : 0u);
     const unsigned cofs = (unsigned)(((in0 ? c0 : c0 - p.C0) + cg * 8) * 2);
 #pragma unroll
     for (int j = 0; j < S::NHS; j++)
-      hval[j] = buffer_load16_asm(rs, hvi[j] != ~0u ? hvi[j] * pitch2 + cofs : 0xfffffff0u);
+      hval[j] = buffer_load16_asm<E8>(rs, hvi[j] != ~0u ? hvi[j] * pitch2 + cofs : 0xfffffff0u);
     const i32x4 ra = dma_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine,
                               p.affine && live ? (unsigned)(p.C * 8) : 0u);
 #pragma unroll
@@ -180,7 +181,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
 #pragma unroll
     for (int j = 0; j < S::NHS; j++) {
       if (hlo[j] < 0) continue;
-      f16x8 v = hval[j];
+      E8 v = hval[j];
       if (xf) {
 #pragma unroll
         for (int e = 0; e < 8; e++) {
@@ -188,10 +189,10 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
           const float of = p.affine ? haff[e >> 1][(e & 1) * 2 + 1] : 0.f;
           float yv = (float)v[e] * sc + of;
           if (p.silu) yv = silu_f(yv);
-          v[e] = hvi[j] != ~0u ? (f16)yv : (f16)0;
+          v[e] = hvi[j] != ~0u ? (E)yv : (E)0;
         }
       }
-      *reinterpret_cast<f16x8*>(hb + hlo[j]) = v;
+      *reinterpret_cast<E8*>(hb + hlo[j]) = v;
     }
   };
 
@@ -226,7 +227,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     const int c0 = ch * CC;
     const bool live = ch < ce;
     const bool in0 = c0 < p.C0;
-    const f16* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
+    const E* base = in0 ? p.x0 + b * vol * p.x0p : p.x1 + b * vol * p.x1p;
     const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
     const i32x4 rs = dma_rsrc(base, live ? (unsigned)(vol * pitch2) : 0u);
     const unsigned cb = (unsigned)((in0 ? c0 : c0 - p.C0) * 2);
@@ -241,7 +242,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // f = (kw * 2 + k) * NOBT + ob, the packed fragment of output block oblk * NOBT + ob, tap
   // (kd, kh, kw) and k-step 2 * chunk + k. Wave w moves fragments (w + 8 i) % NF (a repeat
   // moves the same data to the same place, so every wave issues LW loads per stage).
-  const f16* wsrc[S::LW];
+  const E* wsrc[S::LW];
   unsigned wdst[S::LW];
 #pragma unroll
   for (int i = 0; i < S::LW; i++) {
@@ -282,18 +283,18 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
 
-  f16x8 ra[3][2], rb[3][2];   // operands of taps kw = 0, 1, 2: [kw][fo], [kw][fv]
+  E8 ra[3][2], rb[3][2];   // operands of taps kw = 0, 1, 2: [kw][fo], [kw][fv]
   auto tap_off = [&](int kd, int kh, int kw) { return ((kd * S::HH + kh) * S::RS + kw * PITCH) * 2; };
   // A of tap kw of the stage at ring position `as`.
   auto load_a = [&](int kw, const char* as) {
 #pragma unroll
     for (int fo = 0; fo < 2; fo++)
-      ra[kw][fo] = *reinterpret_cast<const f16x8*>(as + (kw * 2 * S::NOBT + fo) * 1024);
+      ra[kw][fo] = *reinterpret_cast<const E8*>(as + (kw * 2 * S::NOBT + fo) * 1024);
   };
   // B of tap (kd, kh, kw) from halo buffer hb.
   auto load_b = [&](int kw, int kd, int kh, const char* hb) {
 #pragma unroll
-    for (int fv = 0; fv < 2; fv++) rb[kw][fv] = *reinterpret_cast<const f16x8*>(hb + bofs[fv] + tap_off(kd, kh, kw));
+    for (int fv = 0; fv < 2; fv++) rb[kw][fv] = *reinterpret_cast<const E8*>(hb + bofs[fv] + tap_off(kd, kh, kw));
   };
   auto mfma_tap = [&](int kw) {
 #pragma unroll
@@ -394,18 +395,18 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // residual -- requested before the partial rows are written, which hides their latency
   // (and none of these loads delays the prologue's DMA).
   f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
-  f16x8 sv = {};
-  f16x8 res[4];
+  E8 sv = {};
+  E8 res[4];
   if (p.bias && p.split == 1) {
     const float* bias = p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o8;
     bv0 = *reinterpret_cast<const f32x4*>(bias);
     bv1 = *reinterpret_cast<const f32x4*>(bias + 4);
   }
-  if (p.shift && p.split == 1) sv = *reinterpret_cast<const f16x8*>(p.shift + (int64_t)b * p.shiftp + o8);
+  if (p.shift && p.split == 1) sv = *reinterpret_cast<const E8*>(p.shift + (int64_t)b * p.shiftp + o8);
 #pragma unroll
   for (int i = 0; i < 4; i++)
-    res[i] = p.res && p.split == 1 && okr[i] ? *reinterpret_cast<const f16x8*>(p.res + ovr[i] * p.resp + o8)
-                                             : (f16x8){};
+    res[i] = p.res && p.split == 1 && okr[i] ? *reinterpret_cast<const E8*>(p.res + ovr[i] * p.resp + o8)
+                                             : (E8){};
   // Both K-groups leave their partial sums as fp32 rows, [w4][fv][group][voxel][channel]
   // (rows padded to RP floats: 16-byte writes free of bank conflicts).
   float* rowsb = reinterpret_cast<float*>(smem);
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   __syncthreads();
   // Rows fv = kg: (group 0 + group 1), then bias + shift, scale, residual, one rounding --
   // or, split over channel chunks, the fp32 sums of this range (the reduce finishes them).
-  f16x8 outv[4];
+  E8 outv[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     const int ro = ((lane >> 3) + 8 * i) * S::RP + g8 * 8;
@@ -438,13 +439,13 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       }
       continue;
     }
-    f16x8& out = outv[i];
+    E8& out = outv[i];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      out[e] = (f16)((s0[e] + (bv0[e] + (float)sv[e])) * p.scale + (float)res[i][e]);
-      out[e + 4] = (f16)((s1[e] + (bv1[e] + (float)sv[e + 4])) * p.scale + (float)res[i][e + 4]);
+      out[e] = (E)((s0[e] + (bv0[e] + (float)sv[e])) * p.scale + (float)res[i][e]);
+      out[e + 4] = (E)((s1[e] + (bv1[e] + (float)sv[e + 4])) * p.scale + (float)res[i][e + 4]);
     }
-    if (okr[i]) *reinterpret_cast<f16x8*>(p.y + ovr[i] * p.yp + o8) = out;
+    if (okr[i]) *reinterpret_cast<E8*>(p.y + ovr[i] * p.yp + o8) = out;
   }
   // GroupNorm partial moments of the stored values, one block per brick: each wave's
   // 32 voxels x 32 channel pairs (lanes l, l + 8, ... hold the same 8 channels) into LDS
@@ -537,15 +538,15 @@ bool conv3d_stream_plan(const ldx_conv3d_args* a, StreamParams* out, bool check_
   p.C0 = a->c0; p.C1 = a->c1; p.C = a->c0 + a->c1; p.O = a->out_c;
   p.nchunk = p.C / CC;
   p.NKC = (p.C + 63) / 64 * 4;
-  p.x0 = (const f16*)a->x0; p.x0p = a->x0_pitch;
-  p.x1 = a->c1 > 0 ? (const f16*)a->x1 : p.x0; p.x1p = a->c1 > 0 ? a->x1_pitch : a->x0_pitch;
-  p.w = (const f16*)a->weight;
+  p.x0 = (const E*)a->x0; p.x0p = a->x0_pitch;
+  p.x1 = a->c1 > 0 ? (const E*)a->x1 : p.x0; p.x1p = a->c1 > 0 ? a->x1_pitch : a->x0_pitch;
+  p.w = (const E*)a->weight;
   p.bias = a->bias; p.bias_batched = a->bias_batched ? 1 : 0;
-  p.shift = (const f16*)a->shift; p.shiftp = a->shift_pitch;
+  p.shift = (const E*)a->shift; p.shiftp = a->shift_pitch;
   p.affine = a->affine; p.silu = a->silu ? 1 : 0;
-  p.res = (const f16*)a->residual; p.resp = a->residual_pitch;
+  p.res = (const E*)a->residual; p.resp = a->residual_pitch;
   p.scale = a->output_scale;
-  p.y = (f16*)a->y; p.yp = a->y_pitch;
+  p.y = (E*)a->y; p.yp = a->y_pitch;
 
   // Among the tiles that launch at least 200 workgroups: the fewest launched voxel slots
   // (partial-brick waste), then the fewest halo voxels per output, then 128-channel tiles
@@ -611,4 +612,5 @@ int conv3d_stream_launch(StreamParams& p, hipStream_t st) {
   return fail("conv3d (streamed): no kernel for tile %d, brick %dx%dx%d", p.bo, p.TD, p.TH, p.TW);
 }
 
+}  // namespace LDX_ELEM_NS
 }  // namespace ldx

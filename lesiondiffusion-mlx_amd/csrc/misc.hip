@@ -86,8 +86,8 @@ __device__ __forceinline__ void fold_set(int p, int t, int& k_lo, int& k_hi) {
 // parity = pd*4+ph*2+pw, tap = td*4+th*2+tw. Sums are float32 and nest d (innermost),
 // then h, then w, each left to right -- the order of the reference's per-axis folds
 // (_nax_conv.py:394-405) -- and are rounded to fp16 once.
-__global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
-                                     f16* __restrict__ out) {
+template <typename T>
+__global__ void pack_upsample_kernel(const T* __restrict__ w, int O, int C, T* __restrict__ out) {
   const int NOB = (O + 127) / 128 * 4, NKC = (C + 63) / 64 * 4;
   const int64_t n = (int64_t)8 * NOB * 8 * NKC * 512;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
@@ -97,14 +97,14 @@ __global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
     const int parity = (int)(pob / NOB), ob = (int)(pob % NOB);
     const int o = ob * 32 + (l & 31);
     const int c = kc * 16 + 8 * (l >> 5) + e;
-    if (o >= O || c >= C) { out[i] = (f16)0; continue; }
+    if (o >= O || c >= C) { out[i] = (T)0.f; continue; }
     const int pd = parity >> 2, ph = (parity >> 1) & 1, pw = parity & 1;
     const int td = tap >> 2, th = (tap >> 1) & 1, tw = tap & 1;
     int d_lo, d_hi, h_lo, h_hi, w_lo, w_hi;
     fold_set(pd, td, d_lo, d_hi);
     fold_set(ph, th, h_lo, h_hi);
     fold_set(pw, tw, w_lo, w_hi);
-    const f16* base = w + ((int64_t)o * C + c) * 27;
+    const T* base = w + ((int64_t)o * C + c) * 27;
     float tot = 0.0f;
     for (int kw = w_lo; kw <= w_hi; kw++) {
       float hs = 0.0f;
@@ -115,7 +115,7 @@ __global__ void pack_upsample_kernel(const f16* __restrict__ w, int O, int C,
       }
       tot += hs;
     }
-    out[i] = (f16)tot;
+    out[i] = (T)tot;
   }
 }
 
@@ -511,7 +511,7 @@ __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict_
 using namespace ldx;
 
 extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
-extern "C" int ldx_abi_version(void) { return 4; }
+extern "C" int ldx_abi_version(void) { return 5; }
 
 extern "C" size_t ldx_packed_weight_elems(int32_t O, int32_t C, int32_t k, int32_t upsample) {
   if (O < 1 || C < 1 || (k != 1 && k != 3) || (upsample && k != 3)) return 0;
@@ -530,13 +530,19 @@ extern "C" int ldx_pack_weight(const void* weight, int32_t O, int32_t C, int32_t
   return check_launch("pack_weight");
 }
 
-extern "C" int ldx_pack_upsample_weight(const void* weight, int32_t O, int32_t C, void* packed,
+extern "C" int ldx_pack_upsample_weight(const void* weight, int32_t O, int32_t C, int32_t dtype, void* packed,
                                         void* stream) {
   if (!weight || !packed) return fail("pack_upsample_weight: null pointer");
   if (O < 1 || C < 1) return fail("pack_upsample_weight: bad shape O=%d C=%d", O, C);
+  if (dtype != LDX_DTYPE_F16 && dtype != LDX_DTYPE_BF16)
+    return fail("pack_upsample_weight: dtype %d is not LDX_DTYPE_F16 or LDX_DTYPE_BF16", dtype);
   const int64_t n = (int64_t)ldx_packed_weight_elems(O, C, 3, 1);
-  hipLaunchKernelGGL(pack_upsample_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
-                     as_stream(stream), (const f16*)weight, O, C, (f16*)packed);
+  if (dtype == LDX_DTYPE_BF16)
+    hipLaunchKernelGGL(pack_upsample_kernel<bf16>, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
+                       as_stream(stream), (const bf16*)weight, O, C, (bf16*)packed);
+  else
+    hipLaunchKernelGGL(pack_upsample_kernel<f16>, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
+                       as_stream(stream), (const f16*)weight, O, C, (f16*)packed);
   return check_launch("pack_upsample_weight");
 }
 

@@ -62,13 +62,23 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
-def _require_cuda(t: torch.Tensor, name: str, dtype: torch.dtype | None = torch.float16) -> None:
+# Element types of the conv / attention kernels (the C ABI's LDX_DTYPE_*).
+ELEM_DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _require_cuda(t: torch.Tensor, name: str, dtype: torch.dtype | tuple | None = torch.float16) -> None:
     if not isinstance(t, torch.Tensor):
         raise ValueError(f"{name} must be a torch tensor")
     if not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor (got {t.device}); there is no CPU path")
-    if dtype is not None and t.dtype != dtype:
-        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    allowed = dtype if isinstance(dtype, tuple) else (dtype,)
+    if dtype is not None and t.dtype not in allowed:
+        raise ValueError(f"{name} must be {' or '.join(str(d) for d in allowed)}, got {t.dtype}")
+
+
+def _same_elem(t: torch.Tensor, name: str, dtype: torch.dtype) -> None:
+    """``t`` is a device tensor of the call's element type ``dtype``."""
+    _require_cuda(t, name, dtype)
 
 
 def voxel_pitch(x: torch.Tensor, name: str = "x") -> int:
@@ -118,10 +128,10 @@ class PackedWeight:
 
 
 def pack_weight(weight: torch.Tensor) -> PackedWeight:
-    """Pack a Torch-layout ``(O, C, K, K, K)`` (K = 1 or 3) or dense ``(O, C)`` fp16
-    weight (the reference's ``pack_weight``, _nax_conv.py:350-364, in this library's
-    layout)."""
-    _require_cuda(weight, "weight")
+    """Pack a Torch-layout ``(O, C, K, K, K)`` (K = 1 or 3) or dense ``(O, C)`` fp16 or
+    bf16 weight (the reference's ``pack_weight``, _nax_conv.py:350-364, in this library's
+    layout); the packed tensor keeps the weight's dtype."""
+    _require_cuda(weight, "weight", tuple(ELEM_DTYPES))
     if weight.dim() == 2:
         weight = weight.reshape(*weight.shape, 1, 1, 1)
     if weight.dim() != 5 or weight.shape[2] != weight.shape[3] or weight.shape[3] != weight.shape[4] \
@@ -129,21 +139,22 @@ def pack_weight(weight: torch.Tensor) -> PackedWeight:
         raise ValueError(f"weight must be (O, C, K, K, K) with K in (1, 3), got {tuple(weight.shape)}")
     o, c, k = int(weight.shape[0]), int(weight.shape[1]), int(weight.shape[2])
     w = weight.contiguous()
-    out = torch.empty(lib.ldx_packed_weight_elems(o, c, k, 0), dtype=torch.float16, device=weight.device)
+    out = torch.empty(lib.ldx_packed_weight_elems(o, c, k, 0), dtype=w.dtype, device=weight.device)
     check(lib.ldx_pack_weight(_ptr(w), o, c, k, _ptr(out), _stream()), "pack_weight")
     return PackedWeight(out, o, c, k, False)
 
 
 def pack_upsample_weight(weight: torch.Tensor) -> PackedWeight:
     """Fold a ``(O, C, 3, 3, 3)`` fp16 weight into 8 parity 2x2x2 filters for a conv of a
-    nearest 2x upsampling (_nax_conv.py:367-405)."""
-    _require_cuda(weight, "weight")
+    nearest 2x upsampling (_nax_conv.py:367-405), in the weight's dtype (fp16 or bf16)."""
+    _require_cuda(weight, "weight", tuple(ELEM_DTYPES))
     if weight.dim() != 5 or tuple(weight.shape[2:]) != (3, 3, 3):
         raise ValueError(f"weight must be (O, C, 3, 3, 3), got {tuple(weight.shape)}")
     o, c = int(weight.shape[0]), int(weight.shape[1])
     w = weight.contiguous()
-    out = torch.empty(lib.ldx_packed_weight_elems(o, c, 3, 1), dtype=torch.float16, device=weight.device)
-    check(lib.ldx_pack_upsample_weight(_ptr(w), o, c, _ptr(out), _stream()), "pack_upsample_weight")
+    out = torch.empty(lib.ldx_packed_weight_elems(o, c, 3, 1), dtype=w.dtype, device=weight.device)
+    check(lib.ldx_pack_upsample_weight(_ptr(w), o, c, ELEM_DTYPES[w.dtype], _ptr(out), _stream()),
+          "pack_upsample_weight")
     return PackedWeight(out, o, c, 3, True)
 
 
@@ -197,15 +208,21 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     split-K plans; ``moments="always"`` keeps them there too): a later
     ``group_norm_affine`` of the returned tensor then merges them instead of reading it.
 
-    Returns NDHWC ``(B, D', H', W', O)`` fp16 (written into ``out`` when given, which may
-    be a channel slice of a wider tensor).
+    Element type: fp16 or bf16 (``x``'s dtype; ``x1``, the packed weight, ``shift``,
+    ``residual`` and ``out`` must share it; bias and affine are fp32 either way).
+
+    Returns NDHWC ``(B, D', H', W', O)`` in ``x``'s dtype (written into ``out`` when given,
+    which may be a channel slice of a wider tensor).
     """
-    _require_cuda(x, "x")
+    _require_cuda(x, "x", tuple(ELEM_DTYPES))
+    et = x.dtype
+    if packed.data.dtype != et:
+        raise ValueError(f"packed weight is {packed.data.dtype} but x is {et}")
     xp = voxel_pitch(x, "x")
     b, d, h, w, c0 = (int(s) for s in x.shape)
     c1, x1p = 0, 0
     if x1 is not None:
-        _require_cuda(x1, "x1")
+        _same_elem(x1, "x1", et)
         x1p = voxel_pitch(x1, "x1")
         if tuple(x1.shape[:4]) != (b, d, h, w):
             raise ValueError(f"x1 grid {tuple(x1.shape[:4])} != x grid {(b, d, h, w)}")
@@ -231,14 +248,14 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
         aff = affine.contiguous()
     resp = 0
     if residual is not None:
-        _require_cuda(residual, "residual")
+        _same_elem(residual, "residual", et)
         if tuple(residual.shape) != (b, *grid, o):
             raise ValueError(f"residual shape {tuple(residual.shape)} != output {(b, *grid, o)}")
         resp = voxel_pitch(residual, "residual")
     if out is None:
-        out = torch.empty((b, *grid, o), dtype=torch.float16, device=x.device)
+        out = torch.empty((b, *grid, o), dtype=et, device=x.device)
     else:
-        _require_cuda(out, "out")
+        _same_elem(out, "out", et)
         if tuple(out.shape) != (b, *grid, o):
             raise ValueError(f"out shape {tuple(out.shape)} != {(b, *grid, o)}")
     yp = voxel_pitch(out, "out")
@@ -254,8 +271,9 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     a.residual, a.residual_pitch = (residual.data_ptr() if residual is not None else None), resp
     a.output_scale = float(output_scale)
     a.act = {None: ACT_NONE, "gelu": ACT_GELU, "silu": ACT_SILU}[act]
+    a.dtype = ELEM_DTYPES[et]
     if shift is not None:
-        _require_cuda(shift, "shift")
+        _same_elem(shift, "shift", et)
         if shift.dim() != 2 or tuple(shift.shape) != (b, o) or shift.stride(1) != 1:
             raise ValueError(f"shift must be (B, O) = {(b, o)} with contiguous channels")
         a.shift, a.shift_pitch = shift.data_ptr(), shift.stride(0) if b > 1 else o
@@ -438,6 +456,7 @@ def _attn_args(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, o4: torch.T
         setattr(a, name, t.data_ptr())
         getattr(a, name + "_stride")[:] = [t.stride(0), t.stride(1), t.stride(2)]
     a.scale = float(scale)
+    a.dtype = ELEM_DTYPES[q4.dtype]
     a.mask = None
     if mask is not None:
         a.mask = mask.data_ptr()
@@ -469,16 +488,18 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
     """``softmax(q k^T * scale + mask) v`` for fp16 ``(B, H, L, D)`` tensors, the contract
     of ``mx.fast.scaled_dot_product_attention`` (mlx_model.py:485-487, 860-862). ``mask``
     is additive (``-inf`` removes a key) or boolean (``True`` keeps a key), broadcast to
-    ``(B, H, L, LK)``. Returns ``(B, H, L, D)``."""
+    ``(B, H, L, LK)``. fp16 or bf16 (all three alike; the probabilities are rounded to
+    that type for the P V product). Returns ``(B, H, L, D)``."""
+    _require_cuda(q, "q", tuple(ELEM_DTYPES))
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _require_cuda(t, name)
+        _same_elem(t, name, q.dtype)
         if t.dim() != 4:
             raise ValueError(f"{name} must be (B, H, L, D)")
     b, h, lq, d = (int(s) for s in q.shape)
     lk = int(k.shape[2])
     if tuple(k.shape) != (b, h, lk, d) or tuple(v.shape) != (b, h, lk, d):
         raise ValueError(f"k/v shapes {tuple(k.shape)}, {tuple(v.shape)} do not fit q {tuple(q.shape)}")
-    out = torch.empty((b, h, lq, d), dtype=torch.float16, device=q.device)
+    out = torch.empty((b, h, lq, d), dtype=q.dtype, device=q.device)
     m = _prepare_mask(mask, b, h, lq, lk, q.device)
     a = _attn_args(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), out.transpose(1, 2), scale, m)
     if count_flops.active is not None:
@@ -491,9 +512,11 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
                     out: torch.Tensor | None = None) -> torch.Tensor:
     """Multi-head attention on head-interleaved projections ``(B, L, heads * d)``
     (head ``h`` = columns ``h*d .. h*d+d-1``), returning that layout
-    (flash_attention, _attention.py:331-351). Key length may differ from query length."""
+    (flash_attention, _attention.py:331-351). Key length may differ from query length.
+    fp16 or bf16."""
+    _require_cuda(q, "q", tuple(ELEM_DTYPES))
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _require_cuda(t, name)
+        _same_elem(t, name, q.dtype)
         if t.dim() != 3:
             raise ValueError(f"{name} must be (B, L, heads * d)")
     b, lq, f = (int(s) for s in q.shape)
@@ -504,7 +527,9 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
     if tuple(k.shape) != (b, lk, f) or tuple(v.shape) != (b, lk, f):
         raise ValueError("k/v must be (B, LK, heads * d) matching q")
     if out is None:
-        out = torch.empty((b, lq, f), dtype=torch.float16, device=q.device)
+        out = torch.empty((b, lq, f), dtype=q.dtype, device=q.device)
+    else:
+        _same_elem(out, "out", q.dtype)
     a = _attn_args(q.view(b, lq, heads, d) if q.is_contiguous() else q.unflatten(2, (heads, d)),
                    k.unflatten(2, (heads, d)), v.unflatten(2, (heads, d)), out.unflatten(2, (heads, d)),
                    scale, None)

@@ -71,6 +71,7 @@ def _conv_args(lib, **kw):
     {"ksize": 5}, {"stride": 3}, {"batch": 0}, {"in_d": 0}, {"c0": 0}, {"out_c": 0},
     {"ksize": 1, "stride": 2}, {"upsample": 1, "stride": 2}, {"x0": None}, {"weight": None},
     {"c1": 8}, {"x0_pitch": 4}, {"y_pitch": 4}, {"act": 7}, {"residual": 16, "residual_pitch": 2},
+    {"dtype": 1}, {"dtype": 7},
 ])
 def test_conv3d_rejects_bad_arguments_before_launch(pkg, bad) -> None:
     lib = pkg._lib
@@ -93,6 +94,10 @@ def test_attention_rejects_bad_arguments_before_launch(pkg) -> None:
     a.q_stride[1] = 64
     a.kv_len = 0
     assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
+    a.kv_len = 8
+    a.dtype = 1   # fp32 is not an attention element type
+    assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
+    assert "dtype" in lib.last_error()
 
 
 def test_small_ops_reject_bad_arguments(pkg) -> None:
@@ -100,7 +105,8 @@ def test_small_ops_reject_bad_arguments(pkg) -> None:
     E = pkg._lib.LDX_EINVAL
     assert l.ldx_pack_weight(16, 0, 4, 3, 16, None) == E
     assert l.ldx_pack_weight(16, 4, 4, 2, 16, None) == E
-    assert l.ldx_pack_upsample_weight(None, 4, 4, 16, None) == E
+    assert l.ldx_pack_upsample_weight(None, 4, 4, 0, 16, None) == E
+    assert l.ldx_pack_upsample_weight(16, 4, 4, 7, 16, None) == E   # unknown dtype
     assert l.ldx_group_norm_affine(16, 8, 12, None, 0, 0, 1, 10, 5, 16, 16, 1e-5, 16, 16, None) == E
     assert l.ldx_layer_norm(16, 8, 1, 2000, 16, 16, 1e-5, 16, 2000, None) == E
     assert l.ldx_timestep_embedding(16, 1, 7, 16, None) == E
