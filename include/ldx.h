@@ -92,8 +92,9 @@ typedef struct ldx_conv3d_args {
   void* y; int64_t y_pitch;          /* fp16 NDHWC output */
   void* workspace;                   /* optional device scratch for split-K partial sums */
   size_t workspace_bytes;
-  int32_t dtype;                     /* LDX_DTYPE_F16 (0) or LDX_DTYPE_BF16: the type of x0, x1,
-                                        weight, shift, residual and y (bias and affine stay fp32) */
+  int32_t dtype;                     /* LDX_DTYPE_F16 (0), LDX_DTYPE_BF16 or LDX_DTYPE_F32: the type
+                                        of x0, x1, shift, residual and y (bias and affine stay
+                                        fp32); see the FP32 mode below for the weight */
 } ldx_conv3d_args;
 
 /* Bytes of workspace with which ldx_conv3d splits the reduction over channel chunks
@@ -123,6 +124,21 @@ int ldx_conv3d_stats(const ldx_conv3d_args* args, float* moments, void* stream);
  * and beta are fp32 (c0), 16-byte aligned. */
 int ldx_dense_ln(const ldx_conv3d_args* args, const float* gamma, const float* beta, float eps,
                  void* stream);
+
+/* FP32 mode (dtype LDX_DTYPE_F32) -- the reference's exact split-FP16 mode for FP32 networks
+ * (_nax_conv.py:26-34, 210-237, 343-364): every FP32 value v is split into hi = half(v) and
+ * lo = half((v - hi) * 2^11), and y = hi x hi + (hi x lo + lo x hi) * 2^-11 with FP32 sums
+ * (only lo x lo is dropped, about 2^-22 relative; |v| < 65504). The weight is the stacked
+ * split of ldx_pack_weight_exact; the prologue (affine, SiLU), the epilogue (bias + shift,
+ * scale, residual, GELU / SiLU) and y are FP32, with no rounding to 16 bits. upsample = 1
+ * takes the unfolded 3x3x3 weight (the conv runs on the upsampled grid). A workspace of
+ * ldx_conv3d_workspace_bytes() bytes is required (the split input and the FP32 products).
+ * ldx_conv3d_stats and ldx_dense_ln take fp16 / bf16 only. */
+int ldx_pack_weight_exact(const float* weight, int32_t out_c, int32_t in_c, int32_t ksize, void* packed,
+                          void* stream);
+/* ldx_pack_weight_exact: a Torch-layout FP32 (O, C, K, K, K) (or dense (O, C), K = 1) weight
+ * as the fp16 fragment-major packing (ldx_pack_weight) of 2O x 2C rows [[hi(W), 0],
+ * [lo(W), hi(W)]]: ldx_packed_weight_elems(2 O, 2 C, K, 0) halves. */
 
 /* Pack a Torch-layout fp16 or bf16 weight (O, C, K, K, K) (K = 3 or 1; a dense (O, C)
  * weight is K = 1; a pure rearrangement of 16-bit values, the same for both types) into
@@ -188,6 +204,16 @@ int ldx_group_norm_affine_moments(const float* m0, int64_t chunks0, int32_t c0,
                                   const float* gamma, const float* beta, float eps,
                                   float* affine, void* stream);
 
+/* GroupNorm statistics (as ldx_group_norm_affine) and LayerNorm (as ldx_layer_norm) of FP32
+ * tensors, statistics in FP32 (per-thread Welford moments merged in a fixed order; the row
+ * mean, then the mean squared deviation), FP32 output -- the FP32 networks' norms
+ * (mlx_model.py:328-335, 360-367). No workspace. */
+int ldx_group_norm_affine_f32(const float* x0, int64_t x0_pitch, int32_t c0, const float* x1, int64_t x1_pitch,
+                              int32_t c1, int32_t batch, int64_t voxels, int32_t groups, const float* gamma,
+                              const float* beta, float eps, float* affine, void* stream);
+int ldx_layer_norm_f32(const float* x, int64_t x_pitch, int64_t rows, int32_t features, const float* gamma,
+                       const float* beta, float eps, float* y, int64_t y_pitch, void* stream);
+
 /* LayerNorm over the last axis of fp16 (rows, features) (mx.fast.layer_norm,
  * mlx_model.py:360-367): y = half((x - mean) * rsqrt(var + eps) * gamma + beta),
  * statistics in fp32. gamma/beta fp32. */
@@ -205,6 +231,8 @@ int ldx_layer_norm(const void* x, int64_t x_pitch, int64_t rows, int32_t feature
  * (B, H, L, D) are views of this. head_dim in {16, 32, 64, 128, 256}.
  * mask (optional) is additive fp32 with strides (batch, head, query, key), 0 for a
  * broadcast axis; -inf removes a key; a query row with every key removed gives 0.
+ * LDX_DTYPE_F32 (the FP32 networks; the reference's FP32 attention, _attention.py:52-145):
+ * head_dim 16, 32 or 64, no mask, FP32 scores, probabilities and products throughout.
  * No scratch memory is used: V is read as it lies and transposed by the LDS reads.
  * ldx_attention_workspace_bytes returns 0 and the workspace fields are ignored (they
  * may be NULL / 0); they are kept so that callers sized by the query stay valid. */
@@ -217,7 +245,7 @@ typedef struct ldx_attention_args {
   float scale;
   const float* mask; int64_t mask_stride[4];
   void* workspace; size_t workspace_bytes;   /* unused; may be NULL / 0 */
-  int32_t dtype;                        /* LDX_DTYPE_F16 (0) or LDX_DTYPE_BF16: q, k, v and o */
+  int32_t dtype;                        /* LDX_DTYPE_F16 (0), LDX_DTYPE_BF16 or LDX_DTYPE_F32: q, k, v, o */
 } ldx_attention_args;
 
 size_t ldx_attention_workspace_bytes(const ldx_attention_args* args);
@@ -228,6 +256,8 @@ int ldx_attention(const ldx_attention_args* args, void* stream);
  * (mlx_model.py:609-612), written as fp16 (batch, channels). timesteps int32. */
 int ldx_timestep_embedding(const int32_t* timesteps, int32_t batch, int32_t channels,
                            void* out, void* stream);
+/* The same features in FP32 (the FP32 networks). */
+int ldx_timestep_embedding_f32(const int32_t* timesteps, int32_t batch, int32_t channels, float* out, void* stream);
 
 /* y = half(silu(float(x))) elementwise over n fp16 values (LdmUnet.silu,
  * mlx_model.py:409-413). */

@@ -100,6 +100,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_ddim_timestep": (c_i32, [c_vp, c_vp, c_i32, c_vp, c_vp]),
     "ldx_step_advance": (c_i32, [c_vp, c_vp]),
     "ldx_vq_squared_norms4": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_vp]),
+    "ldx_pack_weight_exact": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "ldx_group_norm_affine_f32": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
+                                          c_vp, c_vp, c_f32, c_vp, c_vp]),
+    "ldx_layer_norm_f32": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),
+    "ldx_timestep_embedding_f32": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_vq_nearest4": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
 }
 

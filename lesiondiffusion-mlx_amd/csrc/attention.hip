@@ -1135,6 +1135,7 @@ namespace bf16_path {
 size_t attention_workspace_bytes(const ldx_attention_args* a);
 int attention_entry(const ldx_attention_args* a, void* stream);
 }  // namespace bf16_path
+int attention_f32(const ldx_attention_args* a, void* stream);   // exact.hip
 }  // namespace ldx
 
 // The C entry points (in the fp16 unit only): the kernels of the args' dtype.
@@ -1145,8 +1146,9 @@ extern "C" size_t ldx_attention_workspace_bytes(const ldx_attention_args* a) {
 
 extern "C" int ldx_attention(const ldx_attention_args* a, void* stream) {
   if (a && a->dtype == LDX_DTYPE_BF16) return ldx::bf16_path::attention_entry(a, stream);
+  if (a && a->dtype == LDX_DTYPE_F32) return ldx::attention_f32(a, stream);
   if (a && a->dtype != LDX_DTYPE_F16)
-    return ldx::fail("attention: dtype %d is not LDX_DTYPE_F16 or LDX_DTYPE_BF16", a->dtype);
+    return ldx::fail("attention: dtype %d is not LDX_DTYPE_F16, LDX_DTYPE_BF16 or LDX_DTYPE_F32", a->dtype);
   return ldx::f16_path::attention_entry(a, stream);
 }
 #endif

@@ -49,7 +49,9 @@ struct ConvParams {
   int NKC;                 // 16-channel K fragments of the packed weight
   int NOB;                 // 32-row output blocks of the packed weight
   int split, cps;          // split-K: channel-chunk ranges of cps chunks each
-  float* part;             // split > 1: fp32 partial sums [split][B * output voxels][O]
+  float* part;             // split > 1 or raw: fp32 partial sums [split][B * output voxels][O]
+  int raw;                 // 1: the epilogue leaves the raw fp32 sums in part (plane sidx) even
+                           // unsplit -- the products of the exact fp32 mode, finished elsewhere
   const E* x0; int64_t x0p;
   const E* x1; int64_t x1p;
   const E* w;
@@ -274,7 +276,8 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
   const int o = ec.o, nch = ec.nch;
   const bool vec8 = ec.vec8;
   const int ovol = p.OD * p.OH * p.OW;
-  const bool pref_res = p.res && vec8 && p.split == 1;
+  const bool partial = p.split > 1 || p.raw;
+  const bool pref_res = p.res && vec8 && !partial;
   // One copy of the store loop per activation: no per-element branch on it.
   auto finish = [&](auto act_c) {
   constexpr int ACT = decltype(act_c)::value;
@@ -328,7 +331,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
     for (int i = 0; i < NI; i++) {
       if (!ok[i]) continue;
       const float r8[8] = {lo[i][0], lo[i][1], lo[i][2], lo[i][3], hi[i][0], hi[i][1], hi[i][2], hi[i][3]};
-      if (p.split > 1) {
+      if (partial) {
         // Raw fp32 sums of this channel range; the reduce kernel finishes the epilogue.
         float* prow = p.part + ((int64_t)sidx * p.B * ovol + ov[i]) * p.O + o;
         if (vec8) {
@@ -361,7 +364,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
     // GroupNorm partial moments of the stored values (16-byte epilogue only; the host
     // admits stats with O a multiple of 8 and aligned rows): block schunk + fv of batch
     // item b; lanes g, g + G8, ... hold the same 8 channels.
-    if (p.stats && schunk >= 0 && p.split == 1) {
+    if (p.stats && schunk >= 0 && !partial) {
       bool okv[NI];
 #pragma unroll
       for (int i = 0; i < NI; i++) okv[i] = ok[i] && vec8;
@@ -1494,7 +1497,7 @@ static int launch_dense(ConvParams p, hipStream_t st) {
   p.rTW = 1.0f / (float)BV; p.rTH = 1.0f;
   p.NBD = 1; p.NBH = 1; p.NBW = (NV + BV - 1) / BV;
   p.split = 1;
-  p.part = nullptr;
+  if (!p.raw) p.part = nullptr;
   const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
   if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
   const size_t lds = (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
@@ -1513,7 +1516,7 @@ static int launch_dense_ksplit(ConvParams p, hipStream_t st) {
   p.rTW = 1.0f / (float)BV; p.rTH = 1.0f;
   p.NBD = 1; p.NBH = 1; p.NBW = (NV + BV - 1) / BV;
   p.split = 1;
-  p.part = nullptr;
+  if (!p.raw) p.part = nullptr;
   const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
   if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
   const size_t lds = (size_t)(3 * FO * FV * 1024 + 32 * (FO * 32 + 4) + (LN ? 256 + 1024 : 0)) * sizeof(float);
@@ -1577,7 +1580,8 @@ static int launch_reduce(ConvParams& p, hipStream_t st, const char* what) {
 // One conv, as planned for these arguments. stats: also the GroupNorm partial moments of
 // the output (null: none). With dry, nothing is launched: *chunks receives the voxel
 // blocks per batch item the moments are kept for (0: this plan keeps none).
-static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t* chunks, void* stream) {
+static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t* chunks, void* stream,
+                      float* raw_part = nullptr) {
   ConvParams p;
   Tile t;
   size_t lds;
@@ -1587,6 +1591,33 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
   int rc = plan_conv(a, p, t, lds, vec, ws);
   if (rc != LDX_OK) return rc;
   hipStream_t st = as_stream(stream);
+  if (raw_part) {
+    // Raw fp32 sums into raw_part ([B * output voxels][O]), one pass (no split-K, no moments).
+    p.raw = 1;
+    p.part = raw_part;
+    p.split = 1;
+    p.cps = (p.C + t.CC - 1) / t.CC;
+    if (use_dense(a, vec)) return run_dense(p, st);
+    StreamParams sp;
+    if (conv3d_stream_plan(a, &sp, false) && sp.split == 1) {
+      sp.raw = 1;
+      sp.part = raw_part;
+      return conv3d_stream_launch(sp, st);
+    }
+    const int grid_z = p.B * (p.upsample ? 8 : 1);
+#define LDX_TILE(WO_, WV_, FO_, FV_, KSPL_)                                             \
+  if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_ && t.KSPL == KSPL_) \
+    return dispatch_k<WO_, WV_, FO_, FV_, KSPL_>(p, t.CC, vec, grid_z, st, lds);
+    LDX_TILE(1, 4, 1, 2, 1)
+    LDX_TILE(1, 4, 1, 1, 1)
+    LDX_TILE(1, 4, 2, 2, 1)
+    LDX_TILE(1, 4, 2, 1, 1)
+    LDX_TILE(2, 2, 2, 2, 1)
+    LDX_TILE(2, 2, 1, 1, 1)
+    LDX_TILE(1, 4, 2, 2, 2)
+#undef LDX_TILE
+    return fail("conv3d: no kernel for tile");
+  }
   const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
   // Moments need the 16-byte epilogue; the split-K reduce keeps them for O <= 512.
   const bool can_stats = p.O % 8 == 0 && p.ep_vec;
@@ -1649,6 +1680,13 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
   return launch_reduce(p, st, "conv3d: split reduce");
 }
 
+// The conv's raw fp32 sums (no bias, shift, scale, residual, rounding or activation) into
+// part [batch * output voxels][out_c]: the product pass of the exact fp32 mode.
+int conv3d_raw(const ldx_conv3d_args* a, float* part, void* stream) {
+  if (!part) return fail("conv3d (raw): null partial buffer");
+  return conv3d_run(a, nullptr, false, nullptr, stream, part);
+}
+
 int conv3d_entry(const ldx_conv3d_args* a, void* stream) {
   return conv3d_run(a, nullptr, false, nullptr, stream);
 }
@@ -1701,22 +1739,29 @@ int64_t conv3d_stats_chunks(const ldx_conv3d_args* a);
 int conv3d_stats(const ldx_conv3d_args* a, float* stats, void* stream);
 int dense_ln(const ldx_conv3d_args* a, const float* gamma, const float* beta, float eps, void* stream);
 }  // namespace bf16_path
+// exact.hip: the FP32 (split-FP16) conv.
+size_t conv3d_exact_workspace_bytes(const ldx_conv3d_args* a);
+int conv3d_exact(const ldx_conv3d_args* a, void* stream);
 }  // namespace ldx
 
 static bool conv_is_bf16(const ldx_conv3d_args* a) { return a && a->dtype == LDX_DTYPE_BF16; }
-static int conv_dtype_ok(const ldx_conv3d_args* a) {
-  if (a && a->dtype != LDX_DTYPE_F16 && a->dtype != LDX_DTYPE_BF16)
-    return ldx::fail("conv3d: dtype %d is not LDX_DTYPE_F16 or LDX_DTYPE_BF16", a->dtype);
+static bool conv_is_f32(const ldx_conv3d_args* a) { return a && a->dtype == LDX_DTYPE_F32; }
+static int conv_dtype_ok(const ldx_conv3d_args* a, bool f32_ok = false) {
+  if (a && a->dtype != LDX_DTYPE_F16 && a->dtype != LDX_DTYPE_BF16 && !(f32_ok && a->dtype == LDX_DTYPE_F32))
+    return ldx::fail("conv3d: dtype %d is not %s", a->dtype,
+                     f32_ok ? "LDX_DTYPE_F16, LDX_DTYPE_BF16 or LDX_DTYPE_F32" : "LDX_DTYPE_F16 or LDX_DTYPE_BF16");
   return LDX_OK;
 }
 
 extern "C" size_t ldx_conv3d_workspace_bytes(const ldx_conv3d_args* a) {
-  if (conv_dtype_ok(a) != LDX_OK) return 0;
+  if (conv_dtype_ok(a, true) != LDX_OK) return 0;
+  if (conv_is_f32(a)) return ldx::conv3d_exact_workspace_bytes(a);
   return conv_is_bf16(a) ? ldx::bf16_path::conv3d_workspace_bytes(a) : ldx::f16_path::conv3d_workspace_bytes(a);
 }
 
 extern "C" int ldx_conv3d(const ldx_conv3d_args* a, void* stream) {
-  if (int rc = conv_dtype_ok(a)) return rc;
+  if (int rc = conv_dtype_ok(a, true)) return rc;
+  if (conv_is_f32(a)) return ldx::conv3d_exact(a, stream);
   return conv_is_bf16(a) ? ldx::bf16_path::conv3d_entry(a, stream) : ldx::f16_path::conv3d_entry(a, stream);
 }
 

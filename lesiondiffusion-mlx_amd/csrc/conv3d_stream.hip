@@ -394,18 +394,19 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // The epilogue operands of these rows -- bias (+ per-batch-item bias), fp16 shift and
   // residual -- requested before the partial rows are written, which hides their latency
   // (and none of these loads delays the prologue's DMA).
+  const bool partial = p.split > 1 || p.raw;
   f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
   E8 sv = {};
   E8 res[4];
-  if (p.bias && p.split == 1) {
+  if (p.bias && !partial) {
     const float* bias = p.bias + (p.bias_batched ? (int64_t)b * p.O : 0) + o8;
     bv0 = *reinterpret_cast<const f32x4*>(bias);
     bv1 = *reinterpret_cast<const f32x4*>(bias + 4);
   }
-  if (p.shift && p.split == 1) sv = *reinterpret_cast<const E8*>(p.shift + (int64_t)b * p.shiftp + o8);
+  if (p.shift && !partial) sv = *reinterpret_cast<const E8*>(p.shift + (int64_t)b * p.shiftp + o8);
 #pragma unroll
   for (int i = 0; i < 4; i++)
-    res[i] = p.res && p.split == 1 && okr[i] ? *reinterpret_cast<const E8*>(p.res + ovr[i] * p.resp + o8)
+    res[i] = p.res && !partial && okr[i] ? *reinterpret_cast<const E8*>(p.res + ovr[i] * p.resp + o8)
                                              : (E8){};
   // Both K-groups leave their partial sums as fp32 rows, [w4][fv][group][voxel][channel]
   // (rows padded to RP floats: 16-byte writes free of bank conflicts).
@@ -431,7 +432,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     const float* r1 = rowp(kg, 1) + ro;
     const f32x4 s0 = *reinterpret_cast<const f32x4*>(r0) + *reinterpret_cast<const f32x4*>(r1);
     const f32x4 s1 = *reinterpret_cast<const f32x4*>(r0 + 4) + *reinterpret_cast<const f32x4*>(r1 + 4);
-    if (p.split > 1) {
+    if (partial) {
       if (okr[i]) {
         float* prow = p.part + ((int64_t)sk * p.B * vol + ovr[i]) * p.O + o8;
         *reinterpret_cast<f32x4*>(prow) = s0;
@@ -451,7 +452,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // 32 voxels x 32 channel pairs (lanes l, l + 8, ... hold the same 8 channels) into LDS
   // past the epilogue rows, then thread pp < BO / 2 merges pair pp over the waves of its
   // 64-channel half in a fixed order (K-group, then voxel block).
-  if (p.stats && p.split == 1) {
+  if (p.stats && !partial) {
     float* mst = reinterpret_cast<float*>(smem + S::EPI);   // [8 waves][32 pairs][3]
     pair_moments<4, 8>(outv, okr, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
     __syncthreads();

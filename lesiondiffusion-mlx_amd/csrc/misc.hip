@@ -124,52 +124,6 @@ __global__ void pack_upsample_kernel(const T* __restrict__ w, int O, int C, T* _
 // (count, mean, M2) partials; per-thread sums over a few voxels, converted to
 // (n, mean, M2) and merged (Chan et al.) in a fixed order, so results are
 // deterministic run to run.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
-}
-template <int CTRL>
-__device__ __forceinline__ Moments merge_dpp(Moments m) {
-  return merge(m, Moments{dpp_f<CTRL>(m.n), dpp_f<CTRL>(m.mean), dpp_f<CTRL>(m.m2)});
-}
-// Lane l merges its moments with those of the lane one row (permlane16) or one half
-// (permlane32) away: each swap of v with itself gives a lane its own value and its partner's.
-__device__ __forceinline__ Moments merge_swap16(Moments m) {
-  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_int(m.n), __float_as_int(m.n), false, false);
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_int(m.mean), __float_as_int(m.mean), false, false);
-  const auto c = __builtin_amdgcn_permlane16_swap(__float_as_int(m.m2), __float_as_int(m.m2), false, false);
-  return merge(Moments{__int_as_float(a[0]), __int_as_float(b[0]), __int_as_float(c[0])},
-               Moments{__int_as_float(a[1]), __int_as_float(b[1]), __int_as_float(c[1])});
-}
-__device__ __forceinline__ Moments merge_swap32(Moments m) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_int(m.n), __float_as_int(m.n), false, false);
-  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_int(m.mean), __float_as_int(m.mean), false, false);
-  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_int(m.m2), __float_as_int(m.m2), false, false);
-  return merge(Moments{__int_as_float(a[0]), __int_as_float(b[0]), __int_as_float(c[0])},
-               Moments{__int_as_float(a[1]), __int_as_float(b[1]), __int_as_float(c[1])});
-}
-
-// Merge of a workgroup's 256 per-thread moments in a fixed order: in each wave, lane l
-// merges with the lanes 8, 4, 2, 1 places round its 16-lane row (DPP row rotations), then
-// across rows and halves (v_permlane16/32_swap); lane 0 holds the wave's total. Then the
-// four waves' totals in wave order through LDS (red: 12 floats). Every thread returns the
-// same total; results repeat bit for bit.
-__device__ __forceinline__ Moments block_merge256(Moments m, float* red) {
-  m = merge_dpp<0x128>(m);   // row_ror:8
-  m = merge_dpp<0x124>(m);   // row_ror:4
-  m = merge_dpp<0x122>(m);   // row_ror:2
-  m = merge_dpp<0x121>(m);   // row_ror:1
-  m = merge_swap16(m);
-  m = merge_swap32(m);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  if (lane == 0) { red[w * 3] = m.n; red[w * 3 + 1] = m.mean; red[w * 3 + 2] = m.m2; }
-  __syncthreads();
-  Moments r = {red[0], red[1], red[2]};
-#pragma unroll
-  for (int i = 1; i < 4; i++) r = merge(r, Moments{red[3 * i], red[3 * i + 1], red[3 * i + 2]});
-  return r;
-}
-
 template <int V>
 __global__ __launch_bounds__(256) void gn_partial_kernel(
     const f16* __restrict__ x0, int64_t p0, int C0, const f16* __restrict__ x1, int64_t p1,

@@ -26,7 +26,7 @@ UPSAMPLE_CONV = re.compile(r"(?:^output_blocks\.\d+\.\d+|\.upsample)\.conv$")
 
 def to_device_weights(weights: Mapping[str, object], device: torch.device,
                       dtype: torch.dtype = torch.float16) -> dict[str, torch.Tensor]:
-    """Host arrays / tensors -> device tensors of ``dtype`` (the fp16 network)."""
+    """Host arrays / tensors -> device tensors of ``dtype`` (the network's type)."""
     out: dict[str, torch.Tensor] = {}
     for k, v in weights.items():
         t = torch.as_tensor(np.asarray(v) if not isinstance(v, torch.Tensor) else v)
@@ -40,11 +40,15 @@ def groups_for(channels: int) -> int:
 
 
 class SourceLayers:
-    """Packed, source-keyed conv / dense / norm layers on one device."""
+    """Packed, source-keyed conv / dense / norm layers on one device. ``dtype`` is the
+    network's activation and weight type: fp16 (the conditioned networks), bf16, or fp32
+    (the FP32 networks -- LMNet, the FP32 VQ decode -- on the exact split-fp16 mode)."""
 
-    def __init__(self, weights: Mapping[str, torch.Tensor], *, device: torch.device | str = "cuda"):
+    def __init__(self, weights: Mapping[str, torch.Tensor], *, device: torch.device | str = "cuda",
+                 dtype: torch.dtype = torch.float16):
         self.device = torch.device(device)
-        self.weights = to_device_weights(weights, self.device)
+        self.dtype = dtype
+        self.weights = to_device_weights(weights, self.device, dtype)
         self.packed: dict[str, ops.PackedWeight] = {}
         self.bias32: dict[str, torch.Tensor] = {}
         self.vec32: dict[str, torch.Tensor] = {}
@@ -93,7 +97,7 @@ class SourceLayers:
         allows (a multiple of 16, at most 512 channels), else as its own kernel."""
         if ln is not None:
             c = int(x.shape[-1])
-            if affine is None and c % 16 == 0 and c <= 512:
+            if affine is None and c % 16 == 0 and c <= 512 and x.dtype != torch.float32:
                 return ops.dense(x, self.packed[key], self.bias32.get(key), residual=residual, act=act,
                                  ln=(self.vec32[ln + ".weight"], self.vec32[ln + ".bias"], ln_eps))
             x = self.layer_norm(x, ln, ln_eps)

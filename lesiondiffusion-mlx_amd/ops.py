@@ -62,8 +62,10 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p | None:
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
-# Element types of the conv / attention kernels (the C ABI's LDX_DTYPE_*).
+# Element types of the conv / attention kernels (the C ABI's LDX_DTYPE_*): fp16 and bf16, and
+# fp32 for the FP32 networks (the exact split-fp16 mode).
 ELEM_DTYPES = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16}
+ALL_DTYPES = {**ELEM_DTYPES, torch.float32: _lib.DTYPE_F32}
 
 
 def _require_cuda(t: torch.Tensor, name: str, dtype: torch.dtype | tuple | None = torch.float16) -> None:
@@ -125,13 +127,17 @@ class PackedWeight:
     in_channels: int
     ksize: int
     upsample: bool = False
+    # FP32 weight in the exact mode's stacked split (2 O x 2 C fp16 rows; an upsample conv
+    # keeps its unfolded 3x3x3 taps and runs on the upsampled grid).
+    exact: bool = False
 
 
 def pack_weight(weight: torch.Tensor) -> PackedWeight:
     """Pack a Torch-layout ``(O, C, K, K, K)`` (K = 1 or 3) or dense ``(O, C)`` fp16 or
     bf16 weight (the reference's ``pack_weight``, _nax_conv.py:350-364, in this library's
-    layout); the packed tensor keeps the weight's dtype."""
-    _require_cuda(weight, "weight", tuple(ELEM_DTYPES))
+    layout); the packed tensor keeps the weight's dtype. An fp32 weight is packed for the
+    exact mode (its hi / lo fp16 split, _nax_conv.py:343-364)."""
+    _require_cuda(weight, "weight", tuple(ALL_DTYPES))
     if weight.dim() == 2:
         weight = weight.reshape(*weight.shape, 1, 1, 1)
     if weight.dim() != 5 or weight.shape[2] != weight.shape[3] or weight.shape[3] != weight.shape[4] \
@@ -139,19 +145,31 @@ def pack_weight(weight: torch.Tensor) -> PackedWeight:
         raise ValueError(f"weight must be (O, C, K, K, K) with K in (1, 3), got {tuple(weight.shape)}")
     o, c, k = int(weight.shape[0]), int(weight.shape[1]), int(weight.shape[2])
     w = weight.contiguous()
+    if w.dtype == torch.float32:
+        return _pack_exact(w, o, c, k, False)
     out = torch.empty(lib.ldx_packed_weight_elems(o, c, k, 0), dtype=w.dtype, device=weight.device)
     check(lib.ldx_pack_weight(_ptr(w), o, c, k, _ptr(out), _stream()), "pack_weight")
     return PackedWeight(out, o, c, k, False)
 
 
+def _pack_exact(w: torch.Tensor, o: int, c: int, k: int, upsample: bool) -> PackedWeight:
+    out = torch.empty(lib.ldx_packed_weight_elems(2 * o, 2 * c, k, 0), dtype=torch.float16, device=w.device)
+    check(lib.ldx_pack_weight_exact(_ptr(w), o, c, k, _ptr(out), _stream()), "pack_weight_exact")
+    return PackedWeight(out, o, c, k, upsample, exact=True)
+
+
 def pack_upsample_weight(weight: torch.Tensor) -> PackedWeight:
     """Fold a ``(O, C, 3, 3, 3)`` fp16 weight into 8 parity 2x2x2 filters for a conv of a
-    nearest 2x upsampling (_nax_conv.py:367-405), in the weight's dtype (fp16 or bf16)."""
-    _require_cuda(weight, "weight", tuple(ELEM_DTYPES))
+    nearest 2x upsampling (_nax_conv.py:367-405), in the weight's dtype (fp16 or bf16). An
+    fp32 weight keeps its 3x3x3 taps, split for the exact mode (the conv runs on the
+    upsampled grid)."""
+    _require_cuda(weight, "weight", tuple(ALL_DTYPES))
     if weight.dim() != 5 or tuple(weight.shape[2:]) != (3, 3, 3):
         raise ValueError(f"weight must be (O, C, 3, 3, 3), got {tuple(weight.shape)}")
     o, c = int(weight.shape[0]), int(weight.shape[1])
     w = weight.contiguous()
+    if w.dtype == torch.float32:
+        return _pack_exact(w, o, c, 3, True)
     out = torch.empty(lib.ldx_packed_weight_elems(o, c, 3, 1), dtype=w.dtype, device=weight.device)
     check(lib.ldx_pack_upsample_weight(_ptr(w), o, c, ELEM_DTYPES[w.dtype], _ptr(out), _stream()),
           "pack_upsample_weight")
@@ -209,15 +227,21 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     ``group_norm_affine`` of the returned tensor then merges them instead of reading it.
 
     Element type: fp16 or bf16 (``x``'s dtype; ``x1``, the packed weight, ``shift``,
-    ``residual`` and ``out`` must share it; bias and affine are fp32 either way).
+    ``residual`` and ``out`` must share it; bias and affine are fp32 either way), or fp32:
+    the exact split-fp16 mode of the FP32 networks (a weight packed from fp32; no moments,
+    no fused LayerNorm).
 
     Returns NDHWC ``(B, D', H', W', O)`` in ``x``'s dtype (written into ``out`` when given,
     which may be a channel slice of a wider tensor).
     """
-    _require_cuda(x, "x", tuple(ELEM_DTYPES))
+    _require_cuda(x, "x", tuple(ALL_DTYPES))
     et = x.dtype
-    if packed.data.dtype != et:
-        raise ValueError(f"packed weight is {packed.data.dtype} but x is {et}")
+    exact = et == torch.float32
+    if packed.exact != exact or (not exact and packed.data.dtype != et):
+        raise ValueError(f"packed weight is {'an fp32 (exact) packing' if packed.exact else packed.data.dtype} "
+                         f"but x is {et}")
+    if exact and (ln is not None or moments == "always"):
+        raise ValueError("the fp32 mode has no fused LayerNorm and keeps no moments")
     xp = voxel_pitch(x, "x")
     b, d, h, w, c0 = (int(s) for s in x.shape)
     c1, x1p = 0, 0
@@ -271,7 +295,7 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     a.residual, a.residual_pitch = (residual.data_ptr() if residual is not None else None), resp
     a.output_scale = float(output_scale)
     a.act = {None: ACT_NONE, "gelu": ACT_GELU, "silu": ACT_SILU}[act]
-    a.dtype = ELEM_DTYPES[et]
+    a.dtype = ALL_DTYPES[et]
     if shift is not None:
         _same_elem(shift, "shift", et)
         if shift.dim() != 2 or tuple(shift.shape) != (b, o) or shift.stride(1) != 1:
@@ -307,6 +331,10 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
     # merges the blocks, which there costs more (90 us) than the two-pass GroupNorm over
     # the tensor (measured on MI355X, config 4: caps of 2048 / 4096 / 16384 blocks gave
     # 19.67 / 19.70 / 19.59 ms).
+    if exact:
+        check(lib.ldx_conv3d(ctypes.byref(a), _stream()), "conv3d (fp32)")
+        _set_moments(out, None)
+        return out
     want = moments == "always" or (moments is True and not ws_bytes)
     chunks = lib.ldx_conv3d_stats_chunks(ctypes.byref(a)) if want else 0
     if moments != "always" and chunks > MOMENTS_MAX_BLOCKS:
@@ -391,12 +419,12 @@ def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, 
     """Per-(b, c) ``(scale, offset)`` fp32 ``(B, C, 2)`` of GroupNorm over NDHWC ``x``
     (optionally ``concat([x, x1])``), ``scale = gamma * rsqrt(var + eps)``, ``offset =
     beta - scale * mean`` (medmlx_core group_norm_affine; mlx_model.py:328-335)."""
-    _require_cuda(x, "x")
+    _require_cuda(x, "x", (torch.float16, torch.float32))
     xp = voxel_pitch(x, "x")
     b, d, h, w, c0 = (int(s) for s in x.shape)
     c1, x1p = 0, 0
     if x1 is not None:
-        _require_cuda(x1, "x1")
+        _require_cuda(x1, "x1", x.dtype)
         x1p = voxel_pitch(x1, "x1")
         c1 = int(x1.shape[4])
     c = c0 + c1
@@ -404,6 +432,11 @@ def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, 
         raise ValueError(f"groups {groups} must divide channels {c}")
     g32 = gamma.to(torch.float32).contiguous()
     b32 = beta.to(torch.float32).contiguous()
+    if x.dtype == torch.float32:
+        out = torch.empty((b, c, 2), dtype=torch.float32, device=x.device)
+        check(lib.ldx_group_norm_affine_f32(_ptr(x), xp, c0, _ptr(x1), x1p, c1, b, d * h * w, groups, _ptr(g32),
+                                            _ptr(b32), float(eps), _ptr(out), _stream()), "group_norm_affine_f32")
+        return out
     m0, m1 = moments_of(x), moments_of(x1)
     if m0 is not None and (x1 is None or m1 is not None) and (c // groups) % 2 == 0 and c0 % 2 == 0 \
             and c1 % 2 == 0:
@@ -425,19 +458,21 @@ def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, 
 
 def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5,
                out: torch.Tensor | None = None) -> torch.Tensor:
-    """LayerNorm over the last axis of fp16 ``x`` (mx.fast.layer_norm, mlx_model.py:360-367)."""
-    _require_cuda(x, "x")
+    """LayerNorm over the last axis of fp16 or fp32 ``x`` (mx.fast.layer_norm,
+    mlx_model.py:360-367)."""
+    _require_cuda(x, "x", (torch.float16, torch.float32))
     f = int(x.shape[-1])
     x2 = x.reshape(-1, f)
     if x2.stride(-1) != 1:
         raise ValueError("layer_norm: features must be contiguous")
     if out is None:
-        out = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+        out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    _require_cuda(out, "out", x.dtype)
     o2 = out.reshape(-1, f)
-    check(lib.ldx_layer_norm(_ptr(x2), x2.stride(0), x2.shape[0], f,
-                             _ptr(gamma.to(torch.float32).contiguous()),
-                             _ptr(beta.to(torch.float32).contiguous()), float(eps),
-                             _ptr(o2), o2.stride(0), _stream()), "layer_norm")
+    fn = lib.ldx_layer_norm_f32 if x.dtype == torch.float32 else lib.ldx_layer_norm
+    check(fn(_ptr(x2), x2.stride(0), x2.shape[0], f, _ptr(gamma.to(torch.float32).contiguous()),
+             _ptr(beta.to(torch.float32).contiguous()), float(eps), _ptr(o2), o2.stride(0), _stream()),
+          "layer_norm")
     _wrote(out)
     return out
 
@@ -456,7 +491,7 @@ def _attn_args(q4: torch.Tensor, k4: torch.Tensor, v4: torch.Tensor, o4: torch.T
         setattr(a, name, t.data_ptr())
         getattr(a, name + "_stride")[:] = [t.stride(0), t.stride(1), t.stride(2)]
     a.scale = float(scale)
-    a.dtype = ELEM_DTYPES[q4.dtype]
+    a.dtype = ALL_DTYPES[q4.dtype]
     a.mask = None
     if mask is not None:
         a.mask = mask.data_ptr()
@@ -489,8 +524,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float,
     of ``mx.fast.scaled_dot_product_attention`` (mlx_model.py:485-487, 860-862). ``mask``
     is additive (``-inf`` removes a key) or boolean (``True`` keeps a key), broadcast to
     ``(B, H, L, LK)``. fp16 or bf16 (all three alike; the probabilities are rounded to
-    that type for the P V product). Returns ``(B, H, L, D)``."""
-    _require_cuda(q, "q", tuple(ELEM_DTYPES))
+    that type for the P V product), or fp32 (head widths 16 / 32 / 64, no mask; FP32
+    throughout). Returns ``(B, H, L, D)``."""
+    _require_cuda(q, "q", tuple(ALL_DTYPES))
     for name, t in (("q", q), ("k", k), ("v", v)):
         _same_elem(t, name, q.dtype)
         if t.dim() != 4:
@@ -513,8 +549,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
     """Multi-head attention on head-interleaved projections ``(B, L, heads * d)``
     (head ``h`` = columns ``h*d .. h*d+d-1``), returning that layout
     (flash_attention, _attention.py:331-351). Key length may differ from query length.
-    fp16 or bf16."""
-    _require_cuda(q, "q", tuple(ELEM_DTYPES))
+    fp16, bf16 or fp32 (as ``attention``)."""
+    _require_cuda(q, "q", tuple(ALL_DTYPES))
     for name, t in (("q", q), ("k", k), ("v", v)):
         _same_elem(t, name, q.dtype)
         if t.dim() != 3:
@@ -542,13 +578,16 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, heads:
 
 # ---------------------------------------------------------------- small ops
 
-def timestep_embedding(timesteps: torch.Tensor, channels: int) -> torch.Tensor:
-    """fp16 ``[cos(t f), sin(t f)]`` (mlx_model.py:609-612) for int32 ``timesteps``."""
+def timestep_embedding(timesteps: torch.Tensor, channels: int, dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """``[cos(t f), sin(t f)]`` (mlx_model.py:609-612) for int32 ``timesteps``, fp16 (computed
+    in fp32, rounded once) or fp32."""
     _require_cuda(timesteps, "timesteps", torch.int32)
+    if dtype not in (torch.float16, torch.float32):
+        raise ValueError(f"timestep features are fp16 or fp32, not {dtype}")
     t = timesteps.contiguous()
-    out = torch.empty((t.shape[0], channels), dtype=torch.float16, device=t.device)
-    check(lib.ldx_timestep_embedding(_ptr(t), t.shape[0], channels, _ptr(out), _stream()),
-          "timestep_embedding")
+    out = torch.empty((t.shape[0], channels), dtype=dtype, device=t.device)
+    fn = lib.ldx_timestep_embedding_f32 if dtype == torch.float32 else lib.ldx_timestep_embedding
+    check(fn(_ptr(t), t.shape[0], channels, _ptr(out), _stream()), "timestep_embedding")
     return out
 
 

@@ -47,8 +47,9 @@ class LdmUnet(SourceLayers):
     """Noise-prediction UNet. ``__call__`` takes and returns channels-first tensors like
     the reference (mlx_model.py:554-568); ``forward`` works on NDHWC."""
 
-    def __init__(self, weights: Mapping[str, object], config: UnetConfig, *, device="cuda"):
-        super().__init__(weights, device=device)
+    def __init__(self, weights: Mapping[str, object], config: UnetConfig, *, device="cuda",
+                 dtype: torch.dtype = torch.float16):
+        super().__init__(weights, device=device, dtype=dtype)
         self.config = config
         # All ResBlock time projections read silu(emb): one GEMM.
         emb_keys = sorted(k[: -len(".weight")] for k in self.weights if k.endswith(".emb_layers.1.weight"))
@@ -72,7 +73,7 @@ class LdmUnet(SourceLayers):
         """``emb_layers.1(silu(time_embed(t)))`` of every ResBlock, ``(B, sum O)``
         (mlx_model.py:609-614, 434)."""
         mc = self.config.model_channels
-        t = ops.timestep_embedding(timesteps.to(torch.int32), mc)
+        t = ops.timestep_embedding(timesteps.to(torch.int32), mc, self.dtype)
         h = self.dense(t, "time_embed.0", act="silu")
         semb = self.dense(h, "time_embed.2", act="silu")
         return self.dense(semb, "_emb_layers") if self.emb_slices else None
@@ -132,7 +133,7 @@ class LdmUnet(SourceLayers):
         (prepare_denoiser, mlx_model.py:570-591)."""
         if context is None or self.config.skip_context:
             return None
-        ctx = context.to(device=self.device, dtype=torch.float16).contiguous()
+        ctx = context.to(device=self.device, dtype=self.dtype).contiguous()
         proj = self.dense(ctx, "context_linear_projection")
         out: dict[str, tuple[torch.Tensor, torch.Tensor]] = {}
         for k in self.packed:
@@ -200,7 +201,7 @@ class LdmUnet(SourceLayers):
 
     def __call__(self, x: torch.Tensor, timesteps: torch.Tensor, context: torch.Tensor | None) -> torch.Tensor:
         """Channels-first in and out, as the reference's ``LdmUnet.__call__``."""
-        xs = ncdhw_to_ndhwc(x.to(device=self.device, dtype=torch.float16))
+        xs = ncdhw_to_ndhwc(x.to(device=self.device, dtype=self.dtype))
         t = timesteps.to(device=self.device, dtype=torch.int32)
         return ndhwc_to_ncdhw(self.forward(xs, t, self.project_context(context)))
 

@@ -27,9 +27,11 @@ class VqDecoder(SourceLayers):
 
     def __init__(self, weights: Mapping[str, object], *, levels: tuple[int, ...] = (2, 1, 0),
                  upsample_levels: tuple[int, ...] = (1,), blocks: int = 2, groups: int = 16,
-                 eps: float = 1e-6, device="cuda"):
+                 eps: float = 1e-6, device="cuda", dtype: torch.dtype = torch.float16):
         codebook = weights.get(self.CODEBOOK)
-        super().__init__({k: v for k, v in weights.items() if k != self.CODEBOOK}, device=device)
+        super().__init__({k: v for k, v in weights.items() if k != self.CODEBOOK}, device=device, dtype=dtype)
+        if dtype == torch.float32:
+            self.QUANTIZE_DTYPE = torch.float32   # the FP32 decode quantizes in fp32 too
         self.levels, self.upsample_levels, self.blocks = levels, upsample_levels, blocks
         self.groups, self.eps = groups, eps
         self.set_codebook(codebook)
@@ -116,7 +118,7 @@ class VqDecoder(SourceLayers):
         mlx_model.py:805-819)."""
         if quantize:
             z = self.quantize(z)
-        x = self.conv(z.to(torch.float16), "post_quant_conv")
+        x = self.conv(z.to(self.dtype), "post_quant_conv")
         x = self.conv(x, "decoder.conv_in", moments=True)
         x = self.residual(x, "decoder.mid.block_1")
         if "decoder.mid.attn_1.qkv" in self.packed:
@@ -135,7 +137,7 @@ class VqDecoder(SourceLayers):
         """Channels-first latent in, channels-first volume out."""
         zz = ncdhw_to_ndhwc(z.to(device=self.device))
         if not quantize:
-            zz = zz.to(torch.float16)
+            zz = zz.to(self.dtype)
         return ndhwc_to_ncdhw(self.decode(zz, quantize=quantize))
 
 

@@ -71,7 +71,7 @@ def _conv_args(lib, **kw):
     {"ksize": 5}, {"stride": 3}, {"batch": 0}, {"in_d": 0}, {"c0": 0}, {"out_c": 0},
     {"ksize": 1, "stride": 2}, {"upsample": 1, "stride": 2}, {"x0": None}, {"weight": None},
     {"c1": 8}, {"x0_pitch": 4}, {"y_pitch": 4}, {"act": 7}, {"residual": 16, "residual_pitch": 2},
-    {"dtype": 1}, {"dtype": 7},
+    {"dtype": 3}, {"dtype": 7},
 ])
 def test_conv3d_rejects_bad_arguments_before_launch(pkg, bad) -> None:
     lib = pkg._lib
@@ -95,7 +95,7 @@ def test_attention_rejects_bad_arguments_before_launch(pkg) -> None:
     a.kv_len = 0
     assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
     a.kv_len = 8
-    a.dtype = 1   # fp32 is not an attention element type
+    a.dtype = 5   # not an element type
     assert lib.lib.ldx_attention(ctypes.byref(a), None) == lib.LDX_EINVAL
     assert "dtype" in lib.last_error()
 
