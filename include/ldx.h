@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (5); bumped on any change to the structs below. */
+/* ABI version (6); bumped on any change to the structs below. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -324,6 +324,51 @@ int ldx_vq_squared_norms4(const void* x, int64_t n, int32_t dtype, void* out, vo
 int ldx_vq_nearest4(const void* z, const void* z_norm, const void* codebook, const void* codebook_norm,
                     int64_t positions, int32_t entries, int32_t dtype, int32_t* indices,
                     void* quantized, void* stream);
+
+/* ------------------------------------------------- source-order fp16 arithmetic -------
+ * The reference's "source" arithmetic, which reproduces Torch-CPU's reduction order bit
+ * for bit (src/lesiondiffusion_mlx/_source_half.py). Tensors are fp16, addressed by
+ * (batch, channel, voxel) strides in elements -- NCDHW (voxel stride 1, the reference's
+ * layout) or channels-last -- with voxel index (z * H + y) * W + x; the arithmetic follows
+ * the logical NCDHW order either way.
+ *
+ * ldx_conv3d_source_half replaces conv3d_half (_source_half.py:19-104, 327-384):
+ *   y[n, o, v] = half( ((p0 + p1) + p2) + p3 + float(bias[o]) )
+ * over k = c * KD*KH*KW + (kd * KH + kh) * KW + kw of the zero-padded im2col column,
+ * partial k % 4 for k < K - K % 4 in increasing k, the remaining k into p0, every product
+ * of two fp16 values (exact in fp32) added in fp32. Any kernel size, stride >= 1,
+ * padding >= 0; weight (out_c, in_c, kd, kh, kw) contiguous fp16; bias fp16 or NULL.
+ * Output extents (n + 2 * padding - k) / stride + 1; a kernel larger than the padded
+ * input is rejected ("conv3d kernel exceeds the padded input").
+ *
+ * ldx_group_norm_source_half replaces group_norm_half (_source_half.py:120-300, 387-544):
+ * per (batch item, group) Welford moments of vectors of 8 values in chunks of 16 vectors,
+ * merged by the reference's binary-counter cascade (128-chunk blocks in parallel, then
+ * group-wide), the scalar tail and the four lanes last; var = max(m2 / SIZE, 0),
+ * rstd = float(1 / sqrt(double(var) + double(eps))), scale = rstd * weight[c],
+ * offset = fma(-scale, mean, bias[c]) into affine[b, c, 0..1] (fp32, required); then, if
+ * y is not NULL, y = half(float(scale * x) + offset). weight and bias are fp16 (C,). The
+ * workspace holds the chunk and block moments: ldx_group_norm_source_workspace_bytes. */
+typedef struct ldx_conv3d_source_args {
+  int32_t batch, in_c, in_d, in_h, in_w;
+  int32_t out_c, kd, kh, kw;
+  int32_t stride, padding;
+  const void* x;
+  int64_t x_batch_stride, x_channel_stride, x_voxel_stride;
+  const void* weight;
+  const void* bias;
+  void* y;
+  int64_t y_batch_stride, y_channel_stride, y_voxel_stride;
+} ldx_conv3d_source_args;
+
+int ldx_conv3d_source_half(const ldx_conv3d_source_args* args, void* stream);
+size_t ldx_group_norm_source_workspace_bytes(int32_t batch, int32_t channels, int64_t voxels, int32_t groups);
+int ldx_group_norm_source_half(const void* x, int64_t x_batch_stride, int64_t x_channel_stride,
+                               int64_t x_voxel_stride, int32_t batch, int32_t channels, int64_t voxels,
+                               int32_t groups, const void* weight, const void* bias, float eps,
+                               float* affine, void* y, int64_t y_batch_stride, int64_t y_channel_stride,
+                               int64_t y_voxel_stride, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 #ifdef __cplusplus
 }

@@ -69,6 +69,19 @@ class AttnArgs(ctypes.Structure):
     ]
 
 
+class SourceConvArgs(ctypes.Structure):
+    """Mirror of ``ldx_conv3d_source_args``."""
+
+    _fields_ = [
+        ("batch", c_i32), ("in_c", c_i32), ("in_d", c_i32), ("in_h", c_i32), ("in_w", c_i32),
+        ("out_c", c_i32), ("kd", c_i32), ("kh", c_i32), ("kw", c_i32),
+        ("stride", c_i32), ("padding", c_i32),
+        ("x", c_vp), ("x_batch_stride", c_i64), ("x_channel_stride", c_i64), ("x_voxel_stride", c_i64),
+        ("weight", c_vp), ("bias", c_vp),
+        ("y", c_vp), ("y_batch_stride", c_i64), ("y_channel_stride", c_i64), ("y_voxel_stride", c_i64),
+    ]
+
+
 # name -> (restype, argtypes); every function declared in include/ldx.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_last_error": (ctypes.c_char_p, []),
@@ -106,9 +119,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_layer_norm_f32": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),
     "ldx_timestep_embedding_f32": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_vq_nearest4": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
+    "ldx_conv3d_source_half": (c_i32, [ctypes.POINTER(SourceConvArgs), c_vp]),
+    "ldx_group_norm_source_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i32, c_i64, c_i32]),
+    "ldx_group_norm_source_half": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_vp, c_vp,
+                                           c_f32, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, ctypes.c_size_t,
+                                           c_vp]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def _load() -> ctypes.CDLL:

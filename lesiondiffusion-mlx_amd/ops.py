@@ -20,13 +20,13 @@ import torch
 from torch.autograd.graph import increment_version
 
 from . import _lib
-from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, check, lib
+from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, SourceConvArgs, check, lib
 
 __all__ = [
     "PackedWeight", "pack_weight", "pack_upsample_weight", "nax_conv3d", "conv3d", "dense",
     "group_norm_affine", "layer_norm", "attention", "flash_attention", "timestep_embedding",
     "silu", "upsample_nearest2", "resize_nearest", "output_extent", "count_flops", "squared_norms4",
-    "nearest_codebook4",
+    "nearest_codebook4", "conv3d_half", "group_norm_half",
 ]
 
 
@@ -668,3 +668,93 @@ def nearest_codebook4(z: torch.Tensor, codebook: torch.Tensor, codebook_norm: to
     if quantized is not None:
         _wrote(quantized)
     return idx
+
+
+# --------------------------------------------------------------- source-order arithmetic
+
+
+def _ncdhw_strides(x: torch.Tensor, name: str) -> tuple[int, int, int]:
+    """(batch, channel, voxel) element strides of a logical NCDHW tensor whose voxels are
+    evenly spaced: NCDHW-contiguous (voxel stride 1) or channels-last 3-D (voxel stride C)."""
+    if x.dim() != 5:
+        raise ValueError(f"{name} must be NCDHW (B, C, D, H, W), got shape {tuple(x.shape)}")
+    _, _, d, h, w = x.shape
+    st = x.stride()
+    sv = st[4] if w > 1 else (st[3] // w if h > 1 else (st[2] // (h * w) if d > 1 else 1))
+    if (w > 1 and st[4] != sv) or (h > 1 and st[3] != w * sv) or (d > 1 and st[2] != h * w * sv):
+        raise ValueError(f"{name}: voxels must be evenly spaced (strides {st})")
+    return int(st[0]), int(st[1]), int(sv)
+
+
+def _like(x: torch.Tensor, shape: tuple[int, ...]) -> torch.Tensor:
+    """An empty fp16 tensor of ``shape`` in ``x``'s memory format (NCDHW or channels-last)."""
+    fmt = (torch.channels_last_3d if not x.is_contiguous() and x.is_contiguous(memory_format=torch.channels_last_3d)
+           else torch.contiguous_format)
+    return torch.empty(shape, dtype=torch.float16, device=x.device, memory_format=fmt)
+
+
+def conv3d_half(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, *, padding: int,
+                stride: int) -> torch.Tensor:
+    """Source-order fp16 conv3d (conv3d_half, _source_half.py:327-384): four fp32 partial
+    sums in Torch-CPU's channel-major order, bias added, one fp16 rounding -- Torch-CPU's
+    result bit for bit. ``x`` is NCDHW ``(B, C, D, H, W)`` (contiguous or channels-last),
+    ``weight`` ``(O, C, KD, KH, KW)``, ``bias`` ``(O,)`` or None, all fp16; returns
+    ``(B, O, OD, OH, OW)`` in ``x``'s memory format."""
+    _require_cuda(x, "x")
+    _require_cuda(weight, "weight")
+    xs = _ncdhw_strides(x, "conv3d input")
+    if weight.dim() != 5:
+        raise ValueError(f"weight must be (O, C, KD, KH, KW), got {tuple(weight.shape)}")
+    b, c, d, h, w = x.shape
+    o, wc, kd, kh, kw = weight.shape
+    if wc != c:
+        raise ValueError("conv3d input channels differ from source weights")
+    if bias is not None:
+        _require_cuda(bias, "bias")
+        if tuple(bias.shape) != (o,):
+            raise ValueError("conv3d bias must have one value per output channel")
+        bias = bias.contiguous()
+    ext = [(n + 2 * padding - k) // stride + 1 for n, k in zip((d, h, w), (kd, kh, kw))]
+    if min(ext) < 1:
+        raise ValueError("conv3d kernel exceeds the padded input")
+    weight = weight.contiguous()
+    y = _like(x, (b, o, *ext))
+    ys = _ncdhw_strides(y, "y")
+    a = SourceConvArgs(batch=b, in_c=c, in_d=d, in_h=h, in_w=w, out_c=o, kd=kd, kh=kh, kw=kw, stride=stride,
+                       padding=padding, x=_ptr(x), x_batch_stride=xs[0], x_channel_stride=xs[1],
+                       x_voxel_stride=xs[2], weight=_ptr(weight), bias=_ptr(bias), y=_ptr(y),
+                       y_batch_stride=ys[0], y_channel_stride=ys[1], y_voxel_stride=ys[2])
+    check(lib.ldx_conv3d_source_half(ctypes.byref(a), _stream()), "conv3d_source_half")
+    fc = count_flops.active
+    if fc is not None:
+        fc.conv += 2.0 * b * o * c * kd * kh * kw * ext[0] * ext[1] * ext[2]
+    return y
+
+
+def group_norm_half(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, *, groups: int, eps: float,
+                    return_affine: bool = False):
+    """Source-order fp16 GroupNorm (group_norm_half, _source_half.py:387-544): Torch-CPU's
+    chunked Welford cascade per group, then ``fp16(scale * x + offset)`` with the
+    per-channel fp32 affine. ``x`` is NCDHW (contiguous or channels-last) fp16, ``weight``
+    and ``bias`` fp16 ``(C,)``. Returns the normalized tensor in ``x``'s memory format, and
+    with ``return_affine`` also the fp32 ``(B, C, 2)`` (scale, offset)."""
+    _require_cuda(x, "x")
+    xs = _ncdhw_strides(x, "group_norm input")
+    b, c = x.shape[:2]
+    if groups < 1 or c % groups:
+        raise ValueError(f"group_norm channels {c} must be divisible by num_groups {groups}")
+    for t, nm in ((weight, "weight"), (bias, "bias")):
+        _require_cuda(t, nm)
+        if tuple(t.shape) != (c,):
+            raise ValueError("group_norm affine must have one value per channel")
+    weight, bias = weight.contiguous(), bias.contiguous()
+    voxels = int(x.shape[2] * x.shape[3] * x.shape[4])
+    y = _like(x, tuple(x.shape))
+    ys = _ncdhw_strides(y, "y")
+    affine = torch.empty((b, c, 2), dtype=torch.float32, device=x.device)
+    ws_bytes = lib.ldx_group_norm_source_workspace_bytes(b, c, voxels, groups)
+    ws = torch.empty(max(int(ws_bytes), 1), dtype=torch.uint8, device=x.device)
+    check(lib.ldx_group_norm_source_half(_ptr(x), xs[0], xs[1], xs[2], b, c, voxels, groups, _ptr(weight),
+                                         _ptr(bias), float(eps), _ptr(affine), _ptr(y), ys[0], ys[1], ys[2],
+                                         _ptr(ws), int(ws.numel()), _stream()), "group_norm_source_half")
+    return (y, affine) if return_affine else y

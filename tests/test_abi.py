@@ -33,7 +33,8 @@ def test_library_exports_every_declared_symbol(pkg) -> None:
 
 def test_ctypes_structs_match_c_layout(pkg, tmp_path) -> None:
     lib = pkg._lib
-    fields = {"ldx_conv3d_args": lib.ConvArgs, "ldx_attention_args": lib.AttnArgs}
+    fields = {"ldx_conv3d_args": lib.ConvArgs, "ldx_attention_args": lib.AttnArgs,
+              "ldx_conv3d_source_args": lib.SourceConvArgs}
     src = ["#include <stdio.h>", "#include <stddef.h>", '#include "ldx.h"', "int main(void) {"]
     for cname, cls in fields.items():
         src.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -115,6 +116,37 @@ def test_small_ops_reject_bad_arguments(pkg) -> None:
     assert l.ldx_upsample_nearest2(16, 2, 1, 1, 1, 1, 4, 16, 4, None) == E
     assert l.ldx_group_norm_workspace_bytes(0, 10, 8, 2) == 0
     assert l.ldx_group_norm_workspace_bytes(1, 51200, 64, 32) > 0
+
+
+@pytest.mark.parametrize("bad", [
+    {"x": None}, {"weight": None}, {"y": None}, {"batch": 0}, {"in_c": 0}, {"out_c": 0}, {"kd": 0},
+    {"stride": 0}, {"padding": -1}, {"kd": 9, "padding": 0},
+])
+def test_source_conv_rejects_bad_arguments_before_launch(pkg, bad) -> None:
+    lib = pkg._lib
+    a = lib.SourceConvArgs(batch=1, in_c=4, in_d=4, in_h=4, in_w=4, out_c=4, kd=3, kh=3, kw=3, stride=1, padding=1,
+                           x=16, x_batch_stride=256, x_channel_stride=64, x_voxel_stride=1, weight=16, y=16,
+                           y_batch_stride=256, y_channel_stride=64, y_voxel_stride=1)
+    for k, v in bad.items():
+        setattr(a, k, v)
+    assert lib.lib.ldx_conv3d_source_half(ctypes.byref(a), None) == lib.LDX_EINVAL
+    assert "conv3d" in lib.last_error()
+
+
+def test_source_group_norm_rejects_bad_arguments_before_launch(pkg) -> None:
+    l = pkg._lib.lib
+    E = pkg._lib.LDX_EINVAL
+    gn = l.ldx_group_norm_source_half
+    # channels not divisible by groups; no weight; an empty tensor; too small a workspace
+    assert gn(16, 96, 8, 1, 1, 12, 8, 5, 16, 16, 1e-6, 16, 16, 96, 8, 1, 16, 1 << 20, None) == E
+    assert gn(16, 96, 8, 1, 1, 12, 8, 4, None, 16, 1e-6, 16, 16, 96, 8, 1, 16, 1 << 20, None) == E
+    assert gn(16, 96, 8, 1, 1, 12, 0, 4, 16, 16, 1e-6, 16, 16, 96, 8, 1, 16, 1 << 20, None) == E
+    assert gn(16, 96, 8, 1, 1, 12, 8, 4, 16, 16, 1e-6, 16, 16, 96, 8, 1, 16, 4, None) == E
+    assert "workspace" in pkg._lib.last_error()
+    ws = l.ldx_group_norm_source_workspace_bytes
+    assert ws(1, 12, 8, 5) == 0 and ws(0, 12, 8, 4) == 0
+    # chunks of 16 vectors of 8: (1, 64, 51200 voxels, 32 groups) -> 800 chunks, 6 blocks
+    assert ws(1, 64, 51200, 32) == 32 * 800 * 16 * 4 + 32 * 6 * 8 * 4
 
 
 def test_ops_fail_loudly_on_cpu_tensors(pkg) -> None:
