@@ -32,6 +32,7 @@ sys.path.insert(0, str(REPO))
 METRIC = "conv3d & flash-attn TFLOP/s (% MFMA peak); ms per 3D-UNet denoise step"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3    # MI355X vector fp32 (the source-order conv runs on the VALU)
 # HBM bytes per config-1 conv launch come from the committed profile of the benched kernel:
 # rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over this script with --copy-calibration,
 # each divided by what the counter reports per byte of a plain 512 MiB device copy. The
@@ -164,6 +165,44 @@ def bench_attention(pkg, steps: int, warmup: int) -> dict:
                      "frac_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
                      "gbs": byts / (ms * 1e-3) / 1e9}
     out["_tensors"] = (q, k, v)
+    return out
+
+
+def bench_source(pkg, steps: int, warmup: int, cpu: bool) -> dict:
+    """The reference's source-order fp16 arithmetic at config-1 size: ``conv3d_half`` (Torch-CPU's
+    four-partial reduction order on the VALU, NCDHW) and ``group_norm_half`` (32 groups) on the
+    config-1 tensor. With ``cpu``, Torch-CPU's own fp16 conv3d (oneDNN off: the order these
+    kernels reproduce) on 4 of the 32 output planes, scaled to the whole conv."""
+    import torch
+    import torch.nn.functional as F
+
+    ops = pkg.ops
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(0)
+    xh = rng.standard_normal((1, 64, 32, 40, 40)).astype(np.float16)
+    wh = (rng.standard_normal((64, 64, 3, 3, 3)) / math.sqrt(27 * 64)).astype(np.float16)
+    bh = (rng.standard_normal(64) * 0.01).astype(np.float16)
+    x, w, b = (torch.from_numpy(a).to(dev) for a in (xh, wh, bh))
+    gamma = torch.ones(64, dtype=torch.float16, device=dev)
+    conv_ms = _graph_time(lambda: ops.conv3d_half(x, w, b, padding=1, stride=1), steps, warmup)
+    gn_ms = _graph_time(lambda: ops.group_norm_half(x, gamma, b, groups=32, eps=1e-5), steps, warmup)
+    flop = 2.0 * 51200 * 64 * 64 * 27
+    out = {"conv_ms": round(conv_ms, 5), "conv_tflops": round(flop / (conv_ms * 1e-3) / 1e12, 2),
+           "conv_frac_fp32_peak": round(flop / (conv_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS, 4),
+           "gn_ms": round(gn_ms, 5),
+           "gn_gbs": round(3 * 51200 * 64 * 2 / (gn_ms * 1e-3) / 1e9, 1),
+           "config": "config-1 tensor (1, 64, 32, 40, 40) NCDHW fp16; conv 3x3x3 padding 1; GroupNorm 32 groups "
+                     "(reads x twice, writes y: 3 x 6.55 MB)"}
+    if cpu:
+        threads = _cpu_threads()
+        xs, ws, bs = torch.from_numpy(xh[:, :, :4]), torch.from_numpy(wh), torch.from_numpy(bh)
+        with torch.no_grad(), torch.backends.mkldnn.flags(enabled=False):
+            t0 = time.perf_counter()
+            F.conv3d(xs, ws, bs, padding=1)
+            sec = (time.perf_counter() - t0) * 8
+        out["cpu_torch_conv_ms"] = round(sec * 1e3, 1)
+        out["cpu_sample"] = (f"Torch {torch.__version__} CPU fp16 conv3d (oneDNN off) on 4 of 32 output planes, "
+                             f"x8; {threads} threads")
     return out
 
 
@@ -532,6 +571,7 @@ def main() -> int:
             "config": "config 2: fp16, B=1, 8 heads x 64, 1600 queries; self 1600 keys, cross 77 keys "
                       "(context 77x768 projected by to_k/to_v)"},
     }
+    line["source_order"] = bench_source(pkg, args.steps, args.warmup, not args.skip_cpu)
     if not args.skip_model:
         line["unet_block_stack"] = bench_config3(pkg, max(args.steps // 5, 5))
         line["vq_decoder"] = bench_config4(pkg, 3)

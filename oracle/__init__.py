@@ -20,6 +20,8 @@ This package restates, in float64 NumPy, what the reference
                    the straight-through quantize (_vq.py:12-82, mlx_model.py:742-803).
 * ``torch_cpu`` -- the UNet and VQ decoder in torch fp32 on the CPU: ``bench.py``'s CPU
                    baseline for configs 3-5 (the same layer graphs as ``unet``).
+* ``source_order`` -- the reference's Torch-CPU-ordered fp16 conv3d and Welford GroupNorm
+                   cascade with every float32 rounding explicit (_source_half.py).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
 may import this package, and only as the checker. The product path (the HIP library
