@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol(pkg) -> None:
 def test_ctypes_structs_match_c_layout(pkg, tmp_path) -> None:
     lib = pkg._lib
     fields = {"ldx_conv3d_args": lib.ConvArgs, "ldx_attention_args": lib.AttnArgs,
-              "ldx_conv3d_source_args": lib.SourceConvArgs}
+              "ldx_conv3d_source_args": lib.SourceConvArgs, "ldx_chain_gemm": lib.ChainGemm,
+              "ldx_token_chain_args": lib.TokenChainArgs}
     src = ["#include <stdio.h>", "#include <stddef.h>", '#include "ldx.h"', "int main(void) {"]
     for cname, cls in fields.items():
         src.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
