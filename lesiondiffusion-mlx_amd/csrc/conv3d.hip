@@ -64,6 +64,7 @@ struct ConvParams {
   int ep_vec;              // 16-byte epilogue accesses: y, residual, shift, bias, partials aligned
   int nh;                  // planned halo: register slots per thread (0: generic staging loop)
   int stg_off;             // > 0: LDS offset (floats) of the epilogue staging, past the halo
+  int tps;                 // host only: > 1 asks for whole kw rows per weight stage
   int nob, nbr;            // output-channel blocks of the workgroup tile; bricks per batch item
   const float* ln_g;       // dense_ksplit with LayerNorm: per-channel gamma, beta and eps
   const float* ln_b;
@@ -405,7 +406,11 @@ constexpr int NHL = NHMAX + 4;   // loads per thread of one planned halo request
 
 // PLAN: the planned halo path (VEC only; register slots per thread fixed per workgroup);
 // otherwise the generic staging loop of load_halo.
-template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, bool PLAN, int KSPL>
+// TPS: taps per weight stage. A stage is one ring slot, one barrier and one batch of DMAs;
+// TPS = KSZ (a whole kw row per stage) takes two thirds of the barriers out of the tap loop
+// for a ring three times the size, which pays where one workgroup per CU is all the grid
+// has (the coarse UNet levels).
+template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, bool PLAN, int KSPL, int TPS>
 __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   static_assert(!PLAN || VEC, "the planned halo needs 16-byte channel groups");
   constexpr int NT = 256 * KSPL;
@@ -416,13 +421,15 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   static_assert(KSG * KSPL == KS && KSG >= 1, "K-groups must split the chunk's k-steps");
   constexpr int TAPS = KSZ * KSZ * KSZ;
   constexpr int NFRAG = (BO / 32) * KSG;      // 1 KB weight fragments per group stage
-  constexpr int WSTAGE = NFRAG * 512;         // halves per group stage
+  static_assert((KSZ * KSZ * KSZ) % TPS == 0, "a stage holds whole taps of one chunk");
+  constexpr int WSTAGE = NFRAG * 512 * TPS;   // halves per group stage
   constexpr int LW = (NFRAG + 3) / 4;         // weight DMAs per wave per stage
   constexpr int G = CC / 8;                   // 16-byte channel groups per voxel
   constexpr int VPI = NT / G;                 // halo voxels per pass of the workgroup
-  // Tap of each chunk after whose weight load the next chunk's halo is requested: the
-  // loads then have the last WPF - 1 taps of the chunk to land.
-  constexpr int TPF = TAPS - WPF;
+  constexpr int SPC = TAPS / TPS;             // stages per chunk
+  // Stage of each chunk after whose weight load the next chunk's halo is requested: the
+  // loads then have the last WPF - 1 stages of the chunk to land.
+  constexpr int TPF = SPC - WPF;
   extern __shared__ __attribute__((aligned(16))) E smem[];
   E* halo = smem + KSPL * WRING * WSTAGE;
 
@@ -472,15 +479,15 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   }
   const int sd = p.HH * p.RS, sh = p.RS;
 
-  // Weight staging: stage st = (channel chunk, tap) of this workgroup's sequence goes to
-  // ring slot st % WRING of each K-group by direct global->LDS loads, WPF stages ahead of
-  // its use. Wave w4 of group g moves the group's fragments f = w4 + 4 i ((ob, k) =
+  // Weight staging: stage st = (channel chunk, TPS taps) of this workgroup's sequence goes
+  // to ring slot st % WRING of each K-group by direct global->LDS loads, WPF stages ahead
+  // of its use. Wave w4 of group g moves the group's fragments f = w4 + 4 i ((ob, k) =
   // (f / KSG, f % KSG)): one 1 KB fragment is one 16-byte-per-lane load, already in MFMA
   // lane order. A wave with fewer real fragments repeats one (same data to the same
   // place), so every wave issues LW loads per stage and the vmcnt wait is uniform.
   const int c_begin = sidx * p.cps * CC;
   const int c_end = min(p.C, (sidx + 1) * p.cps * CC);
-  const int nst = (c_end - c_begin + CC - 1) / CC * TAPS;
+  const int nst = (c_end - c_begin + CC - 1) / CC * SPC;
   const unsigned ring_lds = lds_offset(wring);
   // This wave's fragment sources at (tap 0, chunk 0); a stage adds (tap * NKC + kc0) * 512.
   const E* wsrc[LW];
@@ -493,13 +500,17 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   // Next stage to load: (ntap, nkc); it stops advancing at the last stage.
   int ntap = 0, nkc = c_begin / 16, nleft = nst - 1;
   auto issue_stage = [&](int slot) {
-    const int64_t off = ((int64_t)ntap * p.NKC + nkc) * 512;
 #pragma unroll
-    for (int i = 0; i < LW; i++)
-      dma_b128(wsrc[i] + off, ring_lds + (unsigned)((slot * NFRAG + (w4 + 4 * i) % NFRAG) * 1024));
+    for (int j = 0; j < TPS; j++) {
+      const int64_t off = ((int64_t)(ntap + j) * p.NKC + nkc) * 512;
+#pragma unroll
+      for (int i = 0; i < LW; i++)
+        dma_b128(wsrc[i] + off, ring_lds + (unsigned)(((slot * TPS + j) * NFRAG + (w4 + 4 * i) % NFRAG) * 1024));
+    }
     if (nleft > 0) {
       nleft--;
-      if (++ntap == TAPS) { ntap = 0; nkc += KS; }
+      ntap += TPS;
+      if (ntap == TAPS) { ntap = 0; nkc += KS; }
     }
   };
 
@@ -606,7 +617,7 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   auto load_frags = [&](int set, int stage, int tap) {
     const int kd = tap / (KSZ * KSZ), kh = (tap / KSZ) % KSZ, kw = tap % KSZ;
     const int toff = kd * sd + kh * sh + kw * PITCH;
-    const E* wst = wring + (stage % WRING) * WSTAGE + lane * 8;
+    const E* wst = wring + (stage % WRING) * WSTAGE + (tap % TPS) * (NFRAG * 512) + lane * 8;
 #pragma unroll
     for (int kk = 0; kk < KSG; kk++) {
 #pragma unroll
@@ -639,9 +650,9 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
         // weight prefetch at every tap.
         vmcnt_wait<0>();
       } else if (pf) {
-        // Requested during the previous chunk's last taps; younger than them are only
-        // the weight stages of its last WPF - 1 taps.
-        vmcnt_wait<(WPF - 1) * LW>();
+        // Requested during the previous chunk's last stages; younger than them are only
+        // the weight stages of its last WPF - 1 stages.
+        vmcnt_wait<(WPF - 1) * LW * TPS>();
         __syncthreads();  // previous chunk done with the halo
       } else {
         __syncthreads();  // previous chunk done with the halo
@@ -659,20 +670,24 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
     const bool pf_next = PLAN && TPF > 0 && c0 + CC < c_end;
     load_frags(0, st, 0);
 #pragma unroll
-    for (int tap = 0; tap < TAPS; tap++, st++) {
-      // Stage st + 1 has landed once only the WPF - 2 stages after it (and, after TPF,
-      // the next chunk's halo loads) may be pending; the barrier publishes every wave's
-      // part of it and retires stage st - 1 (read into registers two taps ago), whose
-      // slot the next load reuses.
-      if (tap > TPF && pf_next) vmcnt_wait<(WPF - 2) * LW + NHL>();
-      else vmcnt_wait<(WPF - 2) * LW>();
-      __syncthreads();
-      issue_stage((st + WPF) % WRING);
-      if (tap == TPF && pf_next) halo_issue(c0 + CC);
-      if (tap + 1 < TAPS) load_frags((tap + 1) & 1, st + 1, tap + 1);
+    for (int tap = 0; tap < TAPS; tap++) {
+      const int sc = tap / TPS;   // stage of this tap within the chunk
+      if (tap % TPS == 0) {
+        // Stage st + sc + 1 has landed once only the WPF - 2 stages after it (and, after
+        // TPF, the next chunk's halo loads) may be pending; the barrier publishes every
+        // wave's part of it and retires stage st + sc - 1 (its last tap was read into
+        // registers before this stage began), whose slot the next load reuses.
+        if (sc > TPF && pf_next) vmcnt_wait<(WPF - 2) * LW * TPS + NHL>();
+        else vmcnt_wait<(WPF - 2) * LW * TPS>();
+        __syncthreads();
+        issue_stage((st + sc + WPF) % WRING);
+        if (sc == TPF && pf_next) halo_issue(c0 + CC);
+      }
+      if (tap + 1 < TAPS) load_frags((tap + 1) & 1, st + (tap + 1) / TPS, tap + 1);
       mfma_frags(tap & 1);
       if (tap + 1 < TAPS) interleave_reads_mfma<(FO + FV) * KSG, FO * FV * KSG>();
     }
+    st += SPC;
     pf = pf_next;
     c0 += CC;
   } while (c0 < c_end);
@@ -1245,13 +1260,15 @@ static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t halo_byt
   constexpr int BO = WO * FO * 32;
   constexpr int NT = 256 * KSPL, VPI = NT / (CC / 8);
   auto al16 = [](size_t n) { return (n + 15) & ~(size_t)15; };
-  // LDS: weight rings (all K-groups) and the halo; then the epilogue (K-group partial
-  // sums and the staging).
-  const size_t ring = (size_t)WRING * (BO / 32) * (CC / 16) * 1024;
-  const size_t main_bytes = ring + al16(halo_bytes);
   const int hvox = p.HD * p.HH * p.HW;
   p.nh = VEC ? (hvox + VPI - 1) / VPI : 0;
   if (p.nh > NHMAX) p.nh = 0;
+  // Whole kw rows per weight stage on the planned halo path when the planner asks.
+  const int tps = VEC && p.nh > 0 && p.tps > 1 ? KSZ : 1;
+  // LDS: weight rings (all K-groups) and the halo; then the epilogue (K-group partial
+  // sums and the staging).
+  const size_t ring = (size_t)WRING * tps * (BO / 32) * (CC / 16) * 1024;
+  const size_t main_bytes = ring + al16(halo_bytes);
   const size_t stg = (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
   size_t lds;
   p.stg_off = 0;
@@ -1282,10 +1299,11 @@ static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t halo_byt
   dim3 grid((unsigned)nwg);
   void (*kern)(ConvParams);
   if constexpr (VEC) {
-    kern = p.nh > 0 ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, KSPL>
-                    : conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, false, KSPL>;
+    kern = p.nh == 0   ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, false, KSPL, 1>
+           : tps > 1 ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, KSPL, KSZ>
+                     : conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, KSPL, 1>;
   } else {
-    kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, false, false, KSPL>;
+    kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, false, false, KSPL, 1>;
   }
   if (lds > 65536) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1458,6 +1476,18 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
     if (want > nchunks) want = nchunks;
     p.cps = (nchunks + want - 1) / want;
     p.split = (nchunks + p.cps - 1) / p.cps;
+  }
+  // Whole kw rows per weight stage (a third of the tap loop's barriers; half for the
+  // folded 2 x 2 x 2 upsample taps) when the larger ring still keeps the whole grid
+  // resident at once. LDX_CONV_TPS=1 / 3 forces one tap / whole rows (tuning sweeps).
+  {
+    const int kz = p.upsample ? 2 : ks;
+    const size_t ring_row = (size_t)WRING * kz * (t.BO() / 32) * (t.CC / 16) * 1024;
+    const size_t lds_row = ring_row + lds + (size_t)4 * 32 * (t.FO * 32 + 4) * sizeof(float);
+    const int64_t grid = wgs * p.split;
+    p.tps = lds_row <= 160 * 1024 && grid <= (int64_t)256 * (int64_t)((160 * 1024) / lds_row) ? 2 : 1;
+    if (const char* env = getenv("LDX_CONV_TPS")) p.tps = atoi(env) > 1 ? 2 : 1;
+    if (p.tps > 1 && lds_row > 160 * 1024) p.tps = 1;
   }
   const int64_t nvox = (int64_t)p.B * p.OD * p.OH * p.OW;
   ws_bytes = p.split > 1 ? (int64_t)p.split * nvox * p.O * (int64_t)sizeof(float) : 0;
