@@ -78,12 +78,21 @@ __device__ __forceinline__ float halves_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
   return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
 }
+// Maximum of a lane's 16 scores: a tree of three-input maxima.
+__device__ __forceinline__ float max16(const f32x16& s) {
+  const float t0 = fmaxf(fmaxf(s[0], s[1]), s[2]), t1 = fmaxf(fmaxf(s[3], s[4]), s[5]);
+  const float t2 = fmaxf(fmaxf(s[6], s[7]), s[8]), t3 = fmaxf(fmaxf(s[9], s[10]), s[11]);
+  const float t4 = fmaxf(fmaxf(s[12], s[13]), s[14]);
+  return fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, s[15]));
+}
 __device__ __forceinline__ float halves_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
   return __int_as_float(r[0]) + __int_as_float(r[1]);
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 typedef short s16x8 __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -560,16 +569,28 @@ void attention_pipe_kernel(AttnParams p) {
     float alpha[QB];
 #pragma unroll
     for (int j = 0; j < QB; j++) {
-      float top;
+      // The exponent base moves only when the block's maximum exceeds it by more than RB
+      // (log2 units): probabilities stay below 2^RB (fp16-safe), and the accumulator
+      // rescale is skipped for all but the few blocks that raise the maximum that much.
       if constexpr (FULL) {
-        // maximum over the 32 keys: a tree of three-input maxima, then the partner lane's
-        const float t0 = fmaxf(fmaxf(s[j][0], s[j][1]), s[j][2]), t1 = fmaxf(fmaxf(s[j][3], s[j][4]), s[j][5]);
-        const float t2 = fmaxf(fmaxf(s[j][6], s[j][7]), s[j][8]), t3 = fmaxf(fmaxf(s[j][9], s[j][10]), s[j][11]);
-        const float t4 = fmaxf(fmaxf(s[j][12], s[j][13]), s[j][14]);
-        top = halves_max(fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, s[j][15]))) * p.c;
+        // The base is finite here (each wave's first block seeds it): the exponent
+        // arguments s * c - m are formed first and their maximum taken after, over values
+        // the compiler knows to be canonical, so the raw MFMA scores need no quieting; the
+        // base moves by that maximum on the rare blocks where it exceeds RB.
+#pragma unroll
+        for (int e = 0; e < 16; e++) s[j][e] = s[j][e] * p.c - m[j];
+        const float top = halves_max(max16(s[j]));
+        alpha[j] = 1.f;
+        if (__ballot(top > RB)) {
+          const float dlt = top > RB ? top : 0.f;
+#pragma unroll
+          for (int e = 0; e < 16; e++) s[j][e] -= dlt;
+          alpha[j] = __builtin_amdgcn_exp2f(-dlt);
+          m[j] += dlt;
+        }
       } else {
         const int kbase = (wave + SPLIT * it) * KB;
-        top = -INFINITY;
+        float top = -INFINITY;
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
@@ -580,30 +601,27 @@ void attention_pipe_kernel(AttnParams p) {
           top = fmaxf(top, t);
         }
         top = halves_max(top);
-      }
-      // The exponent base moves only when the block's maximum exceeds it by more than RB
-      // (log2 units): probabilities stay below 2^RB (fp16-safe), and the accumulator
-      // rescale is skipped for all but the few blocks that raise the maximum that much. A
-      // query with every key so far removed keeps m = -inf and contributes nothing.
-      const float mn = top > m[j] + RB ? top : m[j];
-      const float base = mn == -INFINITY ? 0.f : mn;
-      alpha[j] = __builtin_amdgcn_exp2f(m[j] - base);
-      m[j] = mn;
-      if constexpr (FULL) {
-#pragma unroll
-        for (int e = 0; e < 16; e++) s[j][e] = s[j][e] * p.c - base;
-      } else {
+        // A query with every key so far removed keeps m = -inf and contributes nothing.
+        const float mn = top > m[j] + RB ? top : m[j];
+        const float base = mn == -INFINITY ? 0.f : mn;
+        alpha[j] = __builtin_amdgcn_exp2f(m[j] - base);
+        m[j] = mn;
 #pragma unroll
         for (int e = 0; e < 16; e++) s[j][e] -= base;
       }
+      // Probabilities rounded to the element type in pairs (one packed conversion each),
+      // summed in fp32 by v_dot2 as the PV product will consume them.
       float sum = 0.f;
+      unsigned pk[8];
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const E2 pr = {(E)__builtin_amdgcn_exp2f(s[j][e]), (E)__builtin_amdgcn_exp2f(s[j][e + 1])};
-        pf[j][e >> 3][e & 7] = pr[0];
-        pf[j][e >> 3][(e & 7) + 1] = pr[1];
+        const E2 pr = __builtin_convertvector(
+            (f32x2){__builtin_amdgcn_exp2f(s[j][e]), __builtin_amdgcn_exp2f(s[j][e + 1])}, E2);
+        pk[e >> 1] = __builtin_bit_cast(unsigned, pr);
         sum = dot2_e(pr, ones, sum);
       }
+      pf[j][0] = __builtin_bit_cast(E8, (u32x4){pk[0], pk[1], pk[2], pk[3]});
+      pf[j][1] = __builtin_bit_cast(E8, (u32x4){pk[4], pk[5], pk[6], pk[7]});
       l[j] = l[j] * alpha[j] + sum;
     }
 #pragma unroll
@@ -657,6 +675,12 @@ void attention_pipe_kernel(AttnParams p) {
   // Blocks before nfull are whole and unmasked (only the sequence's last block can be
   // partial, and only the wave that owns it has it as its last).
   const int nfull = p.mask ? 0 : (p.LK % KB == 0 || (nblk - 1 - wave) % SPLIT != 0 ? nit : nit - 1);
+  // A wave whose first block is whole seeds each query's exponent base with that block's
+  // maximum, so whole blocks never meet an empty (-inf) history.
+  if (nfull > 0) {
+#pragma unroll
+    for (int j = 0; j < QB; j++) m[j] = halves_max(max16(sa[j])) * p.c;
+  }
   using T = std::integral_constant<bool, true>;
   using F = std::integral_constant<bool, false>;
   using V0 = std::integral_constant<int, 0>;
