@@ -233,9 +233,13 @@ int ldx_layer_norm(const void* x, int64_t x_pitch, int64_t rows, int32_t feature
  * broadcast axis; -inf removes a key; a query row with every key removed gives 0.
  * LDX_DTYPE_F32 (the FP32 networks; the reference's FP32 attention, _attention.py:52-145):
  * head_dim 16, 32 or 64, no mask, FP32 scores, probabilities and products throughout.
- * No scratch memory is used: V is read as it lies and transposed by the LDS reads.
- * ldx_attention_workspace_bytes returns 0 and the workspace fields are ignored (they
- * may be NULL / 0); they are kept so that callers sized by the query stay valid. */
+ * V is read as it lies and transposed by the LDS reads. Scratch memory serves one plan
+ * only: wide heads (128, 256) whose 128-query tiles spread unevenly over the CUs (the VQ
+ * decoder's 51,200-token mid attention: 400 tiles on 256 CUs) split each tile's keys into
+ * equal pieces, one workgroup each, and merge the pieces' partial states in a second
+ * launch; ldx_attention_workspace_bytes returns their size (0 for every other plan). A
+ * NULL or smaller workspace runs one workgroup per tile instead (same results within
+ * fp32 summation order). */
 typedef struct ldx_attention_args {
   int32_t batch, heads, q_len, kv_len, head_dim;
   const void* q; int64_t q_stride[3];   /* batch, len, head strides (elements) */
@@ -244,7 +248,7 @@ typedef struct ldx_attention_args {
   void* o; int64_t o_stride[3];
   float scale;
   const float* mask; int64_t mask_stride[4];
-  void* workspace; size_t workspace_bytes;   /* unused; may be NULL / 0 */
+  void* workspace; size_t workspace_bytes;   /* see ldx_attention_workspace_bytes; may be NULL / 0 */
   int32_t dtype;                        /* LDX_DTYPE_F16 (0), LDX_DTYPE_BF16 or LDX_DTYPE_F32: q, k, v, o */
 } ldx_attention_args;
 

@@ -31,6 +31,7 @@
 
 #include "elem.h"
 
+#include <cmath>
 #include <cstdlib>
 #include <type_traits>
 
@@ -45,6 +46,11 @@ struct AttnParams {
   E* o; int64_t os0, os1, os2;
   float c;  // scale * log2(e)
   const float* mask; int64_t ms0, ms1, ms2, ms3;
+  // Split wide-head schedule (attention_wide_kernel): part != null gives each query tile
+  // pmax workgroups, one per equal piece of its key blocks; each leaves its partial
+  // state in part ([tile][piece]) for attention_wide_merge_kernel.
+  float* part; int pmax;
+  size_t part_bytes;   // host only: the caller's workspace size
 };
 
 __device__ __forceinline__ f32x16 mfma32x(E8 a, E8 b, f32x16 c) {
@@ -815,12 +821,20 @@ void attention_wide_kernel(AttnParams p) {
     wg = x * per + min(x, rem) + k;
   }
   const int nqb = (p.L + 127) / 128;
-  const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
-  const int q0 = qblk * 128 + wave * 32;
+  const int nblk_all = (p.LK + KB - 1) / KB;
   E* kbuf = smem;                 // K tiles 0..2, then V tiles 0..2
   E* vbuf = smem + 3 * (TB / 2);
   const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
+  E* qbuf = smem + 6 * (TB / 2) + wave * (TB / 2);
 
+  // This workgroup's query tile and key blocks [kb0, kb0 + nblk): all of them, or under
+  // the split schedule piece `piece` of pmax equal pieces.
+  const int S = p.part ? p.pmax : 1;
+  const int t = wg / S, piece = wg - t * S;
+  const int kb0 = (int)((unsigned)(piece * nblk_all) / (unsigned)S);   // < 2^31: S <= 8
+  const int nblk = (int)((unsigned)((piece + 1) * nblk_all) / (unsigned)S) - kb0;
+  const int qblk = t % nqb, h = (t / nqb) % p.H, b = t / nqb / p.H;
+  const int q0 = qblk * 128 + wave * 32;
   const E* qb_ = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
   const E* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
   const E* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
@@ -835,7 +849,6 @@ void attention_wide_kernel(AttnParams p) {
 #pragma unroll
     for (int dk = 0; dk < DK; dk++) qf[dk] = *reinterpret_cast<const E8*>(qb_ + (int64_t)qi * p.qs1 + dk * 16 + 8 * hf);
   }
-  E* qbuf = smem + 6 * (TB / 2) + wave * (TB / 2);
   f32x16 o[DB];
 #pragma unroll
   for (int i = 0; i < DB; i++)
@@ -852,11 +865,10 @@ void attention_wide_kernel(AttnParams p) {
     koff[jj] = (unsigned)(key_row(R) * p.ks1 + c * 8) * 2u;
     voff[jj] = (unsigned)(R * p.vs1 + c * 8) * 2u;
   }
-  const int nblk = (p.LK + KB - 1) / KB;
   // Block it's tile through a buffer resource that ends at the sequence's last key (none
   // past it: a block beyond the last reads zeros).
   auto issue = [&](const E* base, int64_t rs1, const unsigned (&off)[NHW], unsigned dst_base, int it) {
-    const int kbase = it * KB;
+    const int kbase = (kb0 + it) * KB;
     const int rows = min(KB, p.LK - kbase);
     const i32x4 rs = dma_rsrc(rows > 0 ? base + (int64_t)kbase * rs1 : base,
                               rows > 0 ? (unsigned)(((rows - 1) * rs1 + D) * 2) : 0u);
@@ -924,7 +936,7 @@ void attention_wide_kernel(AttnParams p) {
       const float t4 = fmaxf(fmaxf(s[12], s[13]), s[14]);
       top = halves_max(fmaxf(fmaxf(fmaxf(t0, t1), fmaxf(t2, t3)), fmaxf(t4, s[15]))) * p.c;
     } else {
-      const int kbase = it * KB;
+      const int kbase = (kb0 + it) * KB;
       top = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 16; e++) {
@@ -1015,7 +1027,8 @@ void attention_wide_kernel(AttnParams p) {
   __syncthreads();
   f32x16 sa, sb;
   if (nblk > 0) compute_s(0, sa);
-  const int nfull = p.mask ? 0 : (p.LK % KB == 0 ? nblk : nblk - 1);
+  const int nfull_all = p.mask ? 0 : (p.LK % KB == 0 ? nblk_all : nblk_all - 1);
+  const int nfull = min(max(nfull_all - kb0, 0), nblk);
   using T = std::integral_constant<bool, true>;
   using F = std::integral_constant<bool, false>;
   // Pairs of whole blocks, then the rest (at most a whole block and the partial one, or
@@ -1034,6 +1047,18 @@ void attention_wide_kernel(AttnParams p) {
   if (it < nblk) step(it, F(), sa, sb);
   vmcnt_wait<0>();   // trailing DMAs land before the workgroup's LDS is released
   l = halves_sum(l);
+  if (S > 1) {
+    // A piece of the tile's key range: O^T unnormalized, the base and the row sum, in
+    // register order, for the merge ([tile][piece][wave][DB * 16 + 2][64 lanes]).
+    float* dst = p.part + (((int64_t)t * S + piece) * 4 + wave) * (DB * 16 + 2) * 64 + lane;
+#pragma unroll
+    for (int db = 0; db < DB; db++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) dst[(db * 16 + e) * 64] = o[db][e];
+    dst[(DB * 16) * 64] = m;
+    dst[(DB * 16 + 1) * 64] = l;
+    return;
+  }
   const int qo = q0 + col;
   if (qo < p.L) {
     E* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
@@ -1050,8 +1075,74 @@ void attention_wide_kernel(AttnParams p) {
   }
 }
 
+// The pieces of each split query tile, combined in piece order (deterministic): with M
+// the largest base, o = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j. One workgroup per
+// tile, a wave per 32 of its queries.
 template <int D>
-static int launch_attn_wide(const AttnParams& p, hipStream_t st) {
+__global__ __launch_bounds__(256) void attention_wide_merge_kernel(AttnParams p) {
+  constexpr int DB = D / 32, R = DB * 16 + 2;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int nqb = (p.L + 127) / 128;
+  const int t = blockIdx.x, S = p.pmax;
+  const float* src = p.part + ((int64_t)t * S * 4 + wave) * R * 64 + lane;
+  const int64_t pstride = (int64_t)4 * R * 64;   // floats per piece
+  float M = -INFINITY;
+  for (int j = 0; j < S; j++) M = fmaxf(M, src[j * pstride + (DB * 16) * 64]);
+  const float bse = M == -INFINITY ? 0.f : M;
+  float den = 0.f;
+  for (int j = 0; j < S; j++)
+    den += __builtin_amdgcn_exp2f(src[j * pstride + (DB * 16) * 64] - bse) * src[j * pstride + (DB * 16 + 1) * 64];
+  const float inv = den > 0.f ? 1.0f / den : 0.f;
+  const int qblk = t % nqb, h = (t / nqb) % p.H, b = t / nqb / p.H;
+  const int qo = qblk * 128 + wave * 32 + col;
+  if (qo >= p.L) return;
+  E* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
+#pragma unroll
+  for (int db = 0; db < DB; db++)
+#pragma unroll
+    for (int jj = 0; jj < 4; jj++) {
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < S; j++) {
+        const float f = __builtin_amdgcn_exp2f(src[j * pstride + (DB * 16) * 64] - bse);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[r] += f * src[j * pstride + (db * 16 + jj * 4 + r) * 64];
+      }
+      E4 out;
+#pragma unroll
+      for (int r = 0; r < 4; r++) out[r] = (E)(acc[r] * inv);
+      *reinterpret_cast<E4*>(orow + db * 32 + jj * 8 + 4 * hf) = out;
+    }
+}
+
+// Split schedule of the wide-head kernel: when the query tiles spread unevenly over the
+// CUs (config 4: 400 tiles of 128 queries on 256 CUs, so 144 CUs take two), each tile's
+// key blocks are cut into S equal pieces, one workgroup each, S chosen to minimise the
+// busiest CU's work -- ceil(tiles S / CUs) x (blocks per piece + a piece's start-up) --
+// plus the merge's traffic, in key-block units. S = 1: no split.
+template <int D>
+static void wide_split(const AttnParams& p, int& S, size_t& bytes) {
+  S = 1; bytes = 0;
+  const int64_t ntile = (int64_t)((p.L + 127) / 128) * p.H * p.B;
+  const int nblk = (p.LK + 31) / 32;
+  if (nblk < 64 || getenv("LDX_ATTN_NO_BALANCE")) return;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return;
+  const double startup = 4.0, merge = 0.04;   // key-block units (measured scale, D = 256)
+  double best = 0.0;
+  for (int s = 1; s <= 8; s++) {
+    if (nblk / s < 32 || ntile * s > 0x7fffffff) break;
+    const double per_cu = std::ceil((double)(ntile * s) / cus);
+    const double cost = per_cu * ((double)nblk / s + startup) + (s > 1 ? merge * (double)(ntile * s) : 0.0);
+    if (s == 1 || cost < best * 0.99) { best = cost; S = s; }
+  }
+  if (S > 1) bytes = (size_t)ntile * S * 4 * (D / 32 * 16 + 2) * 64 * sizeof(float);
+}
+
+template <int D>
+static int launch_attn_wide(AttnParams p, hipStream_t st) {
   const int64_t n = (int64_t)((p.L + 127) / 128) * p.H * p.B;
   if (n > 0x7fffffff) return fail("attention: grid too large");
   constexpr size_t lds = AttnWideLds<D>::bytes;
@@ -1060,12 +1151,29 @@ static int launch_attn_wide(const AttnParams& p, hipStream_t st) {
   if (lds > 65536 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return check_launch("attention: set LDS size");
-  hipLaunchKernelGGL(kern, dim3((unsigned)n), dim3(256), lds, st, p);
-  return check_launch("attention (wide heads)");
+  int S = 1;
+  size_t bytes = 0;
+  wide_split<D>(p, S, bytes);
+  // Without a workspace of that size (none given, or a caller sized for another plan):
+  // one workgroup per tile.
+  if (S == 1 || !p.part || p.part_bytes < bytes || ((uintptr_t)p.part & 15)) {
+    p.part = nullptr;
+    p.pmax = 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)n), dim3(256), lds, st, p);
+    return check_launch("attention (wide heads)");
+  }
+  p.pmax = S;
+  hipLaunchKernelGGL(kern, dim3((unsigned)(n * S)), dim3(256), lds, st, p);
+  const int rc = check_launch("attention (wide heads, split)");
+  if (rc != LDX_OK) return rc;
+  hipLaunchKernelGGL((attention_wide_merge_kernel<D>), dim3((unsigned)n), dim3(256), 0, st, p);
+  return check_launch("attention (wide heads, merge)");
 }
 
+// The kernel family launch_d picks: 1 / 4 / 8 (register-staged, key split), -4 / -8
+// (pipelined DMA key split) or -1 (wide heads).
 template <int D>
-static int launch_d(const AttnParams& p, hipStream_t st) {
+static int attn_split(const AttnParams& p) {
   // Key-split workgroups when 128-query workgroups would leave most CUs idle: for long
   // key sequences the pipelined DMA kernel (head widths 32, 64) or eight waves per 32
   // queries (16), else four.
@@ -1075,6 +1183,19 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
   else if (D == 128 && wgs >= 256) split = -1;   // enough 128-query workgroups to fill the CUs
   else if (D <= 128 && wgs < 512 && p.LK > 64)
     split = (D == 32 || D == 64) && p.LK >= 512 ? -4 : (D <= 64 && p.LK >= 512) ? 8 : 4;
+  return split;
+}
+
+// Whether launch_d runs the wide-head kernel.
+template <int D>
+static bool attn_wide(const AttnParams& p) {
+  const int split = attn_split<D>(p);
+  return (D == 128 || D == 256) && (split == -1 || (split == 1 && getenv("LDX_ATTN_SPLIT") == nullptr));
+}
+
+template <int D>
+static int launch_d(const AttnParams& p, hipStream_t st) {
+  const int split = attn_split<D>(p);
   if constexpr (D == 32 || D == 64) {
     // Long key sequences: the DMA-fed, software-pipelined four-way key split
     // (LDX_ATTN_SPLIT=-4 selects it for any length; -8 the eight-way split).
@@ -1120,17 +1241,7 @@ static int check_attention_args(const ldx_attention_args* a) {
   return LDX_OK;
 }
 
-// No scratch memory is needed (V is transposed by the LDS reads); the workspace fields
-// of the argument struct are accepted and ignored.
-size_t attention_workspace_bytes(const ldx_attention_args* a) {
-  (void)a;
-  return 0;
-}
-
-int attention_entry(const ldx_attention_args* a, void* stream) {
-  int rc = check_attention_args(a);
-  if (rc != LDX_OK) return rc;
-  const int D = a->head_dim;
+static AttnParams make_params(const ldx_attention_args* a) {
   AttnParams p{};
   p.B = a->batch; p.H = a->heads; p.L = a->q_len; p.LK = a->kv_len;
   p.q = (const E*)a->q; p.qs0 = a->q_stride[0]; p.qs1 = a->q_stride[1]; p.qs2 = a->q_stride[2];
@@ -1140,6 +1251,28 @@ int attention_entry(const ldx_attention_args* a, void* stream) {
   p.c = a->scale * 1.44269504088896341f;
   p.mask = a->mask;
   p.ms0 = a->mask_stride[0]; p.ms1 = a->mask_stride[1]; p.ms2 = a->mask_stride[2]; p.ms3 = a->mask_stride[3];
+  p.part = (float*)a->workspace;
+  p.part_bytes = a->workspace ? a->workspace_bytes : 0;
+  return p;
+}
+
+// Scratch memory: only the balanced wide-head schedule uses it (the partial states of
+// the query tiles it splits); V needs none, being transposed by the LDS reads.
+size_t attention_workspace_bytes(const ldx_attention_args* a) {
+  if (check_attention_args(a) != LDX_OK) return 0;
+  const AttnParams p = make_params(a);
+  int S = 1;
+  size_t bytes = 0;
+  if (a->head_dim == 128 && attn_wide<128>(p)) wide_split<128>(p, S, bytes);
+  if (a->head_dim == 256 && attn_wide<256>(p)) wide_split<256>(p, S, bytes);
+  return bytes;
+}
+
+int attention_entry(const ldx_attention_args* a, void* stream) {
+  int rc = check_attention_args(a);
+  if (rc != LDX_OK) return rc;
+  const int D = a->head_dim;
+  const AttnParams p = make_params(a);
   hipStream_t st = as_stream(stream);
   switch (D) {
     case 16: return launch_d<16>(p, st);
@@ -1164,7 +1297,8 @@ int attention_f32(const ldx_attention_args* a, void* stream);   // exact.hip
 
 // The C entry points (in the fp16 unit only): the kernels of the args' dtype.
 extern "C" size_t ldx_attention_workspace_bytes(const ldx_attention_args* a) {
-  (void)a;
+  if (a && a->dtype == LDX_DTYPE_BF16) return ldx::bf16_path::attention_workspace_bytes(a);
+  if (a && a->dtype == LDX_DTYPE_F16) return ldx::f16_path::attention_workspace_bytes(a);
   return 0;
 }
 

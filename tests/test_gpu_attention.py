@@ -152,3 +152,40 @@ def test_attention_wide_heads_match_float64(pkg, dev, monkeypatch, split, b, h, 
     act = host(out)
     np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
     assert_fp16_bar(act, exp)
+
+
+@pytest.mark.parametrize(("h", "lq", "lk", "d", "masked"), [
+    (1, 12800, 12800, 256, False),   # 100 tiles of 128 queries on 256 CUs
+    (2, 19200, 4000, 128, False),    # 300 tiles, two workgroups per CU
+    (1, 12800, 9000, 256, True),     # additive mask with removed keys, ragged last key block
+])
+def test_attention_balanced_wide_schedule(pkg, dev, monkeypatch, h, lq, lk, d, masked) -> None:
+    """Wide heads whose query tiles fill the resident workgroups' rounds poorly take the
+    balanced schedule: an even share of (tile, key block) units per workgroup, the pieces
+    of a split tile's key range combined by the merge kernel. Sampled rows against float64
+    over all keys, and the whole output against the one-workgroup-per-tile schedule."""
+    monkeypatch.delenv("LDX_ATTN_SPLIT", raising=False)
+    rng = np.random.default_rng(lq + lk + d)
+    q, k, v = (rng.normal(size=(1, h, n, d)).astype(np.float16) for n in (lq, lk, lk))
+    m_host = m_dev = None
+    if masked:
+        m_host = rng.normal(size=(1, 1, 1, lk)).astype(np.float32)
+        m_host[..., 100:4200] = -np.inf   # whole key blocks removed, inside one piece or across two
+        m_dev = to_dev(m_host, dev)
+    qd, kd, vd = to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
+    a = pkg.ops._attn_args(qd.transpose(1, 2), kd.transpose(1, 2), vd.transpose(1, 2), qd.transpose(1, 2),
+                           d ** -0.5, None)
+    assert a.workspace_bytes > 0, "this shape should take the balanced schedule"
+    print(f"balanced attention h {h} lq {lq} lk {lk} d {d} masked {masked}", flush=True)
+    out = pkg.ops.attention(qd, kd, vd, d ** -0.5, m_dev)
+    monkeypatch.setenv("LDX_ATTN_NO_BALANCE", "1")
+    ref = pkg.ops.attention(qd, kd, vd, d ** -0.5, m_dev)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([[0, 127, 128, lq - 1], rng.integers(0, lq, 60)]))
+    mh = None if m_host is None else m_host
+    exp = oatt.attention(q[:, :, rows], k, v, d ** -0.5, mh)
+    act = host(out)[:, :, rows]
+    np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
+    assert_fp16_bar(act, exp)
+    # the two schedules differ only in fp32 summation order before one fp16 rounding
+    assert_fp16_bar(host(out), host(ref))
