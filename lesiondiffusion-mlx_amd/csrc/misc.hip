@@ -155,7 +155,21 @@ __global__ __launch_bounds__(256) void gn_partial_kernel(
     for (int e = 0; e < V; e++) { k[e] = (float)s0[e]; sum[e] = 0.f; sq[e] = 0.f; }
   }
   if (active) {
-    for (int64_t v = v_begin + vsub; v < v_end; v += vpi) {
+    int64_t v = v_begin + vsub;
+    if constexpr (V == 8) {
+      // Eight voxels' loads in flight per thread (one wave per SIMD would otherwise wait
+      // out each load's latency), summed in the same voxel order as one at a time.
+      for (; v + 7 * vpi < v_end; v += 8 * vpi) {
+        f16x8 h[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) h[u] = *reinterpret_cast<const f16x8*>(src_of(v + u * vpi));
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) { const float f = (float)h[u][e] - k[e]; sum[e] += f; sq[e] += f * f; }
+      }
+    }
+    for (; v < v_end; v += vpi) {
       const f16* src = src_of(v);
       if constexpr (V == 8) {
         const f16x8 h = *reinterpret_cast<const f16x8*>(src);
