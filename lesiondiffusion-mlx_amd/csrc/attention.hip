@@ -1048,15 +1048,15 @@ void attention_wide_kernel(AttnParams p) {
   vmcnt_wait<0>();   // trailing DMAs land before the workgroup's LDS is released
   l = halves_sum(l);
   if (S > 1) {
-    // A piece of the tile's key range: O^T unnormalized, the base and the row sum, in
-    // register order, for the merge ([tile][piece][wave][DB * 16 + 2][64 lanes]).
-    float* dst = p.part + (((int64_t)t * S + piece) * 4 + wave) * (DB * 16 + 2) * 64 + lane;
+    // A piece of the tile's key range: O^T unnormalized in register order, four registers
+    // per lane and row, then (base, row sum): [tile][piece][wave][DB * 4 + 1][64 lanes][4].
+    f32x4* dst = reinterpret_cast<f32x4*>(p.part) + (((int64_t)t * S + piece) * 4 + wave) * (DB * 4 + 1) * 64 + lane;
 #pragma unroll
     for (int db = 0; db < DB; db++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) dst[(db * 16 + e) * 64] = o[db][e];
-    dst[(DB * 16) * 64] = m;
-    dst[(DB * 16 + 1) * 64] = l;
+      for (int e4 = 0; e4 < 4; e4++)
+        dst[(db * 4 + e4) * 64] = (f32x4){o[db][4 * e4], o[db][4 * e4 + 1], o[db][4 * e4 + 2], o[db][4 * e4 + 3]};
+    dst[(DB * 4) * 64] = (f32x4){m, l, 0.f, 0.f};
     return;
   }
   const int qo = q0 + col;
@@ -1078,41 +1078,59 @@ void attention_wide_kernel(AttnParams p) {
 // The pieces of each split query tile, combined in piece order (deterministic): with M
 // the largest base, o = sum_j 2^(m_j - M) O_j / sum_j 2^(m_j - M) l_j. One workgroup per
 // tile, a wave per 32 of its queries.
-template <int D>
+template <int D, int S>
 __global__ __launch_bounds__(256) void attention_wide_merge_kernel(AttnParams p) {
-  constexpr int DB = D / 32, R = DB * 16 + 2;
+  constexpr int DB = D / 32, R4 = DB * 4 + 1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hf = lane >> 5, col = lane & 31;
   const int nqb = (p.L + 127) / 128;
-  const int t = blockIdx.x, S = p.pmax;
-  const float* src = p.part + ((int64_t)t * S * 4 + wave) * R * 64 + lane;
-  const int64_t pstride = (int64_t)4 * R * 64;   // floats per piece
-  float M = -INFINITY;
-  for (int j = 0; j < S; j++) M = fmaxf(M, src[j * pstride + (DB * 16) * 64]);
+  const int t = blockIdx.x;
+  const f32x4* src = reinterpret_cast<const f32x4*>(p.part) + ((int64_t)t * S * 4 + wave) * R4 * 64 + lane;
+  constexpr int64_t pstride = (int64_t)4 * R4 * 64;   // float4 rows per piece
+  float mj[S], f[S];
+  float M = -INFINITY, den = 0.f;
+#pragma unroll
+  for (int j = 0; j < S; j++) {
+    const f32x4 ml = src[j * pstride + (DB * 4) * 64];
+    mj[j] = ml[0];
+    f[j] = ml[1];   // the row sum, until it becomes the weight below
+    M = fmaxf(M, mj[j]);
+  }
   const float bse = M == -INFINITY ? 0.f : M;
-  float den = 0.f;
-  for (int j = 0; j < S; j++)
-    den += __builtin_amdgcn_exp2f(src[j * pstride + (DB * 16) * 64] - bse) * src[j * pstride + (DB * 16 + 1) * 64];
+#pragma unroll
+  for (int j = 0; j < S; j++) {
+    const float w = __builtin_amdgcn_exp2f(mj[j] - bse);
+    den += w * f[j];
+    f[j] = w;
+  }
   const float inv = den > 0.f ? 1.0f / den : 0.f;
   const int qblk = t % nqb, h = (t / nqb) % p.H, b = t / nqb / p.H;
   const int qo = qblk * 128 + wave * 32 + col;
   if (qo >= p.L) return;
   E* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
+  // Two tiles of 32 dims (8 rows of every piece) requested before any is summed.
 #pragma unroll
-  for (int db = 0; db < DB; db++)
+  for (int db = 0; db < DB; db += 2) {
+    f32x4 v[2][4][S];
 #pragma unroll
-    for (int jj = 0; jj < 4; jj++) {
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int j = 0; j < S; j++) {
-        const float f = __builtin_amdgcn_exp2f(src[j * pstride + (DB * 16) * 64] - bse);
+    for (int u = 0; u < 2; u++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) acc[r] += f * src[j * pstride + (db * 16 + jj * 4 + r) * 64];
+      for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+        for (int j = 0; j < S; j++) v[u][jj][j] = src[j * pstride + ((db + u) * 4 + jj) * 64];
+#pragma unroll
+    for (int u = 0; u < 2; u++)
+#pragma unroll
+      for (int jj = 0; jj < 4; jj++) {
+        f32x4 acc = f[0] * v[u][jj][0];
+#pragma unroll
+        for (int j = 1; j < S; j++) acc += f[j] * v[u][jj][j];
+        E4 out;
+#pragma unroll
+        for (int r = 0; r < 4; r++) out[r] = (E)(acc[r] * inv);
+        *reinterpret_cast<E4*>(orow + (db + u) * 32 + jj * 8 + 4 * hf) = out;
       }
-      E4 out;
-#pragma unroll
-      for (int r = 0; r < 4; r++) out[r] = (E)(acc[r] * inv);
-      *reinterpret_cast<E4*>(orow + db * 32 + jj * 8 + 4 * hf) = out;
-    }
+  }
 }
 
 // Split schedule of the wide-head kernel: when the query tiles spread unevenly over the
@@ -1138,7 +1156,7 @@ static void wide_split(const AttnParams& p, int& S, size_t& bytes) {
     const double cost = per_cu * ((double)nblk / s + startup) + (s > 1 ? merge * (double)(ntile * s) : 0.0);
     if (s == 1 || cost < best * 0.99) { best = cost; S = s; }
   }
-  if (S > 1) bytes = (size_t)ntile * S * 4 * (D / 32 * 16 + 2) * 64 * sizeof(float);
+  if (S > 1) bytes = (size_t)ntile * S * 4 * (D / 32 * 4 + 1) * 64 * 4 * sizeof(float);
 }
 
 template <int D>
@@ -1166,7 +1184,13 @@ static int launch_attn_wide(AttnParams p, hipStream_t st) {
   hipLaunchKernelGGL(kern, dim3((unsigned)(n * S)), dim3(256), lds, st, p);
   const int rc = check_launch("attention (wide heads, split)");
   if (rc != LDX_OK) return rc;
-  hipLaunchKernelGGL((attention_wide_merge_kernel<D>), dim3((unsigned)n), dim3(256), 0, st, p);
+  switch (S) {
+#define LDX_MERGE(S_) \
+  case S_: hipLaunchKernelGGL((attention_wide_merge_kernel<D, S_>), dim3((unsigned)n), dim3(256), 0, st, p); break;
+    LDX_MERGE(2) LDX_MERGE(3) LDX_MERGE(4) LDX_MERGE(5) LDX_MERGE(6) LDX_MERGE(7) LDX_MERGE(8)
+#undef LDX_MERGE
+    default: return fail("attention: %d key pieces", S);
+  }
   return check_launch("attention (wide heads, merge)");
 }
 
