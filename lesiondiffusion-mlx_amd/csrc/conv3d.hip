@@ -24,6 +24,7 @@
 // stride-2 / upsample window rule :185-189, 251-253.
 
 #include "elem.h"
+#include "conv3d_quad.h"
 #include "conv3d_stream.h"
 
 #include <algorithm>
@@ -1510,6 +1511,8 @@ size_t conv3d_workspace_bytes(const ldx_conv3d_args* a) {
   int64_t ws = 0;
   if (plan_conv(a, p, t, lds, vec, ws) != LDX_OK) return 0;
   if (use_dense(a, vec)) return 0;
+  QuadParams qp;
+  if (conv3d_quad_plan(a, &qp)) return 0;
   StreamParams sp;
   if (conv3d_stream_plan(a, &sp, false))
     return sp.split > 1 ? (size_t)sp.split * (size_t)p.B * p.OD * p.OH * p.OW * p.O * sizeof(float) : 0;
@@ -1656,6 +1659,17 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
     if (dry) return LDX_OK;
     if (stats) return fail("conv3d_stats: pointwise convs keep no moments");
     return run_dense(p, st);
+  }
+  {
+    QuadParams qp;
+    if (conv3d_quad_plan(a, &qp)) {
+      const int64_t ch = can_stats ? qp.schunks : 0;
+      if (chunks) *chunks = ch;
+      if (dry) return LDX_OK;
+      if (stats && ch == 0) return fail("conv3d_stats: this conv keeps no moments");
+      qp.stats = stats;
+      return conv3d_quad_launch(qp, st);
+    }
   }
   {
     StreamParams sp;

@@ -1,0 +1,440 @@
+// K-quarter implicit-GEMM 3x3x3 stride-1 convolution on gfx950 MFMA
+// (v_mfma_f32_32x32x16_f16 / _bf16) for volumes whose bricks of at most 224 voxels fill the
+// GPU: input channels in 64-channel chunks, output channels in 64-channel tiles, 16-byte
+// aligned NDHWC rows, no input transform.
+//
+// Workgroup: 8 waves, two per SIMD (one workgroup per CU). The workgroup owns one brick of
+// V <= 224 voxels (NCOL = ceil(V / 32) MFMA columns) x 64 output channels. The two waves
+// of SIMD s take the same quarter of the reduction -- channels 16 s .. 16 s + 15 of every
+// 64-channel chunk, all 27 taps -- one for columns 0..3, the other for columns 4..NCOL-1,
+// each in 2 x 4 (2 x 3) accumulator tiles: per tap a wave reads 2 weight fragments and 4
+// halo fragments for 8 MFMAs (a SIMD: 10 fragments per 14 MFMAs at NCOL = 7, against one
+// per MFMA for a 2 x 2 register block).
+//
+// Operands: the brick's halo (64 channels) is copied global -> LDS by DMA once per chunk,
+// in rows along W of 9 16-byte units per voxel (8 of channels, 1 of padding) with row and
+// plane strides padded so that the halo unit of the brick's raster voxel v is 9 v (mod 16):
+// any 16 consecutive voxels of a column hit 16 distinct bank groups at every tap offset.
+// Each tap's offset is a compile-time constant, so a halo fragment is one ds_read_b128 at
+// a base register plus an immediate. The weight fragments come straight from global
+// memory (L2) into registers, three taps ahead; no LDS and no barrier in the tap loop.
+//
+// Epilogue, in two rounds (columns 0..3, then 4..NCOL-1): the four waves holding the
+// round's columns write their partial sums as fp32 voxel rows to LDS; after one barrier a
+// thread of any wave takes 8 consecutive channels of a voxel, adds the four quarters in
+// order, then bias (+ per-batch-item bias) plus fp16 shift, output scale, fp16 residual,
+// one rounding, and one 16-byte store (whole 128-byte rows per 8 lanes).
+//
+// Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619), epilogue
+// _nax_conv.py:265-270 (+ scaled variant :418-421).
+
+#include "elem.h"
+#include "conv3d_quad.h"
+
+#include <cstdlib>
+
+namespace ldx {
+namespace LDX_ELEM_NS {
+namespace cq {
+
+constexpr int NT = 512;                 // 8 waves, two per SIMD
+constexpr int KC = 64;                  // input channels per halo chunk
+constexpr int PU = 9;                   // 16-byte units per halo voxel (8 + 1 of padding)
+constexpr int RP = 68;                  // floats per epilogue row: 64 channels + 4 of padding
+constexpr int NA = 4;                   // weight operand sets in flight (three taps ahead)
+constexpr unsigned OOB = 0xfffffff0u;   // a buffer offset past every extent: reads zeros
+
+// Smallest x >= base with x = r (mod 16).
+constexpr int up16(int base, int r) { return base + ((r - base) % 16 + 16) % 16; }
+
+template <int TD, int TH, int TW>
+struct QShape {
+  static constexpr int V = TD * TH * TW;            // voxels per brick
+  static constexpr int NCOL = (V + 31) / 32;        // 32-voxel MFMA columns
+  static_assert(NCOL <= 7, "at most seven columns (224 voxels) per brick");
+  static constexpr int HD = TD + 2, HH = TH + 2, HW = TW + 2;
+  // Unit of brick voxel (vd, vh, vw) in the halo: vd PSU + vh RSU + vw PU, which is 9 v
+  // (mod 16) for the voxel's raster index v = (vd TH + vh) TW + vw.
+  static constexpr int RU = HW * PU;                // units of a row holding voxels
+  static constexpr int RDMA = (RU + 63) / 64;       // 64-lane DMAs per row
+  // Rows at least RDMA * 64 units apart, so that a row's DMAs never reach the next row.
+  static constexpr int RSU = up16(RDMA * 64, (9 * TW) % 16);
+  static constexpr int PSU = up16(HH * RSU, (9 * TW * TH) % 16);
+  static constexpr int HALO = HD * PSU * 16;
+  static constexpr int NROW = HD * HH;              // halo rows (along W)
+  static constexpr int RPW = (NROW + 7) / 8;        // rows per wave
+  static constexpr int NC0 = NCOL < 4 ? NCOL : 4;   // columns of group 0 (the first round)
+  static constexpr int NC1 = NCOL - NC0;            // columns of group 1 (the second round)
+  static constexpr int EPI = 4 * NC0 * 32 * RP * 4;
+  static constexpr int MST = 8 * 32 * 3 * 4;         // per-wave GroupNorm moments, past the rows
+  static constexpr int LDS = HALO > EPI + MST ? HALO : EPI + MST;
+  static constexpr int NV0 = V < 128 ? V : 128;      // voxels of the first epilogue round
+  static constexpr int NI0 = (NV0 * 8 + NT - 1) / NT, NI1 = ((V - NV0) * 8 + NT - 1) / NT;
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert((2 * PSU + 2 * RSU + 2 * PU) * 16 < 65536, "tap offsets fit the ds_read immediate");
+};
+
+__device__ __forceinline__ f32x16 mfma(E8 a, E8 b, f32x16 c) { return mfma_e(a, b, c); }
+
+template <int TD, int TH, int TW>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv3q_kernel(QuadParams p) {
+  using S = QShape<TD, TH, TW>;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int sq = wave & 3, grp = wave >> 2;   // reduction quarter, column group
+
+  // Workgroup -> (output tile, brick, batch item); each XCD (workgroups are dealt to the 8
+  // XCDs round-robin) receives a contiguous range, so neighbouring halos meet in its L2.
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x * per + min(x, rem) + k;
+  }
+  const int q1 = udiv(wg, p.dv_nob);
+  const int oblk = wg - q1 * p.nob;
+  const int b = udiv(q1, p.dv_nbr);
+  const int brick = q1 - b * p.nbr;
+  const int bt = udiv(brick, p.dv_nbw), bw_i = brick - bt * p.NBW;
+  const int bd_i = udiv(bt, p.dv_nbh), bh_i = bt - bd_i * p.NBH;
+  const int d0 = bd_i * TD, h0 = bh_i * TH, w0 = bw_i * TW;
+  const int vol = p.D * p.H * p.W;
+
+  // ---- halo DMA lanes: unit u = 64 h + lane of a halo row is voxel hw = u / PU, 16-byte
+  // channel group q = u % PU. Units past the row's voxels and the padding unit q = 8 load
+  // zeros (they are never read); so do voxels outside the volume, which are the conv's
+  // zero padding.
+  bool lok[S::RDMA];
+  unsigned lpos[S::RDMA];
+#pragma unroll
+  for (int h = 0; h < S::RDMA; h++) {
+    const int u = 64 * h + lane, hw = u / PU, q = u - hw * PU;
+    const int iw = w0 - 1 + hw;
+    lok[h] = u < S::RU && q < 8 && (unsigned)iw < (unsigned)p.W;
+    lpos[h] = (unsigned)(iw * 65536 + q * 16);   // voxel along W, byte of its channel group
+  }
+  // Chunk j's halo: the wave's rows r = wave + 8 i, RDMA DMAs of 1 KB each.
+  auto halo_dma = [&](int j) {
+    const int c0 = j * KC;
+    const bool in0 = c0 < p.C0;
+    const E* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
+    const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
+    const i32x4 rs = dma_rsrc(base, (unsigned)vol * pitch2);
+    const unsigned cb = (unsigned)((in0 ? c0 : c0 - p.C0) * 2);
+    unsigned lo[S::RDMA];
+#pragma unroll
+    for (int h = 0; h < S::RDMA; h++) lo[h] = (lpos[h] >> 16) * pitch2 + (lpos[h] & 0xffffu) + cb;
+    unsigned m0 = lds_offset(smem) + (unsigned)((wave / S::HH) * S::PSU + (wave % S::HH) * S::RSU) * 16u;
+    int hd = wave / S::HH, hh = wave % S::HH;
+#pragma unroll
+    for (int i = 0; i < S::RPW; i++) {
+      if (wave + 8 * i >= S::NROW) break;
+      const int id = d0 - 1 + hd, ih = h0 - 1 + hh;
+      const bool rowok = (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H;
+      const unsigned roff = (unsigned)((id * p.H + ih) * p.W) * pitch2;
+#pragma unroll
+      for (int h = 0; h < S::RDMA; h++) dma_buffer_b128(rs, rowok && lok[h] ? lo[h] + roff : OOB, 0, m0 + 1024u * h);
+      // next row of this wave: eight rows on
+      hh += 8;
+      m0 += 8u * S::RSU * 16u;
+#pragma unroll
+      for (int k = 0; k < 8 / S::HH + 1; k++)
+        if (hh >= S::HH) { hh -= S::HH; hd += 1; m0 += (unsigned)(S::PSU - S::HH * S::RSU) * 16u; }
+    }
+  };
+
+  // ---- weight fragments: (tile o, tap t, k-step 4 j + wave) of output block 2 oblk + o,
+  // 1 KB each, the lane's 16 bytes at lane * 16. wa walks the taps of a chunk.
+  const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (unsigned)(p.O * 27 * p.NKC * 32));
+  const unsigned voffa = (unsigned)(lane * 16 + sq * 1024);
+  E8 aq[NA][2];
+  unsigned wa = 0, wstep = 0, wob = 0;
+  auto load_a = [&](E8(&dst)[2]) {
+    dst[0] = as_e8(buffer_load16(wr, voffa, wa));
+    dst[1] = as_e8(buffer_load16(wr, voffa, wa + wob));
+    wa += wstep;
+  };
+
+  f32x16 acc[4][2];
+
+  // The wave's column group G (NC columns, 4 G .. 4 G + NC - 1), all chunks.
+  auto body = [&](auto gc) {
+    constexpr int G = decltype(gc)::value;
+    constexpr int NC = G == 0 ? S::NC0 : S::NC1;
+    // ---- halo fragments: column 4 G + c's lane reads voxel min(32 (4 G + c) + lane % 32,
+    // V - 1), channels 16 sq + 8 (lane / 32) .. + 7.
+    int bb[NC > 0 ? NC : 1];
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      int v = 32 * (4 * G + c) + (lane & 31);
+      if (v > S::V - 1) v = S::V - 1;
+      const int vw = v % TW, vh = (v / TW) % TH, vd = v / (TW * TH);
+      bb[c] = ((vd * S::PSU + vh * S::RSU + vw * PU) + 2 * sq + (lane >> 5)) * 16;
+    }
+    E8 bq[2][NC > 0 ? NC : 1];
+
+    // One 64-channel chunk: its halo by DMA and the first three taps' weights, one wait and
+    // barrier, then the 27 taps. FIRST: the accumulators start from the first MFMA (C = 0).
+    auto run_chunk = [&](int j, auto first) {
+      constexpr bool FIRST = decltype(first)::value;
+      halo_dma(j);
+      if constexpr (NC > 0) {
+        // Per-chunk weight walk; the asm keeps the step opaque, so that no tap's offset is
+        // computed once outside the chunk loop and held for the whole kernel.
+        wstep = (unsigned)(p.NKC * 1024);
+        asm volatile("" : "+s"(wstep));
+        wob = 27u * wstep;
+        wa = (unsigned)(oblk * 2) * wob + (unsigned)(4 * j * 1024);
+#pragma unroll
+        for (int t = 0; t < NA - 1; t++) load_a(aq[t]);
+        vmcnt_wait<(NA - 1) * 2>();   // the halo has landed (the weights may be in flight)
+      } else {
+        vmcnt_wait<0>();
+      }
+      __syncthreads();
+      if constexpr (NC > 0) {
+#pragma unroll
+        for (int c = 0; c < NC; c++) bq[0][c] = *reinterpret_cast<const E8*>(smem + bb[c]);
+#pragma unroll
+        for (int t = 0; t < 27; t++) {
+          // Issue order, pinned by scheduling barriers: per column the MFMA pair of this
+          // tap, then that column's halo fragment of the next tap (it has a tap of MFMAs to
+          // land in); the weight requests after the first pair.
+          const int kd = (t + 1) / 9, kh = ((t + 1) / 3) % 3, kw = (t + 1) % 3;
+          const int toff = (kd * S::PSU + kh * S::RSU + kw * PU) * 16;
+#pragma unroll
+          for (int c = 0; c < NC; c++) {
+#pragma unroll
+            for (int o = 0; o < 2; o++) {
+              if (FIRST && t == 0) acc[c][o] = mfma(aq[0][o], bq[0][c], (f32x16){});
+              else acc[c][o] = mfma(aq[t % NA][o], bq[t & 1][c], acc[c][o]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (t + 1 < 27) bq[(t + 1) & 1][c] = *reinterpret_cast<const E8*>(smem + bb[c] + toff);
+            if (c == 0 && t + NA - 1 < 27) load_a(aq[(t + NA - 1) % NA]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+    };
+    run_chunk(0, std::true_type{});
+    for (int j = 1; j < p.nchunk; j++) {
+      __syncthreads();   // every wave done with the previous chunk's halo
+      run_chunk(j, std::false_type{});
+    }
+  };
+  if (grp == 0) body(std::integral_constant<int, 0>{});
+  else body(std::integral_constant<int, 1>{});
+
+  // ---- epilogue
+  const int col = lane & 31, hf = lane >> 5, g8 = tid & 7;
+  const int o8 = oblk * 64 + g8 * 8;
+  // bias (+ per-batch-item bias) + fp16 shift of this thread's 8 channels
+  float bs[8];
+  {
+    f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
+    E8 sv = {};
+    if (p.bias) {
+      const float* bias = p.bias + (p.bias_batched ? b * p.O : 0) + o8;
+      bv0 = *reinterpret_cast<const f32x4*>(bias);
+      bv1 = *reinterpret_cast<const f32x4*>(bias + 4);
+    }
+    if (p.shift) sv = *reinterpret_cast<const E8*>(p.shift + (int64_t)b * p.shiftp + o8);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      bs[e] = bv0[e] + (float)sv[e];
+      bs[e + 4] = bv1[e] + (float)sv[e + 4];
+    }
+  }
+  // Outputs and residual rows through buffer resources (32-bit byte offsets).
+  const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, (unsigned)(p.B * vol) * (unsigned)p.yp * 2u);
+  const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.res, p.res ? (unsigned)(p.B * vol) * (unsigned)p.resp * 2u : 0u);
+  const bool has_res = p.res != nullptr, scaled = p.scale != 1.0f;
+  float* rows = reinterpret_cast<float*>(smem);
+  // The stored values and their validity, kept for the GroupNorm moments.
+  E8 outv[S::NI0 + S::NI1 > 0 ? S::NI0 + S::NI1 : 1];
+  bool okv[S::NI0 + S::NI1 > 0 ? S::NI0 + S::NI1 : 1];
+  auto round = [&](auto kc) {
+    constexpr int K = decltype(kc)::value;
+    constexpr int NCR = K == 0 ? S::NC0 : S::NC1;
+    constexpr int NV = K == 0 ? S::NV0 : S::V - S::NV0;   // voxels of the round
+    constexpr int NU = NV * 8, NI = K == 0 ? S::NI0 : S::NI1, I0 = K == 0 ? 0 : S::NI0;
+    // This thread's outputs of the round (voxel 128 K + 64 i + tid / 8), and their
+    // residual rows, requested first.
+    unsigned ovr[NI > 0 ? NI : 1];
+    E8 res[NI > 0 ? NI : 1];
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      const int v = 128 * K + 64 * i + (tid >> 3);
+      const int vd = v / (TW * TH), rv = v - vd * (TW * TH), vh = rv / TW, vw = rv - vh * TW;
+      const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
+      okv[I0 + i] = (i * NT + tid < NU) && od < p.D && oh < p.H && ow < p.W;
+      ovr[i] = (unsigned)(b * vol + (od * p.H + oh) * p.W + ow);
+      res[i] = (E8){};
+      if (has_res && okv[I0 + i]) res[i] = buffer_load16<E8>(rr, (ovr[i] * (unsigned)p.resp + o8) * 2u);
+    }
+    if (K > 0) __syncthreads();   // the previous round's rows have been read
+    if (grp == K) {
+#pragma unroll
+      for (int cl = 0; cl < NCR; cl++)
+#pragma unroll
+        for (int o = 0; o < 2; o++)
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const f32x16& a = acc[cl][o];
+            const f32x4 v = {a[4 * jj], a[4 * jj + 1], a[4 * jj + 2], a[4 * jj + 3]};
+            *reinterpret_cast<f32x4*>(rows + ((sq * 4 + cl) * 32 + col) * RP + 32 * o + 8 * jj + 4 * hf) = v;
+          }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NI; i++) {
+      E8& out = outv[I0 + i];
+      out = (E8){};
+      if (!okv[I0 + i]) continue;
+      const float* r0 = rows + (64 * i + (tid >> 3)) * RP + g8 * 8;
+      f32x4 s0 = *reinterpret_cast<const f32x4*>(r0);
+      f32x4 s1 = *reinterpret_cast<const f32x4*>(r0 + 4);
+#pragma unroll
+      for (int w = 1; w < 4; w++) {
+        const float* rw = r0 + w * 4 * 32 * RP;
+        s0 += *reinterpret_cast<const f32x4*>(rw);
+        s1 += *reinterpret_cast<const f32x4*>(rw + 4);
+      }
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        f[e] = s0[e] + bs[e];
+        f[e + 4] = s1[e] + bs[e + 4];
+      }
+      if (scaled) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) f[e] *= p.scale;
+      }
+      if (has_res) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) f[e] += (float)res[i][e];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) out[e] = (E)f[e];
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, out), yr,
+                                             (int)((ovr[i] * (unsigned)p.yp + o8) * 2u), 0, 0);
+    }
+  };
+  __syncthreads();   // every wave done with the halo
+  round(std::integral_constant<int, 0>{});
+  if constexpr (S::NC1 > 0) round(std::integral_constant<int, 1>{});
+
+  // GroupNorm partial moments of the stored values, one block per brick: each wave's
+  // channel pairs over its voxels (lanes l, l + 8, ... hold the same 8 channels) into LDS
+  // past the epilogue rows, then thread pp < 32 merges pair pp over the eight waves in order.
+  if (p.stats) {
+    float* mst = reinterpret_cast<float*>(smem + S::EPI);   // [8 waves][32 pairs][3]
+    pair_moments<S::NI0 + S::NI1, 8>(outv, okv, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
+    __syncthreads();
+    if (tid < 32) {
+      Moments m = {0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        const float* q = mst + (w * 32 + tid) * 3;
+        m = merge(m, Moments{q[0], q[1], q[2]});
+      }
+      float* dst = p.stats + (((int64_t)b * p.schunks + brick) * (p.O / 2) + oblk * 32 + tid) * 3;
+      dst[0] = m.n; dst[1] = m.mean; dst[2] = m.m2;
+    }
+  }
+}
+
+template <int TD, int TH, int TW>
+static int launch(QuadParams& p, hipStream_t st) {
+  using S = QShape<TD, TH, TW>;
+  p.dv_nob = make_udiv((unsigned)p.nob);
+  p.dv_nbr = make_udiv((unsigned)p.nbr);
+  p.dv_nbw = make_udiv((unsigned)p.NBW);
+  p.dv_nbh = make_udiv((unsigned)p.NBH);
+  auto kern = conv3q_kernel<TD, TH, TW>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS) != hipSuccess)
+    return check_launch("conv3d (K-quarter): set LDS size");
+  const int64_t nwg = (int64_t)p.nbr * p.nob * p.B;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nwg), dim3(NT), S::LDS, st, p);
+  return check_launch("conv3d (K-quarter)");
+}
+
+struct QBrick {
+  int TD, TH, TW;
+};
+static const QBrick kQBricks[] = {{4, 5, 10}};
+
+}  // namespace cq
+
+bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* out) {
+  using namespace cq;
+  int force = -1;
+  if (const char* env = getenv("LDX_CONV_QUAD")) force = atoi(env);
+  if (force == 0) return false;
+  if (a->ksize != 3 || a->stride != 1 || a->upsample || a->act != LDX_ACT_NONE) return false;
+  if (a->affine || a->silu) return false;
+  if (a->c0 % KC || a->c1 % KC || a->out_c % 64) return false;
+  if (a->c1 > 0 && !a->x1) return false;
+  if (a->x0_pitch % 8 || (a->c1 > 0 && a->x1_pitch % 8)) return false;
+  if ((uintptr_t)a->x0 % 16 || (a->c1 > 0 && (uintptr_t)a->x1 % 16)) return false;
+  if (a->y_pitch % 8 || (uintptr_t)a->y % 16) return false;
+  if (a->residual && (a->residual_pitch % 8 || (uintptr_t)a->residual % 16)) return false;
+  if (a->shift && (a->shift_pitch % 8 || (uintptr_t)a->shift % 16)) return false;
+  if (a->bias && (uintptr_t)a->bias % 16) return false;
+  const int64_t vol = (int64_t)a->in_d * a->in_h * a->in_w;
+  if (vol * a->x0_pitch * 2 >= ((int64_t)1 << 31)) return false;
+  if (a->c1 > 0 && vol * a->x1_pitch * 2 >= ((int64_t)1 << 31)) return false;
+  if ((int64_t)a->batch * vol >= ((int64_t)1 << 31)) return false;
+  if ((int64_t)a->batch * vol * a->y_pitch * 2 >= ((int64_t)1 << 32)) return false;
+  if (a->residual && (int64_t)a->batch * vol * a->residual_pitch * 2 >= ((int64_t)1 << 32)) return false;
+  if ((int64_t)a->out_c * 27 * ((a->c0 + a->c1 + 63) / 64 * 4) * 32 >= ((int64_t)1 << 31)) return false;
+
+  const QBrick& k = kQBricks[0];
+  const int64_t nb = ceil_div64(a->in_d, k.TD) * ceil_div64(a->in_h, k.TH) * ceil_div64(a->in_w, k.TW);
+  const int64_t nwg = nb * (a->out_c / 64) * a->batch;
+  if (nwg > 0x7fffffff) return false;
+  if (force != 1) {
+    // Modelled workgroup time (cycles per 64 input channels): MFMA cycles of the busiest
+    // SIMD at the measured main-loop efficiency of each kernel, plus the per-workgroup
+    // fixed cost, times the rounds of workgroups over 256 CUs. The streamed kernel's brick
+    // is 256 voxels.
+    const int ncol = (k.TD * k.TH * k.TW + 31) / 32;
+    const int64_t nchunk = (a->c0 + a->c1) / KC;
+    const double quad = (double)ceil_div64(nwg, 256) * (nchunk * ncol * 54 * 32 / 0.95 + 6000.0);
+    const int64_t snb = ceil_div64(a->in_d, 4) * ceil_div64(a->in_h, 8) * ceil_div64(a->in_w, 8);
+    const int64_t swg = snb * (a->out_c / 64) * a->batch;
+    const double stream = (double)ceil_div64(swg, 256) * (nchunk * 432 * 32 / 0.7 + 9000.0);
+    if (!(quad < stream)) return false;
+  }
+  QuadParams& p = *out;
+  p = QuadParams{};
+  p.B = a->batch; p.D = a->in_d; p.H = a->in_h; p.W = a->in_w;
+  p.C0 = a->c0; p.C1 = a->c1; p.C = a->c0 + a->c1; p.O = a->out_c;
+  p.nchunk = p.C / KC;
+  p.NKC = (p.C + 63) / 64 * 4;
+  p.x0 = (const E*)a->x0; p.x0p = a->x0_pitch;
+  p.x1 = a->c1 > 0 ? (const E*)a->x1 : p.x0; p.x1p = a->c1 > 0 ? a->x1_pitch : a->x0_pitch;
+  p.w = (const E*)a->weight;
+  p.bias = a->bias; p.bias_batched = a->bias_batched ? 1 : 0;
+  p.shift = (const E*)a->shift; p.shiftp = a->shift_pitch;
+  p.res = (const E*)a->residual; p.resp = a->residual_pitch;
+  p.scale = a->output_scale;
+  p.y = (E*)a->y; p.yp = a->y_pitch;
+  p.TD = k.TD; p.TH = k.TH; p.TW = k.TW;
+  p.nob = p.O / 64;
+  p.NBD = (int)ceil_div64(p.D, k.TD);
+  p.NBH = (int)ceil_div64(p.H, k.TH);
+  p.NBW = (int)ceil_div64(p.W, k.TW);
+  p.nbr = (int)nb;
+  p.schunks = p.nbr;
+  return true;
+}
+
+int conv3d_quad_launch(QuadParams& p, hipStream_t st) {
+  if (p.TD == 4 && p.TH == 5 && p.TW == 10) return cq::launch<4, 5, 10>(p, st);
+  return fail("conv3d (K-quarter): no kernel for brick %dx%dx%d", p.TD, p.TH, p.TW);
+}
+
+}  // namespace LDX_ELEM_NS
+}  // namespace ldx

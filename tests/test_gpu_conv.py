@@ -16,19 +16,25 @@ from tests.conftest import ACCUMULATION_EPS, OPERAND_ROUNDING, assert_fp16_bar, 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(autouse=True, params=["default", "streamed", "streamed-split"])
+@pytest.fixture(autouse=True, params=["default", "streamed", "streamed-split", "quad"])
 def conv_path(request, monkeypatch):
-    """Every case three times: with the library's own kernel choice; with the streamed
+    """Every case four times: with the library's own kernel choice; with the streamed
     3x3x3 kernel taking every shape it supports (its fill threshold lowered to one
-    workgroup), so small cases cover its partial bricks, batches, concat and fusions; and
+    workgroup), so small cases cover its partial bricks, batches, concat and fusions;
     with that threshold out of reach, so every streamed shape with two or more channel
-    chunks splits them over workgroups (fp32 partial sums, fixed-order reduce)."""
+    chunks splits them over workgroups (fp32 partial sums, fixed-order reduce); and with
+    the K-quarter kernel taking every shape it supports (64-channel input chunks and
+    output tiles, no input transform)."""
+    monkeypatch.delenv("LDX_CONV_STREAM_MIN_WG", raising=False)
+    monkeypatch.delenv("LDX_CONV_QUAD", raising=False)
     if request.param == "streamed":
         monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1")
+        monkeypatch.setenv("LDX_CONV_QUAD", "0")
     elif request.param == "streamed-split":
         monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1000000")
-    else:
-        monkeypatch.delenv("LDX_CONV_STREAM_MIN_WG", raising=False)
+        monkeypatch.setenv("LDX_CONV_QUAD", "0")
+    elif request.param == "quad":
+        monkeypatch.setenv("LDX_CONV_QUAD", "1")
     return request.param
 
 
@@ -92,6 +98,35 @@ def test_conv3d_matches_float64_and_rounds_once(pkg, dev, shape, out_c, stride) 
     ext = tuple(ocv.output_extent(n, stride=stride) for n in shape[2:])
     assert tuple(y.shape) == (shape[0], *ext, out_c)
     check_single_rounding(host(y), x.astype(np.float64), w.astype(np.float64), b.astype(np.float64), stride)
+
+
+@pytest.mark.parametrize(("shape", "c0", "out_c"), [
+    ((2, 128, 6, 7, 13), 64, 128),    # two inputs, two output tiles, partial bricks, batch 2
+    ((1, 192, 5, 11, 21), 128, 64),   # three chunks (two from the first input)
+    ((1, 64, 4, 5, 10), 64, 64),      # exactly one brick
+])
+def test_conv3d_fuses_concat_bias_shift_residual_scale(pkg, dev, shape, c0, out_c) -> None:
+    """concat([x, skip]) read from two tensors without forming it, a per-batch-item fp32
+    bias, an fp16 shift, output scale and residual, one rounding of the sum (no input
+    transform: the shapes every 3x3x3 kernel takes)."""
+    rng = np.random.default_rng(sum(shape) + c0)
+    x, w, _ = case(shape, out_c, 3, sum(shape))
+    bias = rng.normal(size=(shape[0], out_c)).astype(np.float32)
+    shift = rng.normal(size=(shape[0], out_c)).astype(np.float16)
+    res = rng.normal(size=(shape[0], out_c, *shape[2:])).astype(np.float16)
+    scale = 0.5
+    x0t, x1t = to_dev(ndhwc(x[:, :c0]), dev), to_dev(ndhwc(x[:, c0:]), dev)
+    y = pkg.ops.nax_conv3d(x0t, pkg.ops.pack_weight(to_dev(w, dev)), to_dev(bias, dev), x1=x1t,
+                           shift=to_dev(shift, dev), residual=to_dev(ndhwc(res), dev), output_scale=scale)
+    torch.cuda.synchronize()
+    x64, w64 = x.astype(np.float64), w.astype(np.float64)
+    products = ocv.conv3d(x64, w64)
+    add = bias.astype(np.float64) + shift.astype(np.float64)
+    expected = (products + add[:, :, None, None, None]) * scale + res
+    mag = ocv.conv3d_magnitude(x64, w64)
+    err = np.abs(ncdhw(host(y)) - expected)
+    assert np.all(err <= half_spacing(expected) + ACCUMULATION_EPS * mag * scale)
+    assert_fp16_bar(ncdhw(host(y)), expected)
 
 
 def test_conv3d_reads_a_strided_channel_slice(pkg, dev) -> None:
