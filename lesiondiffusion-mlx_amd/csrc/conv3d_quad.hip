@@ -43,6 +43,7 @@ constexpr int PU = 9;                   // 16-byte units per halo voxel (8 + 1 o
 constexpr int RP = 68;                  // floats per epilogue row: 64 channels + 4 of padding
 constexpr int NA = 4;                   // weight operand sets in flight (three taps ahead)
 constexpr unsigned OOB = 0xfffffff0u;   // a buffer offset past every extent: reads zeros
+constexpr int TB = 4;                   // tap at whose start the halo's last planes are awaited
 
 // Smallest x >= base with x = r (mod 16).
 constexpr int up16(int base, int r) { return base + ((r - base) % 16 + 16) % 16; }
@@ -52,24 +53,31 @@ struct QShape {
   static constexpr int V = TD * TH * TW;            // voxels per brick
   static constexpr int NCOL = (V + 31) / 32;        // 32-voxel MFMA columns
   static_assert(NCOL <= 7, "at most seven columns (224 voxels) per brick");
+  // Column groups: group 0 takes columns [0, NC0), group 1 [NC0, NCOL). Group 0 is the
+  // smaller: its waves finish the tap loop first and reduce their columns while group 1
+  // still runs MFMAs.
+  static constexpr int NC0 = NCOL / 2, NC1 = NCOL - NC0;
+  static_assert(NC1 <= 4, "at most four columns per group");
   static constexpr int HD = TD + 2, HH = TH + 2, HW = TW + 2;
   // Unit of brick voxel (vd, vh, vw) in the halo: vd PSU + vh RSU + vw PU, which is 9 v
   // (mod 16) for the voxel's raster index v = (vd TH + vh) TW + vw.
   static constexpr int RU = HW * PU;                // units of a row holding voxels
   static constexpr int RDMA = (RU + 63) / 64;       // 64-lane DMAs per row
-  // Rows at least RDMA * 64 units apart, so that a row's DMAs never reach the next row.
-  static constexpr int RSU = up16(RDMA * 64, (9 * TW) % 16);
+  static constexpr int RLAST = RU - 64 * (RDMA - 1);   // lanes of a row's last DMA
+  static constexpr int RSU = up16(RU, (9 * TW) % 16);
   static constexpr int PSU = up16(HH * RSU, (9 * TW * TH) % 16);
   static constexpr int HALO = HD * PSU * 16;
   static constexpr int NROW = HD * HH;              // halo rows (along W)
   static constexpr int RPW = (NROW + 7) / 8;        // rows per wave
-  static constexpr int NC0 = NCOL < 4 ? NCOL : 4;   // columns of group 0 (the first round)
-  static constexpr int NC1 = NCOL - NC0;            // columns of group 1 (the second round)
-  static constexpr int EPI = 4 * NC0 * 32 * RP * 4;
-  static constexpr int MST = 8 * 32 * 3 * 4;         // per-wave GroupNorm moments, past the rows
-  static constexpr int LDS = HALO > EPI + MST ? HALO : EPI + MST;
-  static constexpr int NV0 = V < 128 ? V : 128;      // voxels of the first epilogue round
-  static constexpr int NI0 = (NV0 * 8 + NT - 1) / NT, NI1 = ((V - NV0) * 8 + NT - 1) / NT;
+  // Group 0's exchange, past the halo: for each of its columns, the partial sums of the
+  // three quarters that do not own it (8 KB each, in the MFMA lane layout), then a counter.
+  static constexpr int G0X = HALO;
+  static constexpr int CNT = G0X + NC0 * 3 * 8192;
+  // Group 1's epilogue rows (after the barrier that ends the tap loops): [quarter][column]
+  // [voxel] rows of RP floats; the GroupNorm moments past them.
+  static constexpr int EPI = 4 * 4 * 32 * RP * 4;
+  static constexpr int MST = EPI;
+  static constexpr int LDS = CNT + 16 > MST + 8 * 32 * 3 * 4 ? CNT + 16 : MST + 8 * 32 * 3 * 4;
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert((2 * PSU + 2 * RSU + 2 * PU) * 16 < 65536, "tap offsets fit the ds_read immediate");
 };
@@ -101,19 +109,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const int vol = p.D * p.H * p.W;
 
   // ---- halo DMA lanes: unit u = 64 h + lane of a halo row is voxel hw = u / PU, 16-byte
-  // channel group q = u % PU. Units past the row's voxels and the padding unit q = 8 load
-  // zeros (they are never read); so do voxels outside the volume, which are the conv's
-  // zero padding.
+  // channel group q = u % PU. The padding unit q = 8 loads zeros (it is never read); so do
+  // voxels outside the volume, which are the conv's zero padding. A row's last DMA runs on
+  // its first RLAST lanes only, so that no DMA writes past its row.
   bool lok[S::RDMA];
   unsigned lpos[S::RDMA];
 #pragma unroll
   for (int h = 0; h < S::RDMA; h++) {
     const int u = 64 * h + lane, hw = u / PU, q = u - hw * PU;
     const int iw = w0 - 1 + hw;
-    lok[h] = u < S::RU && q < 8 && (unsigned)iw < (unsigned)p.W;
+    lok[h] = q < 8 && (unsigned)iw < (unsigned)p.W;
     lpos[h] = (unsigned)(iw * 65536 + q * 16);   // voxel along W, byte of its channel group
   }
-  // Chunk j's halo: the wave's rows r = wave + 8 i, RDMA DMAs of 1 KB each.
+  // Chunk j's halo: the wave's rows r = wave + 8 i, RDMA DMAs of 1 KB each; first the rows
+  // of planes 0 .. TD - 1 (all the taps kd = 0 read), then the last two planes. Returns the
+  // number of DMAs of the second part.
   auto halo_dma = [&](int j) {
     const int c0 = j * KC;
     const bool in0 = c0 < p.C0;
@@ -124,26 +134,52 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     unsigned lo[S::RDMA];
 #pragma unroll
     for (int h = 0; h < S::RDMA; h++) lo[h] = (lpos[h] >> 16) * pitch2 + (lpos[h] & 0xffffu) + cb;
-    unsigned m0 = lds_offset(smem) + (unsigned)((wave / S::HH) * S::PSU + (wave % S::HH) * S::RSU) * 16u;
-    int hd = wave / S::HH, hh = wave % S::HH;
+    unsigned m0[S::RPW], roff[S::RPW];
+    bool rowok[S::RPW];
+    {
+      int hd = wave / S::HH, hh = wave % S::HH;
+#pragma unroll
+      for (int i = 0; i < S::RPW; i++) {
+        const int id = d0 - 1 + hd, ih = h0 - 1 + hh;
+        rowok[i] = wave + 8 * i < S::NROW && (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H;
+        roff[i] = (unsigned)((id * p.H + ih) * p.W) * pitch2;
+        m0[i] = lds_offset(smem) + (unsigned)(hd * S::PSU + hh * S::RSU) * 16u;
+        hh += 8;
+#pragma unroll
+        for (int k = 0; k < 8 / S::HH + 1; k++)
+          if (hh >= S::HH) { hh -= S::HH; hd += 1; }
+      }
+    }
+    int late = 0;
+#pragma unroll
+    for (int part = 0; part < 2; part++) {
+#pragma unroll
+      for (int h = 0; h < S::RDMA - 1; h++)
+#pragma unroll
+        for (int i = 0; i < S::RPW; i++) {
+          const int r = wave + 8 * i;
+          if (r < S::NROW && (r < TD * S::HH) == (part == 0))
+            dma_buffer_b128(rs, rowok[i] && lok[h] ? lo[h] + roff[i] : OOB, 0, m0[i] + 1024u * h);
+        }
+      if (lane < S::RLAST) {
+        constexpr int h = S::RDMA - 1;
+#pragma unroll
+        for (int i = 0; i < S::RPW; i++) {
+          const int r = wave + 8 * i;
+          if (r < S::NROW && (r < TD * S::HH) == (part == 0))
+            dma_buffer_b128(rs, rowok[i] && lok[h] ? lo[h] + roff[i] : OOB, 0, m0[i] + 1024u * h);
+        }
+      }
+    }
 #pragma unroll
     for (int i = 0; i < S::RPW; i++) {
-      if (wave + 8 * i >= S::NROW) break;
-      const int id = d0 - 1 + hd, ih = h0 - 1 + hh;
-      const bool rowok = (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H;
-      const unsigned roff = (unsigned)((id * p.H + ih) * p.W) * pitch2;
-#pragma unroll
-      for (int h = 0; h < S::RDMA; h++) dma_buffer_b128(rs, rowok && lok[h] ? lo[h] + roff : OOB, 0, m0 + 1024u * h);
-      // next row of this wave: eight rows on
-      hh += 8;
-      m0 += 8u * S::RSU * 16u;
-#pragma unroll
-      for (int k = 0; k < 8 / S::HH + 1; k++)
-        if (hh >= S::HH) { hh -= S::HH; hd += 1; m0 += (unsigned)(S::PSU - S::HH * S::RSU) * 16u; }
+      const int r = wave + 8 * i;
+      if (r < S::NROW && r >= TD * S::HH) late += S::RDMA;
     }
+    return late;
   };
 
-  // ---- weight fragments: (tile o, tap t, k-step 4 j + wave) of output block 2 oblk + o,
+  // ---- weight fragments: (tile o, tap t, k-step 4 j + sq) of output block 2 oblk + o,
   // 1 KB each, the lane's 16 bytes at lane * 16. wa walks the taps of a chunk.
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (unsigned)(p.O * 27 * p.NKC * 32));
   const unsigned voffa = (unsigned)(lane * 16 + sq * 1024);
@@ -156,17 +192,19 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   };
 
   f32x16 acc[4][2];
+  int* cnt = reinterpret_cast<int*>(smem + S::CNT);
+  if (tid == 0) *cnt = 0;   // ordered before its use by the barrier of the first chunk
 
-  // The wave's column group G (NC columns, 4 G .. 4 G + NC - 1), all chunks.
+  // The wave's column group G (NC columns from CB), all chunks.
   auto body = [&](auto gc) {
     constexpr int G = decltype(gc)::value;
-    constexpr int NC = G == 0 ? S::NC0 : S::NC1;
-    // ---- halo fragments: column 4 G + c's lane reads voxel min(32 (4 G + c) + lane % 32,
+    constexpr int NC = G == 0 ? S::NC0 : S::NC1, CB = G == 0 ? 0 : S::NC0;
+    // ---- halo fragments: column CB + c's lane reads voxel min(32 (CB + c) + lane % 32,
     // V - 1), channels 16 sq + 8 (lane / 32) .. + 7.
     int bb[NC > 0 ? NC : 1];
 #pragma unroll
     for (int c = 0; c < NC; c++) {
-      int v = 32 * (4 * G + c) + (lane & 31);
+      int v = 32 * (CB + c) + (lane & 31);
       if (v > S::V - 1) v = S::V - 1;
       const int vw = v % TW, vh = (v / TW) % TH, vd = v / (TW * TH);
       bb[c] = ((vd * S::PSU + vh * S::RSU + vw * PU) + 2 * sq + (lane >> 5)) * 16;
@@ -177,7 +215,7 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // barrier, then the 27 taps. FIRST: the accumulators start from the first MFMA (C = 0).
     auto run_chunk = [&](int j, auto first) {
       constexpr bool FIRST = decltype(first)::value;
-      halo_dma(j);
+      const int late = halo_dma(j);
       if constexpr (NC > 0) {
         // Per-chunk weight walk; the asm keeps the step opaque, so that no tap's offset is
         // computed once outside the chunk loop and held for the whole kernel.
@@ -187,16 +225,29 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         wa = (unsigned)(oblk * 2) * wob + (unsigned)(4 * j * 1024);
 #pragma unroll
         for (int t = 0; t < NA - 1; t++) load_a(aq[t]);
-        vmcnt_wait<(NA - 1) * 2>();   // the halo has landed (the weights may be in flight)
+        // The first TD planes of the halo have landed once at most the last planes' DMAs
+        // and the weight requests are in flight (the count is wave-uniform).
+        static_assert(2 * S::RDMA <= 8, "late DMA counts handled below");
+        if (late == 0) vmcnt_wait<(NA - 1) * 2>();
+        else if (late == S::RDMA) vmcnt_wait<(NA - 1) * 2 + S::RDMA>();
+        else vmcnt_wait<(NA - 1) * 2 + 2 * S::RDMA>();
       } else {
         vmcnt_wait<0>();
       }
       __syncthreads();
+      if constexpr (NC == 0) __syncthreads();   // the tap loop's barrier
       if constexpr (NC > 0) {
 #pragma unroll
         for (int c = 0; c < NC; c++) bq[0][c] = *reinterpret_cast<const E8*>(smem + bb[c]);
 #pragma unroll
         for (int t = 0; t < 27; t++) {
+          if (t == TB) {
+            // The last planes, first read by the taps kd = 1 (whose fragments are requested
+            // from tap 8 on): every wave's DMAs have landed once its weight requests older
+            // than tap TB's have.
+            vmcnt_wait<(NA - 1) * 2>();
+            __syncthreads();
+          }
           // Issue order, pinned by scheduling barriers: per column the MFMA pair of this
           // tap, then that column's halo fragment of the next tap (it has a tap of MFMAs to
           // land in); the weight requests after the first pair.
@@ -226,10 +277,10 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   if (grp == 0) body(std::integral_constant<int, 0>{});
   else body(std::integral_constant<int, 1>{});
 
-  // ---- epilogue
+  // ---- epilogue operands: bias (+ per-batch-item bias) + fp16 shift of the thread's 8
+  // channels (channels 8 (lane % 8) .. + 7 of the tile in every row layout below)
   const int col = lane & 31, hf = lane >> 5, g8 = tid & 7;
   const int o8 = oblk * 64 + g8 * 8;
-  // bias (+ per-batch-item bias) + fp16 shift of this thread's 8 channels
   float bs[8];
   {
     f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
@@ -250,48 +301,146 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   const __amdgpu_buffer_rsrc_t yr = make_rsrc(p.y, (unsigned)(p.B * vol) * (unsigned)p.yp * 2u);
   const __amdgpu_buffer_rsrc_t rr = make_rsrc(p.res, p.res ? (unsigned)(p.B * vol) * (unsigned)p.resp * 2u : 0u);
   const bool has_res = p.res != nullptr, scaled = p.scale != 1.0f;
-  float* rows = reinterpret_cast<float*>(smem);
-  // The stored values and their validity, kept for the GroupNorm moments.
-  E8 outv[S::NI0 + S::NI1 > 0 ? S::NI0 + S::NI1 : 1];
-  bool okv[S::NI0 + S::NI1 > 0 ? S::NI0 + S::NI1 : 1];
-  auto round = [&](auto kc) {
-    constexpr int K = decltype(kc)::value;
-    constexpr int NCR = K == 0 ? S::NC0 : S::NC1;
-    constexpr int NV = K == 0 ? S::NV0 : S::V - S::NV0;   // voxels of the round
-    constexpr int NU = NV * 8, NI = K == 0 ? S::NI0 : S::NI1, I0 = K == 0 ? 0 : S::NI0;
-    // This thread's outputs of the round (voxel 128 K + 64 i + tid / 8), and their
-    // residual rows, requested first.
-    unsigned ovr[NI > 0 ? NI : 1];
-    E8 res[NI > 0 ? NI : 1];
+  // The stored values and their validity, kept for the GroupNorm moments: units 0..3 of a
+  // group-0 owner, units 4..5 of the final round.
+  E8 outv[6] = {};
+  bool okv[6] = {false, false, false, false, false, false};
+  // Output voxel of brick voxel v (okv: inside the volume), and its residual row.
+  auto locate = [&](int v, bool valid, unsigned& ovr, E8& res) {
+    const int vd = v / (TW * TH), rv = v - vd * (TW * TH), vh = rv / TW, vw = rv - vh * TW;
+    const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
+    const bool ok = valid && v < S::V && od < p.D && oh < p.H && ow < p.W;
+    ovr = (unsigned)(b * vol + (od * p.H + oh) * p.W + ow);
+    res = (E8){};
+    if (has_res && ok) res = buffer_load16<E8>(rr, (ovr * (unsigned)p.resp + o8) * 2u);
+    return ok;
+  };
+  // One row of summed partials (8 channels at r0, 8 at r0 + 4): bias, shift, scale,
+  // residual, one rounding, one 16-byte store.
+  auto finish = [&](f32x4 s0, f32x4 s1, const E8& res, unsigned ovr, E8& out) {
+    float f[8];
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-      const int v = 128 * K + 64 * i + (tid >> 3);
-      const int vd = v / (TW * TH), rv = v - vd * (TW * TH), vh = rv / TW, vw = rv - vh * TW;
-      const int od = d0 + vd, oh = h0 + vh, ow = w0 + vw;
-      okv[I0 + i] = (i * NT + tid < NU) && od < p.D && oh < p.H && ow < p.W;
-      ovr[i] = (unsigned)(b * vol + (od * p.H + oh) * p.W + ow);
-      res[i] = (E8){};
-      if (has_res && okv[I0 + i]) res[i] = buffer_load16<E8>(rr, (ovr[i] * (unsigned)p.resp + o8) * 2u);
+    for (int e = 0; e < 4; e++) {
+      f[e] = s0[e] + bs[e];
+      f[e + 4] = s1[e] + bs[e + 4];
     }
-    if (K > 0) __syncthreads();   // the previous round's rows have been read
-    if (grp == K) {
+    if (scaled) {
 #pragma unroll
-      for (int cl = 0; cl < NCR; cl++)
+      for (int e = 0; e < 8; e++) f[e] *= p.scale;
+    }
+    if (has_res) {
+#pragma unroll
+      for (int e = 0; e < 8; e++) f[e] += (float)res[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) out[e] = (E)f[e];
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, out), yr, (int)((ovr * (unsigned)p.yp + o8) * 2u),
+                                           0, 0);
+  };
+  // Partial sums of column c's tile o as four 16-byte pieces per lane (MFMA layout) at
+  // slot base sb: piece jj of lane l at sb + ((o * 4 + jj) * 64 + l) * 16.
+  float* rows = reinterpret_cast<float*>(smem);
+
+  // ---- group 0: reduce its columns while group 1 still runs its tap loop. Column c's
+  // owner is quarter c; the other three quarters leave their sums in the owner's slots,
+  // count themselves in, and the owner waits for all four, adds the quarters in order, and
+  // finishes the column through rows of its own (the slots it has read).
+  if constexpr (S::NC0 > 0) {
+    if (grp == 0) {
+      char* g0x = smem + S::G0X;
+#pragma unroll
+      for (int c = 0; c < S::NC0; c++) {
+        if (c == sq) continue;
+        const int k = sq < c ? sq : sq - 1;
+        char* sb = g0x + (c * 3 + k) * 8192;
 #pragma unroll
         for (int o = 0; o < 2; o++)
 #pragma unroll
           for (int jj = 0; jj < 4; jj++) {
-            const f32x16& a = acc[cl][o];
-            const f32x4 v = {a[4 * jj], a[4 * jj + 1], a[4 * jj + 2], a[4 * jj + 3]};
+            const f32x4 v = {acc[c][o][4 * jj], acc[c][o][4 * jj + 1], acc[c][o][4 * jj + 2], acc[c][o][4 * jj + 3]};
+            *reinterpret_cast<f32x4*>(sb + ((o * 4 + jj) * 64 + lane) * 16) = v;
+          }
+      }
+      // The writes above are performed before the count (LDS requests of a wave complete
+      // in order); the owner reads the slots only after all four quarters counted in.
+      __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+      if (lane == 0) __hip_atomic_fetch_add(cnt, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      while (__hip_atomic_load(cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 4) __builtin_amdgcn_s_sleep(1);
+      auto owner = [&](auto cc) {
+        constexpr int C = decltype(cc)::value;
+        char* sb = g0x + C * 3 * 8192;
+        f32x16 sum[2];
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+#pragma unroll
+          for (int o = 0; o < 2; o++) {
+            f32x16 v;
+            if (q == C) {
+              v = acc[C][o];
+            } else {
+              const char* src = sb + (q < C ? q : q - 1) * 8192;
+#pragma unroll
+              for (int jj = 0; jj < 4; jj++) {
+                const f32x4 x = *reinterpret_cast<const f32x4*>(src + ((o * 4 + jj) * 64 + lane) * 16);
+                v[4 * jj] = x[0]; v[4 * jj + 1] = x[1]; v[4 * jj + 2] = x[2]; v[4 * jj + 3] = x[3];
+              }
+            }
+            sum[o] = q == 0 ? v : sum[o] + v;
+          }
+        // The column's 32 voxels, transposed into rows over the slots just read.
+        float* tr = reinterpret_cast<float*>(sb);
+#pragma unroll
+        for (int o = 0; o < 2; o++)
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const f32x4 v = {sum[o][4 * jj], sum[o][4 * jj + 1], sum[o][4 * jj + 2], sum[o][4 * jj + 3]};
+            *reinterpret_cast<f32x4*>(tr + col * RP + 32 * o + 8 * jj + 4 * hf) = v;
+          }
+        unsigned ovr[4];
+        E8 res[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) okv[i] = locate(32 * C + (lane >> 3) + 8 * i, true, ovr[i], res[i]);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          if (!okv[i]) continue;
+          const float* r0 = tr + ((lane >> 3) + 8 * i) * RP + g8 * 8;
+          finish(*reinterpret_cast<const f32x4*>(r0), *reinterpret_cast<const f32x4*>(r0 + 4), res[i], ovr[i],
+                 outv[i]);
+        }
+      };
+      if (sq == 0) owner(std::integral_constant<int, 0>{});
+      if constexpr (S::NC0 > 1) if (sq == 1) owner(std::integral_constant<int, 1>{});
+      if constexpr (S::NC0 > 2) if (sq == 2) owner(std::integral_constant<int, 2>{});
+    }
+  }
+
+  // ---- group 1's columns, after every tap loop: the four group-1 waves write their
+  // partial sums as rows [quarter][column][voxel]; any thread then takes 8 channels of a
+  // voxel (units i = 0, 1: row 64 i + tid / 8), adds the quarters in order and finishes.
+  {
+    unsigned ovr[2];
+    E8 res[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int r = 64 * i + (tid >> 3);
+      okv[4 + i] = locate(32 * S::NC0 + r, (r >> 5) < S::NC1, ovr[i], res[i]);
+    }
+    __syncthreads();   // every wave done with the halo and the group-0 exchange
+    if (grp == 1) {
+#pragma unroll
+      for (int cl = 0; cl < S::NC1; cl++)
+#pragma unroll
+        for (int o = 0; o < 2; o++)
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const f32x4 v = {acc[cl][o][4 * jj], acc[cl][o][4 * jj + 1], acc[cl][o][4 * jj + 2], acc[cl][o][4 * jj + 3]};
             *reinterpret_cast<f32x4*>(rows + ((sq * 4 + cl) * 32 + col) * RP + 32 * o + 8 * jj + 4 * hf) = v;
           }
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-      E8& out = outv[I0 + i];
-      out = (E8){};
-      if (!okv[I0 + i]) continue;
+    for (int i = 0; i < 2; i++) {
+      if (!okv[4 + i]) continue;
       const float* r0 = rows + (64 * i + (tid >> 3)) * RP + g8 * 8;
       f32x4 s0 = *reinterpret_cast<const f32x4*>(r0);
       f32x4 s1 = *reinterpret_cast<const f32x4*>(r0 + 4);
@@ -301,36 +450,16 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         s0 += *reinterpret_cast<const f32x4*>(rw);
         s1 += *reinterpret_cast<const f32x4*>(rw + 4);
       }
-      float f[8];
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        f[e] = s0[e] + bs[e];
-        f[e + 4] = s1[e] + bs[e + 4];
-      }
-      if (scaled) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) f[e] *= p.scale;
-      }
-      if (has_res) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) f[e] += (float)res[i][e];
-      }
-#pragma unroll
-      for (int e = 0; e < 8; e++) out[e] = (E)f[e];
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, out), yr,
-                                             (int)((ovr[i] * (unsigned)p.yp + o8) * 2u), 0, 0);
+      finish(s0, s1, res[i], ovr[i], outv[4 + i]);
     }
-  };
-  __syncthreads();   // every wave done with the halo
-  round(std::integral_constant<int, 0>{});
-  if constexpr (S::NC1 > 0) round(std::integral_constant<int, 1>{});
+  }
 
   // GroupNorm partial moments of the stored values, one block per brick: each wave's
   // channel pairs over its voxels (lanes l, l + 8, ... hold the same 8 channels) into LDS
   // past the epilogue rows, then thread pp < 32 merges pair pp over the eight waves in order.
   if (p.stats) {
-    float* mst = reinterpret_cast<float*>(smem + S::EPI);   // [8 waves][32 pairs][3]
-    pair_moments<S::NI0 + S::NI1, 8>(outv, okv, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
+    float* mst = reinterpret_cast<float*>(smem + S::MST);   // [8 waves][32 pairs][3]
+    pair_moments<6, 8>(outv, okv, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
     __syncthreads();
     if (tid < 32) {
       Moments m = {0.f, 0.f, 0.f};
