@@ -130,6 +130,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_timestep_embedding": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_silu": (c_i32, [c_vp, c_i64, c_vp, c_vp]),
     "ldx_copy_channels": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i64, c_i32, c_vp]),
+    "ldx_group_norm_apply": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i32, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32,
+                                     c_vp]),
     "ldx_upsample_nearest2": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "ldx_ddim_prepare": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "ldx_ddim_update": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp]),
@@ -150,7 +152,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            c_vp]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 
 def _load() -> ctypes.CDLL:

@@ -524,6 +524,8 @@ bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* out) {
   const int64_t nwg = nb * (a->out_c / 64) * a->batch;
   if (nwg > 0x7fffffff) return false;
   if (force != 1) {
+    // Grids that leave CUs idle go to the kernels built for them.
+    if (nwg < 200) return false;
     // Modelled workgroup time (cycles per 64 input channels): MFMA cycles of the busiest
     // SIMD at the measured main-loop efficiency of each kernel, plus the per-workgroup
     // fixed cost, times the rounds of workgroups over 256 CUs. The streamed kernel's brick
