@@ -20,6 +20,7 @@ struct QuadParams {
   const E* w;
   const float* bias; int bias_batched;
   const E* shift; int64_t shiftp;
+  const float* affine; int silu;   // GroupNorm affine (B, C, 2) and SiLU of the input, or none
   const E* res; int64_t resp;
   float scale;
   E* y; int64_t yp;
@@ -28,9 +29,8 @@ struct QuadParams {
 };
 
 // True (and *p planned, bricks counted) when the K-quarter kernel takes this conv: a 3x3x3
-// stride-1 conv with 64-channel input chunks and 64-channel output tiles and no input
-// transform, whose modelled time beats the streamed kernel's (LDX_CONV_QUAD=1 takes every
-// eligible shape, =0 none).
+// stride-1 conv with 64-channel input chunks and 64-channel output tiles, whose modelled
+// time beats the streamed kernel's (LDX_CONV_QUAD=1 takes every eligible shape, =0 none).
 bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* p);
 int conv3d_quad_launch(QuadParams& p, hipStream_t st);
 

@@ -1,7 +1,7 @@
 // K-quarter implicit-GEMM 3x3x3 stride-1 convolution on gfx950 MFMA
 // (v_mfma_f32_32x32x16_f16 / _bf16) for volumes whose bricks of at most 224 voxels fill the
 // GPU: input channels in 64-channel chunks, output channels in 64-channel tiles, 16-byte
-// aligned NDHWC rows, no input transform.
+// aligned NDHWC rows, with or without the GroupNorm affine + SiLU input transform.
 //
 // Workgroup: 8 waves, two per SIMD (one workgroup per CU). The workgroup owns one brick of
 // V <= 224 voxels (NCOL = ceil(V / 32) MFMA columns) x 64 output channels. The two waves
@@ -11,8 +11,10 @@
 // halo fragments for 8 MFMAs (a SIMD: 10 fragments per 14 MFMAs at NCOL = 7, against one
 // per MFMA for a 2 x 2 register block).
 //
-// Operands: the brick's halo (64 channels) is copied global -> LDS by DMA once per chunk,
-// in rows along W of 9 16-byte units per voxel (8 of channels, 1 of padding) with row and
+// Operands: the brick's halo (64 channels) is copied global -> LDS by DMA once per chunk
+// (with the input transform: loaded into registers, transformed -- fp32 affine, SiLU, one
+// fp16 rounding -- and written), in rows along W of 9 16-byte units per voxel (8 of
+// channels, 1 of padding) with row and
 // plane strides padded so that the halo unit of the brick's raster voxel v is 9 v (mod 16):
 // any 16 consecutive voxels of a column hit 16 distinct bank groups at every tap offset.
 // Each tap's offset is a compile-time constant, so a halo fragment is one ds_read_b128 at
@@ -69,6 +71,8 @@ struct QShape {
   static constexpr int HALO = HD * PSU * 16;
   static constexpr int NROW = HD * HH;              // halo rows (along W)
   static constexpr int RPW = (NROW + 7) / 8;        // rows per wave
+  static constexpr int NXU = NROW * HW * 8;          // 16-byte data units of a halo
+  static constexpr int XPT = (NXU + NT - 1) / NT;    // of them per thread (input transform)
   // Group 0's exchange, past the halo: for each of its columns, the partial sums of the
   // three quarters that do not own it (8 KB each, in the MFMA lane layout), then a counter.
   static constexpr int G0X = HALO;
@@ -84,7 +88,7 @@ struct QShape {
 
 __device__ __forceinline__ f32x16 mfma(E8 a, E8 b, f32x16 c) { return mfma_e(a, b, c); }
 
-template <int TD, int TH, int TW>
+template <int TD, int TH, int TW, bool XF>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv3q_kernel(QuadParams p) {
   using S = QShape<TD, TH, TW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -179,6 +183,63 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     return late;
   };
 
+  // Chunk j's halo through registers with the GroupNorm affine + SiLU prologue: unit
+  // u = i * NT + tid is halo row u / (HW * 8), voxel (u / 8) % HW, channel group u % 8 =
+  // tid % 8 (one affine per thread). The arithmetic is the streamed kernel's (fp32 multiply-
+  // add, silu_f, one rounding); voxels outside the volume are zero after the transform
+  // (the conv pads the normalised input). The loads are asm, awaited explicitly.
+  auto halo_xf = [&](int j) __attribute__((always_inline)) {
+    const int c0 = j * KC;
+    const bool in0 = c0 < p.C0;
+    const E* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
+    const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
+    const i32x4 rs = dma_rsrc(base, (unsigned)vol * pitch2);
+    const unsigned cb = (unsigned)((in0 ? c0 : c0 - p.C0) * 2);
+    const int q = tid & 7;
+    const i32x4 ra = dma_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine, p.affine ? (unsigned)(p.C * 8) : 0u);
+    f32x4 af[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) af[k] = __builtin_bit_cast(f32x4, buffer_load16_asm(ra, (unsigned)((c0 + q * 8) * 8 + k * 16)));
+    // Two batches of units, so that a later chunk's staging fits beside the live
+    // accumulators.
+    constexpr int XB = (S::XPT + 1) / 2;
+#pragma unroll
+    for (int b0 = 0; b0 < S::XPT; b0 += XB) {
+      E8 xv[XB];
+      int dst[XB];
+      bool in[XB];
+#pragma unroll
+      for (int ii = 0; ii < XB; ii++) {
+        const int u = (b0 + ii) * NT + tid;
+        const int r = u / (S::HW * 8), hw = (u / 8) % S::HW;
+        const int hd = r / S::HH, hh = r - hd * S::HH;
+        const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
+        in[ii] = b0 + ii < S::XPT && u < S::NXU && (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H &&
+                 (unsigned)iw < (unsigned)p.W;
+        dst[ii] = b0 + ii < S::XPT && u < S::NXU ? (hd * S::PSU + hh * S::RSU + hw * PU + q) * 16 : -1;
+        xv[ii] = buffer_load16_asm<E8>(rs, in[ii] ? (unsigned)((id * p.H + ih) * p.W + iw) * pitch2 + cb + q * 16 : OOB);
+      }
+      vmcnt_wait<0>();
+#pragma unroll
+      for (int k = 0; k < 4; k++) pin_value(af[k]);
+#pragma unroll
+      for (int ii = 0; ii < XB; ii++) {
+        pin_value(xv[ii]);
+        if (dst[ii] < 0) continue;
+        E8 v = xv[ii];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float sc = p.affine ? af[e >> 1][(e & 1) * 2] : 1.f;
+          const float of = p.affine ? af[e >> 1][(e & 1) * 2 + 1] : 0.f;
+          float yv = (float)v[e] * sc + of;
+          if (p.silu) yv = silu_f(yv);
+          v[e] = in[ii] ? (E)yv : (E)0;
+        }
+        *reinterpret_cast<E8*>(smem + dst[ii]) = v;
+      }
+    }
+  };
+
   // ---- weight fragments: (tile o, tap t, k-step 4 j + sq) of output block 2 oblk + o,
   // 1 KB each, the lane's 16 bytes at lane * 16. wa walks the taps of a chunk.
   const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.w, (unsigned)(p.O * 27 * p.NKC * 32));
@@ -215,16 +276,21 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // barrier, then the 27 taps. FIRST: the accumulators start from the first MFMA (C = 0).
     auto run_chunk = [&](int j, auto first) {
       constexpr bool FIRST = decltype(first)::value;
-      const int late = halo_dma(j);
+      // With the input transform the halo is staged through registers first, while no
+      // weight operands are held: a later chunk's staging runs beside live accumulators.
+      if constexpr (XF) halo_xf(j);
+      const int late = XF ? 0 : halo_dma(j);
       if constexpr (NC > 0) {
         // Per-chunk weight walk; the asm keeps the step opaque, so that no tap's offset is
         // computed once outside the chunk loop and held for the whole kernel.
-        wstep = (unsigned)(p.NKC * 1024);
+        wstep = (unsigned)__builtin_amdgcn_readfirstlane(p.NKC * 1024);
         asm volatile("" : "+s"(wstep));
         wob = 27u * wstep;
         wa = (unsigned)(oblk * 2) * wob + (unsigned)(4 * j * 1024);
 #pragma unroll
         for (int t = 0; t < NA - 1; t++) load_a(aq[t]);
+      }
+      if constexpr (NC > 0) {
         // The first TD planes of the halo have landed once at most the last planes' DMAs
         // and the weight requests are in flight (the count is wave-uniform).
         static_assert(2 * S::RDMA <= 8, "late DMA counts handled below");
@@ -481,7 +547,7 @@ static int launch(QuadParams& p, hipStream_t st) {
   p.dv_nbr = make_udiv((unsigned)p.nbr);
   p.dv_nbw = make_udiv((unsigned)p.NBW);
   p.dv_nbh = make_udiv((unsigned)p.NBH);
-  auto kern = conv3q_kernel<TD, TH, TW>;
+  auto kern = p.affine || p.silu ? conv3q_kernel<TD, TH, TW, true> : conv3q_kernel<TD, TH, TW, false>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS) != hipSuccess)
     return check_launch("conv3d (K-quarter): set LDS size");
   const int64_t nwg = (int64_t)p.nbr * p.nob * p.B;
@@ -502,7 +568,6 @@ bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* out) {
   if (const char* env = getenv("LDX_CONV_QUAD")) force = atoi(env);
   if (force == 0) return false;
   if (a->ksize != 3 || a->stride != 1 || a->upsample || a->act != LDX_ACT_NONE) return false;
-  if (a->affine || a->silu) return false;
   if (a->c0 % KC || a->c1 % KC || a->out_c % 64) return false;
   if (a->c1 > 0 && !a->x1) return false;
   if (a->x0_pitch % 8 || (a->c1 > 0 && a->x1_pitch % 8)) return false;
@@ -526,6 +591,12 @@ bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* out) {
   if (force != 1) {
     // Grids that leave CUs idle go to the kernels built for them.
     if (nwg < 200) return false;
+    // Several rounds of workgroups with the input transform, several channel chunks or
+    // several output tiles: the streamed kernel, whose double-buffered halo hides the next
+    // chunk's staging (measured: 64x80x80 128 -> 128 with the transform 391 against 462 us,
+    // 128x160x160 64 -> 64 949 against 1062 us; one round of 32x40x40 up to 192 -> 64
+    // channels favours this kernel by 4-6 %).
+    if (nwg > 256 && (a->affine || a->silu || a->c0 + a->c1 > KC || a->out_c > 64)) return false;
     // Modelled workgroup time (cycles per 64 input channels): MFMA cycles of the busiest
     // SIMD at the measured main-loop efficiency of each kernel, plus the per-workgroup
     // fixed cost, times the rounds of workgroups over 256 CUs. The streamed kernel's brick
@@ -549,6 +620,7 @@ bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* out) {
   p.w = (const E*)a->weight;
   p.bias = a->bias; p.bias_batched = a->bias_batched ? 1 : 0;
   p.shift = (const E*)a->shift; p.shiftp = a->shift_pitch;
+  p.affine = a->affine; p.silu = a->silu ? 1 : 0;
   p.res = (const E*)a->residual; p.resp = a->residual_pitch;
   p.scale = a->output_scale;
   p.y = (E*)a->y; p.yp = a->y_pitch;

@@ -129,6 +129,47 @@ def test_conv3d_fuses_concat_bias_shift_residual_scale(pkg, dev, shape, c0, out_
     assert_fp16_bar(ncdhw(host(y)), expected)
 
 
+@pytest.mark.parametrize(("shape", "c0", "out_c", "silu_only"), [
+    ((2, 128, 6, 7, 13), 64, 128, False),   # two inputs, two output tiles, partial bricks
+    ((1, 192, 5, 11, 21), 128, 64, False),  # three chunks
+    ((1, 64, 4, 5, 10), 64, 64, True),      # SiLU without an affine
+])
+def test_conv3d_fuses_norm_silu_concat_shift_residual(pkg, dev, shape, c0, out_c, silu_only) -> None:
+    """The GroupNorm affine + SiLU prologue on 64-channel chunks (what the K-quarter kernel
+    stages through registers) with a two-tensor concat, per-batch bias, shift, scale and
+    residual: against float64 of the normalised input rounded once to fp16."""
+    rng = np.random.default_rng(sum(shape) + 3)
+    x, w, _ = case(shape, out_c, 3, sum(shape) + 1)
+    c = shape[1]
+    bias = rng.normal(size=(shape[0], out_c)).astype(np.float32)
+    shift = rng.normal(size=(shape[0], out_c)).astype(np.float16)
+    res = rng.normal(size=(shape[0], out_c, *shape[2:])).astype(np.float16)
+    x0t = to_dev(ndhwc(x[:, :c0]), dev)
+    x1t = to_dev(ndhwc(x[:, c0:]), dev) if c0 < c else None
+    if silu_only:
+        aff = None
+        prep = onm.silu(x.astype(np.float64))
+    else:
+        gamma = rng.normal(size=(c,)).astype(np.float32)
+        beta = rng.normal(size=(c,)).astype(np.float32)
+        aff = pkg.ops.group_norm_affine(x0t, to_dev(gamma, dev), to_dev(beta, dev), groups=16, eps=1e-5, x1=x1t)
+        a = aff.cpu().numpy().astype(np.float64)
+        prep = onm.silu(x.astype(np.float64) * a[:, :, 0, None, None, None] + a[:, :, 1, None, None, None])
+    y = pkg.ops.nax_conv3d(x0t, pkg.ops.pack_weight(to_dev(w, dev)), to_dev(bias, dev), x1=x1t, affine=aff,
+                           silu=True, shift=to_dev(shift, dev), residual=to_dev(ndhwc(res), dev), output_scale=0.5)
+    torch.cuda.synchronize()
+    normalized = ocv.f16(prep)
+    w64 = w.astype(np.float64)
+    products = ocv.conv3d(normalized, w64)
+    add = bias.astype(np.float64) + shift.astype(np.float64)
+    expected = (products + add[:, :, None, None, None]) * 0.5 + res
+    mag = ocv.conv3d_magnitude(normalized, w64)
+    err = np.abs(ncdhw(host(y)) - expected)
+    # the normalised operand is rounded to fp16 on the GPU from the same fp32 affine
+    assert np.all(err <= half_spacing(expected) + (ACCUMULATION_EPS + OPERAND_ROUNDING) * mag * 0.5)
+    assert_fp16_bar(ncdhw(host(y)), expected)
+
+
 def test_conv3d_reads_a_strided_channel_slice(pkg, dev) -> None:
     """A channel slice of a wider NDHWC tensor (voxel pitch > C), as a view, not a copy."""
     x, w, b = case((1, 32, 5, 6, 7), 48, 3, 3)
@@ -486,7 +527,7 @@ def test_group_norm_apply_then_conv_equals_the_fused_conv(pkg, dev, conv_path, s
     want = onm.silu(xx * a[:, :, 0, None, None, None] + a[:, :, 1, None, None, None])
     got = np.concatenate([ncdhw(host(t0))] + ([ncdhw(host(t1))] if t1 is not None else []), axis=1)
     assert np.all(np.abs(got - want) <= 2 * half_spacing(want) + 1e-7)
-    if conv_path in ("streamed", "streamed-split"):
+    if conv_path in ("streamed", "streamed-split", "quad"):
         assert torch.equal(fused, split)
     tt = got.astype(np.float16).astype(np.float64)
     w64 = w.astype(np.float64)
