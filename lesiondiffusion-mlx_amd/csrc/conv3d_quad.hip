@@ -6,26 +6,32 @@
 // Workgroup: 8 waves, two per SIMD (one workgroup per CU). The workgroup owns one brick of
 // V <= 224 voxels (NCOL = ceil(V / 32) MFMA columns) x 64 output channels. The two waves
 // of SIMD s take the same quarter of the reduction -- channels 16 s .. 16 s + 15 of every
-// 64-channel chunk, all 27 taps -- one for columns 0..3, the other for columns 4..NCOL-1,
-// each in 2 x 4 (2 x 3) accumulator tiles: per tap a wave reads 2 weight fragments and 4
-// halo fragments for 8 MFMAs (a SIMD: 10 fragments per 14 MFMAs at NCOL = 7, against one
+// 64-channel chunk, all 27 taps -- one for column group 0 (columns 0 .. NC0 - 1, NC0 =
+// NCOL / 2), the other for group 1 (the rest), in 2 x NC accumulator tiles: per tap a wave
+// reads 2 weight fragments and NC halo fragments for 2 NC MFMAs (a SIMD at NCOL = 7: 7 halo
+// fragments from LDS and 4 weight fragments from L2 per 14 MFMAs, against one LDS fragment
 // per MFMA for a 2 x 2 register block).
 //
 // Operands: the brick's halo (64 channels) is copied global -> LDS by DMA once per chunk
 // (with the input transform: loaded into registers, transformed -- fp32 affine, SiLU, one
 // fp16 rounding -- and written), in rows along W of 9 16-byte units per voxel (8 of
-// channels, 1 of padding) with row and
-// plane strides padded so that the halo unit of the brick's raster voxel v is 9 v (mod 16):
-// any 16 consecutive voxels of a column hit 16 distinct bank groups at every tap offset.
-// Each tap's offset is a compile-time constant, so a halo fragment is one ds_read_b128 at
-// a base register plus an immediate. The weight fragments come straight from global
-// memory (L2) into registers, three taps ahead; no LDS and no barrier in the tap loop.
+// channels, 1 of padding) with row and plane strides padded so that the halo unit of the
+// brick's raster voxel v is 9 v (mod 16): any 16 consecutive voxels of a column hit 16
+// distinct bank groups at every tap offset. Each tap's offset is a compile-time constant,
+// so a halo fragment is one ds_read_b128 at a base register plus an immediate. The weight
+// fragments come straight from global memory (L2) into registers, three taps ahead; the
+// tap loop writes no LDS. The DMA path awaits the halo's first TD planes (all that the
+// taps kd = 0 read) before the tap loop and the last two at tap TB.
 //
-// Epilogue, in two rounds (columns 0..3, then 4..NCOL-1): the four waves holding the
-// round's columns write their partial sums as fp32 voxel rows to LDS; after one barrier a
-// thread of any wave takes 8 consecutive channels of a voxel, adds the four quarters in
-// order, then bias (+ per-batch-item bias) plus fp16 shift, output scale, fp16 residual,
-// one rounding, and one 16-byte store (whole 128-byte rows per 8 lanes).
+// Epilogue: group 0 has fewer columns and leaves the tap loop first. Its waves reduce their
+// columns while group 1 still runs MFMAs: quarter c owns column c, the other three leave
+// their partial sums in LDS slots past the halo and count themselves in on an LDS counter;
+// the owner adds the four quarters in order and finishes the column through LDS rows of
+// its own. After the barrier that ends every tap loop, group 1's waves write their partial
+// sums as fp32 voxel rows and every thread takes 8 consecutive channels of a voxel, adds
+// the quarters in order and finishes it. Finishing: bias (+ per-batch-item bias) plus fp16
+// shift, output scale, fp16 residual, one rounding, one 16-byte store (whole 128-byte rows
+// per 8 lanes); optionally the GroupNorm moments of the stored values, one block per brick.
 //
 // Reference semantics: nax_conv3d (src/lesiondiffusion_mlx/_nax_conv.py:451-619), epilogue
 // _nax_conv.py:265-270 (+ scaled variant :418-421).
