@@ -61,16 +61,21 @@ def check_bound(actual, expected, mag, *, rerounded: bool) -> None:
     assert_bf16_bar(actual, expected)
 
 
-@pytest.fixture(params=["default", "streamed", "streamed-split"])
+@pytest.fixture(params=["default", "streamed", "streamed-split", "quad"])
 def conv_path(request, monkeypatch):
     """The library's kernel choice; the streamed kernel for every shape it takes; that
-    kernel with its reduction split over workgroups."""
+    kernel with its reduction split over workgroups; the K-quarter kernel for every shape
+    it takes (64-channel input chunks, 64-channel output tiles)."""
+    monkeypatch.delenv("LDX_CONV_STREAM_MIN_WG", raising=False)
+    monkeypatch.delenv("LDX_CONV_QUAD", raising=False)
     if request.param == "streamed":
         monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1")
+        monkeypatch.setenv("LDX_CONV_QUAD", "0")
     elif request.param == "streamed-split":
         monkeypatch.setenv("LDX_CONV_STREAM_MIN_WG", "1000000")
-    else:
-        monkeypatch.delenv("LDX_CONV_STREAM_MIN_WG", raising=False)
+        monkeypatch.setenv("LDX_CONV_QUAD", "0")
+    elif request.param == "quad":
+        monkeypatch.setenv("LDX_CONV_QUAD", "1")
     return request.param
 
 
@@ -103,19 +108,21 @@ def test_bf16_conv3d_matches_float64(pkg, dev, conv_path, shape, out_c, stride) 
     check_bound(host(y).transpose(0, 4, 1, 2, 3), expected, mag, rerounded=False)
 
 
-def test_bf16_fused_prologue_epilogue_and_concat(pkg, dev, conv_path) -> None:
+@pytest.mark.parametrize(("c", "c0"), [(64, 32), (128, 64)])
+def test_bf16_fused_prologue_epilogue_and_concat(pkg, dev, conv_path, c, c0) -> None:
     """concat([x, skip]) through the GroupNorm affine + SiLU prologue (one bf16 rounding of
-    the prepared input), per-batch bias + bf16 shift, output scale and a bf16 residual."""
-    x, w, _ = _case((2, 64, 5, 8, 9), 64, 3, 7, offset=0.4)
+    the prepared input), per-batch bias + bf16 shift, output scale and a bf16 residual. The
+    64 + 64 split is one the K-quarter kernel takes."""
+    x, w, _ = _case((2, c, 5, 8, 9), 64, 3, 7 + c, offset=0.4)
     rng = np.random.default_rng(8)
-    gamma, beta = rng.normal(size=64), rng.normal(size=64) * 0.3
+    gamma, beta = rng.normal(size=c), rng.normal(size=c) * 0.3
     aff = onm.group_norm_affine(x, gamma, beta, groups=32, eps=1e-5)
     bias = rng.normal(size=(2, 64)) * 0.1
     shift = bf16_values(rng.normal(size=(2, 64)) * 0.1)
     res = bf16_values(rng.normal(size=(2, 64, 5, 8, 9)))
     xd = x.transpose(0, 2, 3, 4, 1)
-    y = pkg.ops.nax_conv3d(to_dev(xd[..., :32], dev), pkg.ops.pack_weight(to_dev(w, dev)),
-                           torch.from_numpy(bias).float().to(dev), x1=to_dev(xd[..., 32:], dev),
+    y = pkg.ops.nax_conv3d(to_dev(xd[..., :c0], dev), pkg.ops.pack_weight(to_dev(w, dev)),
+                           torch.from_numpy(bias).float().to(dev), x1=to_dev(xd[..., c0:], dev),
                            affine=torch.from_numpy(aff.astype(np.float32)).to(dev), silu=True,
                            shift=to_dev(shift, dev), residual=to_dev(res.transpose(0, 2, 3, 4, 1), dev),
                            output_scale=0.5)
