@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (8); bumped on any change to the structs below or the entry points. */
+/* ABI version (9); bumped on any change to the structs below or the entry points. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -203,6 +203,20 @@ int ldx_group_norm_affine_moments(const float* m0, int64_t chunks0, int32_t c0,
                                   int32_t batch, int32_t groups,
                                   const float* gamma, const float* beta, float eps,
                                   float* affine, void* stream);
+/* The same for moments of many blocks (more than 4,096 (pair, block) items per group): each
+ * input's blocks are first folded, a pass over whole block rows on many workgroups, into
+ * at most 65,535 blocks in the caller's workspace, then merged per group as above (a fixed
+ * order; it differs from the one-pass order, so the pairs agree with
+ * ldx_group_norm_affine_moments to fp32 rounding, not bit for bit). The workspace size is
+ * ldx_group_norm_moments_workspace_bytes(); with 0 (few items) the call is
+ * ldx_group_norm_affine_moments and the workspace is not used. Same output. */
+size_t ldx_group_norm_moments_workspace_bytes(int64_t chunks0, int32_t c0, int64_t chunks1, int32_t c1,
+                                              int32_t batch, int32_t groups);
+int ldx_group_norm_affine_moments_ws(const float* m0, int64_t chunks0, int32_t c0,
+                                     const float* m1, int64_t chunks1, int32_t c1,
+                                     int32_t batch, int32_t groups,
+                                     const float* gamma, const float* beta, float eps,
+                                     float* affine, void* workspace, size_t workspace_bytes, void* stream);
 
 /* GroupNorm statistics (as ldx_group_norm_affine) and LayerNorm (as ldx_layer_norm) of FP32
  * tensors, statistics in FP32 (per-thread Welford moments merged in a fixed order; the row

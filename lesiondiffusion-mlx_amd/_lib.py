@@ -122,6 +122,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                               c_vp, c_vp, c_f32, c_vp, c_vp]),
     "ldx_group_norm_affine_moments": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32,
                                                c_vp, c_vp, c_f32, c_vp, c_vp]),
+    "ldx_group_norm_moments_workspace_bytes": (ctypes.c_size_t, [c_i64, c_i32, c_i64, c_i32, c_i32, c_i32]),
+    "ldx_group_norm_affine_moments_ws": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i32,
+                                                 c_vp, c_vp, c_f32, c_vp, c_vp, ctypes.c_size_t, c_vp]),
     "ldx_group_norm_affine": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
                                       c_vp, c_vp, c_f32, c_vp, c_vp, c_vp]),
     "ldx_layer_norm": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),
@@ -152,7 +155,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            c_vp]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 def _load() -> ctypes.CDLL:

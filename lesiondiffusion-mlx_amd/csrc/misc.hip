@@ -333,6 +333,60 @@ __global__ __launch_bounds__(256) void gn_moments_kernel(
   }
 }
 
+// First pass of the moments merge for outputs with many moment blocks: workgroup (k, b)
+// folds blocks [k per, min(n, (k + 1) per)) of every pair of m ([batch][n][P][3]) into
+// block k of part ([batch][K][P][3]). Pairs go to consecutive threads (a block's pairs are
+// one contiguous row: whole cache lines), S = 256 / np threads per pair take its blocks
+// j0 + s, j0 + s + S, ... (at most GN_FOLD_ITEMS each, requested before any is merged),
+// and the pair's S threads are merged in order. gn_moments_kernel then merges the K folded
+// blocks: one workgroup per group reading its pairs out of every block would fetch a
+// whole cache line per 12-byte block.
+constexpr int GN_FOLD_ITEMS = 8;
+__global__ __launch_bounds__(256) void gn_moments_fold_kernel(const float* __restrict__ m, int64_t n, int P,
+                                                              int64_t per, float* __restrict__ part, int K) {
+  __shared__ float sh[256 * 3];
+  const int k = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
+  const int64_t j0 = (int64_t)k * per, j1 = j0 + per < n ? j0 + per : n;
+  for (int p0 = 0; p0 < P; p0 += 256) {
+    const int np = P - p0 < 256 ? P - p0 : 256;
+    const int S = 256 / np, u = t % np, s = t / np;
+    Moments acc = {0.f, 0.f, 0.f};
+    if (s < S) {
+      float3 r[GN_FOLD_ITEMS];
+#pragma unroll
+      for (int i = 0; i < GN_FOLD_ITEMS; i++) {
+        const int64_t j = j0 + s + (int64_t)S * i;
+        r[i] = j < j1 ? *reinterpret_cast<const float3*>(m + (((int64_t)b * n + j) * P + p0 + u) * 3)
+                      : make_float3(0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < GN_FOLD_ITEMS; i++)
+        if (j0 + s + (int64_t)S * i < j1) acc = merge(acc, Moments{r[i].x, r[i].y, r[i].z});
+    }
+    __syncthreads();   // the previous round's reads of sh are done
+    sh[t * 3] = acc.n; sh[t * 3 + 1] = acc.mean; sh[t * 3 + 2] = acc.m2;
+    __syncthreads();
+    if (t < np) {
+      Moments r = {sh[t * 3], sh[t * 3 + 1], sh[t * 3 + 2]};
+      for (int s2 = 1; s2 < S; s2++) {
+        const int q = s2 * np + t;
+        r = merge(r, Moments{sh[q * 3], sh[q * 3 + 1], sh[q * 3 + 2]});
+      }
+      float* d = part + (((int64_t)b * K + k) * P + p0 + t) * 3;
+      d[0] = r.n; d[1] = r.mean; d[2] = r.m2;
+    }
+  }
+}
+
+// Folded blocks of a moments tensor with n blocks of P pairs: K = 0 when one workgroup per
+// group merges them directly (few items per group).
+static int64_t gn_fold_blocks(int64_t n, int P, int nu) {
+  if ((int64_t)nu * n <= 4096) return 0;
+  const int np = P < 256 ? P : 256;
+  const int64_t per = (int64_t)(256 / np) * GN_FOLD_ITEMS;
+  return (n + per - 1) / per;
+}
+
 static int64_t gn_chunk(int64_t S, int batch) {
   // about 256 workgroups in pass 1 (one per CU), chunks of 64 .. 8192 voxels
   int64_t per = (S * batch + 255) / 256;
@@ -506,7 +560,7 @@ __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict_
 using namespace ldx;
 
 extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
-extern "C" int ldx_abi_version(void) { return 8; }
+extern "C" int ldx_abi_version(void) { return 9; }
 
 extern "C" size_t ldx_packed_weight_elems(int32_t O, int32_t C, int32_t k, int32_t upsample) {
   if (O < 1 || C < 1 || (k != 1 && k != 3) || (upsample && k != 3)) return 0;
@@ -665,6 +719,56 @@ extern "C" int ldx_group_norm_affine_moments(const float* m0, int64_t chunks0, i
   hipLaunchKernelGGL(gn_moments_kernel, dim3(groups, batch), dim3(256), 0, st, m0, chunks0, c0 / 2,
                      c1 > 0 ? m1 : m0, c1 > 0 ? chunks1 : chunks0, c1 > 0 ? c1 / 2 : 1, C, groups, gamma, beta,
                      eps, affine);
+  return check_launch("group_norm_affine_moments");
+}
+
+extern "C" size_t ldx_group_norm_moments_workspace_bytes(int64_t chunks0, int32_t c0, int64_t chunks1, int32_t c1,
+                                                         int32_t batch, int32_t groups) {
+  const int C = c0 + (c1 > 0 ? c1 : 0);
+  if (batch < 1 || chunks0 < 1 || c0 < 2 || groups < 1 || C % groups || (C / groups) % 2) return 0;
+  const int nu = C / groups / 2;
+  const int64_t k0 = gn_fold_blocks(chunks0, c0 / 2, nu);
+  const int64_t k1 = c1 > 0 ? gn_fold_blocks(chunks1, c1 / 2, nu) : 0;
+  if (k0 == 0 && k1 == 0) return 0;
+  return (size_t)batch * (size_t)(k0 * (c0 / 2) + k1 * (c1 > 0 ? c1 / 2 : 0)) * 3 * sizeof(float);
+}
+
+extern "C" int ldx_group_norm_affine_moments_ws(const float* m0, int64_t chunks0, int32_t c0, const float* m1,
+                                                int64_t chunks1, int32_t c1, int32_t batch, int32_t groups,
+                                                const float* gamma, const float* beta, float eps, float* affine,
+                                                void* workspace, size_t workspace_bytes, void* stream) {
+  const size_t need = ldx_group_norm_moments_workspace_bytes(chunks0, c0, chunks1, c1, batch, groups);
+  if (need == 0)
+    return ldx_group_norm_affine_moments(m0, chunks0, c0, m1, chunks1, c1, batch, groups, gamma, beta, eps,
+                                         affine, stream);
+  if (!m0 || !gamma || !beta || !affine || !workspace) return fail("group_norm_affine_moments: null pointer");
+  if (c1 > 0 && (!m1 || chunks1 < 1)) return fail("group_norm_affine_moments: c1 > 0 without moments");
+  if (workspace_bytes < need)
+    return fail("group_norm_affine_moments: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  if (c0 % 2 || (c1 > 0 && c1 % 2)) return fail("group_norm_affine_moments: c0 and c1 must be even");
+  const int C = c0 + (c1 > 0 ? c1 : 0), nu = C / groups / 2;
+  hipStream_t st = as_stream(stream);
+  float* part = (float*)workspace;
+  // Each input's blocks folded (or taken as they are when few), then the per-group merge.
+  const float* f[2] = {m0, c1 > 0 ? m1 : m0};
+  int64_t nf[2] = {chunks0, c1 > 0 ? chunks1 : chunks0};
+  const int64_t ns[2] = {chunks0, c1 > 0 ? chunks1 : 0};
+  const int P[2] = {c0 / 2, c1 > 0 ? c1 / 2 : 1};
+  for (int i = 0; i < (c1 > 0 ? 2 : 1); i++) {
+    const int64_t K = gn_fold_blocks(ns[i], P[i], nu);
+    if (K == 0) continue;
+    if (K > 65535 || batch > 65535) return fail("group_norm_affine_moments: too many blocks");
+    const int np = P[i] < 256 ? P[i] : 256;
+    const int64_t per = (int64_t)(256 / np) * GN_FOLD_ITEMS;
+    hipLaunchKernelGGL(gn_moments_fold_kernel, dim3((unsigned)K, batch), dim3(256), 0, st, f[i], ns[i], P[i], per,
+                       part, (int)K);
+    if (int rc = check_launch("group_norm_affine_moments: fold")) return rc;
+    f[i] = part;
+    nf[i] = K;
+    part += (size_t)batch * K * P[i] * 3;
+  }
+  hipLaunchKernelGGL(gn_moments_kernel, dim3(groups, batch), dim3(256), 0, st, f[0], nf[0], P[0], f[1], nf[1],
+                     P[1], C, groups, gamma, beta, eps, affine);
   return check_launch("group_norm_affine_moments");
 }
 

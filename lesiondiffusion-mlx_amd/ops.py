@@ -509,9 +509,13 @@ def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, 
             and c1 % 2 == 0:
         # Moments the producing convs kept: no pass over x.
         out = torch.empty((b, c, 2), dtype=torch.float32, device=x.device)
-        check(lib.ldx_group_norm_affine_moments(
-            _ptr(m0), int(m0.shape[1]), c0, _ptr(m1), int(m1.shape[1]) if m1 is not None else 0, c1, b, groups,
-            _ptr(g32), _ptr(b32), float(eps), _ptr(out), _stream()), "group_norm_affine_moments")
+        n1 = int(m1.shape[1]) if m1 is not None else 0
+        # Many blocks per group: the blocks are first folded by a pass over whole rows.
+        ws_bytes = lib.ldx_group_norm_moments_workspace_bytes(int(m0.shape[1]), c0, n1, c1, b, groups)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+        check(lib.ldx_group_norm_affine_moments_ws(
+            _ptr(m0), int(m0.shape[1]), c0, _ptr(m1), n1, c1, b, groups, _ptr(g32), _ptr(b32), float(eps),
+            _ptr(out), _ptr(ws), ws_bytes, _stream()), "group_norm_affine_moments")
         return out
     voxels = d * h * w
     ws = torch.empty(max(1, lib.ldx_group_norm_workspace_bytes(b, voxels, c, groups)),

@@ -50,6 +50,77 @@ def test_group_norm_affine_matches_oracle(pkg, dev, shape, groups, split) -> Non
     assert torch.equal(aff, aff2)
 
 
+def _merged(n, mean, m2, axis):
+    """Pairwise-free closed form of merging (count, mean, M2) blocks along ``axis``:
+    N = sum n, mean = sum n mean / N, M2 = sum M2 + sum n (mean - mean_total)^2."""
+    tot = n.sum(axis=axis)
+    mu = (n * mean).sum(axis=axis) / tot
+    return tot, mu, m2.sum(axis=axis) + (n * (mean - np.expand_dims(mu, axis)) ** 2).sum(axis=axis)
+
+
+@pytest.mark.parametrize(("n0", "c0", "n1", "c1", "groups"), [
+    (3000, 64, 0, 0, 8),       # 12,000 (pair, block) items per group: folded first
+    (20000, 32, 0, 0, 16),     # one pair per group, 20,000 blocks
+    (2500, 64, 600, 32, 8),    # concat: x0's blocks folded, x1's (3,600 items) merged as they are
+])
+def test_group_norm_from_many_moment_blocks(pkg, dev, n0, c0, n1, c1, groups) -> None:
+    """ldx_group_norm_affine_moments_ws: moments of many blocks folded on many workgroups,
+    then merged per group -- against the closed-form merge of the same blocks in float64
+    and against the one-pass merge (fp32 rounding apart)."""
+    import ctypes
+
+    lib = pkg._lib
+    rng = np.random.default_rng(n0 + c0)
+    b = 2
+
+    def blocks(n, c):
+        cnt = np.full((b, n, c // 2), 2.0 * 32)
+        mean = rng.normal(size=(b, n, c // 2)) * 0.5 + 1.0
+        m2 = rng.uniform(0.5, 2.0, size=(b, n, c // 2)) * cnt
+        return np.stack([cnt, mean, m2], -1)
+
+    m0 = blocks(n0, c0)
+    m1 = blocks(n1, c1) if c1 else None
+    c = c0 + c1
+    gamma, beta = rng.normal(size=c).astype(np.float32), rng.normal(size=c).astype(np.float32)
+    d_m0 = to_dev(m0.astype(np.float32), dev)
+    d_m1 = to_dev(m1.astype(np.float32), dev) if c1 else None
+    g, bt = to_dev(gamma, dev), to_dev(beta, dev)
+    ws_bytes = lib.lib.ldx_group_norm_moments_workspace_bytes(n0, c0, n1, c1, b, groups)
+    assert ws_bytes > 0
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    aff = torch.empty((b, c, 2), dtype=torch.float32, device=dev)
+    aff1 = torch.empty((b, c, 2), dtype=torch.float32, device=dev)
+    p1 = d_m1.data_ptr() if c1 else None
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    lib.check(lib.lib.ldx_group_norm_affine_moments_ws(d_m0.data_ptr(), n0, c0, p1, n1, c1, b, groups, g.data_ptr(),
+                                                       bt.data_ptr(), 1e-5, aff.data_ptr(), ws.data_ptr(), ws_bytes, s),
+              "moments_ws")
+    lib.check(lib.lib.ldx_group_norm_affine_moments(d_m0.data_ptr(), n0, c0, p1, n1, c1, b, groups, g.data_ptr(),
+                                                    bt.data_ptr(), 1e-5, aff1.data_ptr(), s), "moments")
+    torch.cuda.synchronize()
+    # float64 closed form: the group's pairs over every block of both inputs
+    gs = c // groups
+    scale = np.empty((b, c)); offset = np.empty((b, c))
+    for gi in range(groups):
+        parts = []
+        for lo_pair in range(gi * gs // 2, (gi + 1) * gs // 2):
+            if lo_pair < c0 // 2:
+                parts.append(m0[:, :, lo_pair].astype(np.float32).astype(np.float64))
+            else:
+                parts.append(m1[:, :, lo_pair - c0 // 2].astype(np.float32).astype(np.float64))
+        allb = np.concatenate(parts, axis=1)
+        tot, mu, m2 = _merged(allb[..., 0], allb[..., 1], allb[..., 2], 1)
+        rstd = 1.0 / np.sqrt(m2 / tot + 1e-5)
+        for ch in range(gi * gs, (gi + 1) * gs):
+            scale[:, ch] = gamma[ch] * rstd
+            offset[:, ch] = beta[ch] - gamma[ch] * rstd * mu
+    a = host(aff)
+    np.testing.assert_allclose(a[..., 0], scale, rtol=2e-5, atol=1e-6)
+    np.testing.assert_allclose(a[..., 1], offset, rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(a, host(aff1), rtol=2e-5, atol=2e-6)
+
+
 def test_layer_norm_matches_oracle(pkg, dev) -> None:
     rng = np.random.default_rng(2)
     for f in (16, 256, 768):
