@@ -372,6 +372,7 @@ def test_dense_rounds_once_and_fuses_gelu(pkg, dev) -> None:
 @pytest.mark.parametrize(("rows", "c", "o", "act", "with_res"), [
     (800, 256, 768, None, False),    # LINet level-2 norm1 -> q/k/v
     (100, 256, 1024, "gelu", False),  # level-3 norm3 -> feed-forward with GELU
+    (800, 256, 1024, "gelu", True),   # level-2 norm3 -> feed-forward (800 workgroups), residual
     (37, 512, 64, None, True),        # widest fused LayerNorm, ragged row block, residual
     (5, 16, 32, None, False),         # one k-step in total
 ])
