@@ -10,7 +10,8 @@
 // 16-byte stores, loaded one or two blocks ahead through buffer resources; the V^T
 // operand is read back with gfx950's transposing LDS read (ds_read_b64_tr_b16), so V is
 // never transposed in memory. Masking and key bounds are applied only on blocks that
-// need them; row sums use v_dot2 on the fp16 probabilities the PV product consumes.
+// need them. Row sums add the fp32 probabilities before their rounding, as the
+// reference's total does; fp32 adds issue beside the MFMAs, v_dot2 does not (measured).
 //
 // SPLIT = 1: a workgroup's 4 waves own 4 x 32 queries and share each K/V tile.
 // SPLIT = 4 / 8: the waves own the same 32 queries and take interleaved key blocks with
@@ -256,7 +257,6 @@ void attention_kernel(AttnParams p) {
     if (nit > 1) load_tile(S1(), blk_of(1) * KB);
   }
   if constexpr (SPLIT == 1) __syncthreads();
-  const E2 ones = {(E)1, (E)1};
 
   // One key block: block it is in LDS, block it + 1 in register set NEXT (stored after
   // the multiply), block it + 2 is loaded into the other set.
@@ -317,15 +317,17 @@ void attention_kernel(AttnParams p) {
     const float alpha = __builtin_amdgcn_exp2f(m - base);
     m = mn;
     E8 pf[2];
-    float sum = 0.f;
+    float sum0 = 0.f, sum1 = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
-      const E2 pr = {(E)__builtin_amdgcn_exp2f(s[e]), (E)__builtin_amdgcn_exp2f(s[e + 1])};
+      const float p0 = __builtin_amdgcn_exp2f(s[e]), p1 = __builtin_amdgcn_exp2f(s[e + 1]);
+      const E2 pr = __builtin_convertvector((f32x2){p0, p1}, E2);
       pf[e >> 3][e & 7] = pr[0];
       pf[e >> 3][(e & 7) + 1] = pr[1];
-      sum = dot2_e(pr, ones, sum);
+      sum0 += p0;
+      sum1 += p1;
     }
-    l = l * alpha + sum;
+    l = l * alpha + (sum0 + sum1);
     // Rescale only when some query's running max moved (wave-uniform test).
     if (__ballot(alpha != 1.f)) {
 #pragma unroll
@@ -426,36 +428,39 @@ void attention_kernel(AttnParams p) {
 }
 
 // Key-split kernel with tiles moved by DMA and a software-pipelined block loop: a
-// workgroup's SPLIT waves own the same 32 * QB queries and take interleaved 32-key blocks
+// workgroup's SPLIT waves own the same 32 queries and take interleaved 32-key blocks
 // (block SPLIT * i + wave). Each wave has private tile buffers in LDS -- K three deep, V
-// two deep -- that direct global->LDS loads fill, so no register holds a tile in transit
-// and the S^T MFMAs of block it + 1 are issued before the softmax and P V of block it,
-// whose VALU work then runs under them. Tile rows are D halves without padding; 16-byte
-// chunk c of row r sits at chunk position c ^ (r mod KG) (KG = D / 8 chunks per row),
-// which spreads both the K-fragment reads and the transposing V reads over the banks. K
-// rows are permuted by key_row as in attention_kernel; the loads go through buffer
-// resources that end at the last key, so rows past the sequence read zeros (probability
-// zero).
-// Whole unmasked blocks (all but possibly a wave's last) take a branch-free softmax
-// instantiation; for one query block per wave the V^T operands are read before the
-// softmax so that their LDS latency runs under it.
-template <int D, int QB, int SPLIT>
+// two deep -- that direct global->LDS loads fill, so no register holds a tile in transit.
+// Tile rows are D halves without padding; 16-byte chunk c of row r sits at chunk position
+// c ^ (r mod KG) (KG = D / 8 chunks per row), which spreads both the K-fragment reads and
+// the transposing V reads over the banks. K rows are permuted by key_row as in
+// attention_kernel; the loads go through buffer resources that end at the last key, so
+// rows past the sequence read zeros (probability zero).
+//
+// Step it of the loop issues eight MFMAs whose operands are already in registers -- S^T
+// of block it + 1 (K fragments read during step it - 1) and O^T += V^T P^T of block it - 1
+// (probabilities and V^T fragments from step it - 1), the S chain and the two O chains
+// alternating -- then reads the K fragments of block it + 2 and the V^T fragments of
+// block it, whose latency the softmax of block it covers. No MFMA waits on an LDS read or
+// on the softmax it runs beside; two register sets alternate with the step's parity.
+template <int D, int SPLIT>
 struct AttnPipeLds {
   static constexpr int HT = 32 * D;                              // halves per K or V tile
-  static constexpr int MERGE = QB * SPLIT * 32 * (D + 4) + 2 * QB * 32 * SPLIT;   // floats for the merge
+  static constexpr int MERGE = SPLIT * 32 * (D + 4) + 2 * 32 * SPLIT;   // floats for the merge
   static constexpr size_t bytes = (size_t)(SPLIT * 5 * HT * 2 > MERGE * 4 ? SPLIT * 5 * HT * 2 : MERGE * 4);
 };
 
-template <int D, int QB, int SPLIT>
+template <int D, int SPLIT>
 __global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void attention_pipe_kernel(AttnParams p) {
   constexpr int NT = 64 * SPLIT;
   constexpr int KB = 32;
   constexpr int DK = D / 16, DB = D / 32, KG = D / 8;
-  constexpr int HT = AttnPipeLds<D, QB, SPLIT>::HT;
+  constexpr int HT = AttnPipeLds<D, SPLIT>::HT;
   constexpr int NH = HT * 2 / 1024;           // 1 KB DMA instructions per K or V tile
   constexpr int RPD = 1024 / (D * 2);
   static_assert(D == 32 || D == 64, "DMA tiles for head widths 32 and 64");
+  static_assert(DK == 2 * DB, "one PV (k-step, dims block) pair per S k-step");
   extern __shared__ __attribute__((aligned(16))) E smem[];
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -465,9 +470,9 @@ void attention_pipe_kernel(AttnParams p) {
     const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
     wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
   }
-  const int nqb = (p.L + 32 * QB - 1) / (32 * QB);
+  const int nqb = (p.L + 31) / 32;
   const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
-  const int q0 = qblk * 32 * QB;
+  const int q0 = qblk * 32;
   E* kbuf = smem + wave * 5 * HT;           // three K tiles, then two V tiles
   E* vbuf = kbuf + 3 * HT;
   const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
@@ -476,23 +481,15 @@ void attention_pipe_kernel(AttnParams p) {
   const E* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
   const E* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
 
-  int qi[QB];
-  const float* mrow[QB];
+  const int qi = min(q0 + col, p.L - 1);
+  const float* mrow = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi * p.ms2 : nullptr;
+  f32x16 o[DB];
 #pragma unroll
-  for (int j = 0; j < QB; j++) {
-    qi[j] = min(q0 + 32 * j + col, p.L - 1);
-    mrow[j] = p.mask ? p.mask + (int64_t)b * p.ms0 + (int64_t)h * p.ms1 + (int64_t)qi[j] * p.ms2 : nullptr;
-  }
-  f32x16 o[QB][DB];
+  for (int i = 0; i < DB; i++)
 #pragma unroll
-  for (int j = 0; j < QB; j++)
-#pragma unroll
-    for (int i = 0; i < DB; i++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) o[j][i][e] = 0.f;
-  float l[QB];
-#pragma unroll
-  for (int j = 0; j < QB; j++) l[j] = 0.f;
+    for (int e = 0; e < 16; e++) o[i][e] = 0.f;
+  float l = 0.f;
+  float m = -INFINITY;   // exponent base of the lane's query (log2 units), -inf before its first key
 
   unsigned koff[NH], voff[NH];
 #pragma unroll
@@ -522,25 +519,6 @@ void attention_pipe_kernel(AttnParams p) {
   const int vr0 = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int vd0 = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   auto vaddr = [&](int r, int d) { return r * D + (((d >> 3) ^ (r % KG)) << 3) + (d & 7); };
-
-  E8 qf[QB][DK];
-  float m[QB];   // exponent base of each query (log2 units), -inf before its first key
-#pragma unroll
-  for (int j = 0; j < QB; j++) m[j] = -INFINITY;
-  // S^T = K Q^T of block it (rows = keys permuted by key_row, columns = queries).
-  auto compute_s = [&](int it, f32x16 (&s)[QB]) {
-    const E* Kc = kbuf + (it % 3) * HT;
-#pragma unroll
-    for (int j = 0; j < QB; j++) s[j] = (f32x16){};
-#pragma unroll
-    for (int dk = 0; dk < DK; dk++) {
-      const int c = 2 * dk + hf;
-      const E8 kf = *reinterpret_cast<const E8*>(Kc + col * D + ((c ^ (col % KG)) << 3));
-#pragma unroll
-      for (int j = 0; j < QB; j++) s[j] = mfma32x(kf, qf[j][dk], s[j]);
-    }
-  };
-  const E2 ones = {(E)1, (E)1};
   // V^T read addresses (halves, in the first V buffer; the second is HT further).
   int va[2][DB][2];
 #pragma unroll
@@ -550,156 +528,195 @@ void attention_pipe_kernel(AttnParams p) {
       va[ks][db][0] = vaddr(vr0 + ks * 16, vd0 + db * 32);
       va[ks][db][1] = vaddr(vr0 + ks * 16 + 4, vd0 + db * 32);
     }
-  // Online softmax of block it and O^T += V^T P^T. FULL: every key of the block lies in
-  // the sequence and there is no mask.
+  // K fragment (k-step dk) of the block in K slot `slot`, V^T fragment (ks, db) of the
+  // block in V slot `slot`.
+  auto read_k = [&](int slot, int dk) {
+    const int c = 2 * dk + hf;
+    return *reinterpret_cast<const E8*>(kbuf + slot * HT + col * D + ((c ^ (col % KG)) << 3));
+  };
+  auto read_v = [&](int slot, int ks, int db) {
+    const E* Vc = vbuf + slot * HT;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][0]));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][1]));
+    return __builtin_bit_cast(E8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+  };
+
+  // Pipeline state, two register sets alternating with the parity of the step.
+  E8 qf[DK];
+  E8 kf[2][DK];        // K fragments of the block whose S^T the step issues
+  E8 pf[2][2];         // probabilities of a block (the B operands of its two PV k-steps)
+  E8 vf[2][2][DB];     // V^T fragments of a block
+  f32x16 sacc[2];      // S^T of the block in softmax / of the next block
+#pragma unroll
+  for (int x = 0; x < 2; x++) {
+#pragma unroll
+    for (int y = 0; y < 2; y++) {
+      pf[x][y] = (E8){};
+#pragma unroll
+      for (int db = 0; db < DB; db++) vf[x][y][db] = (E8){};
+    }
+  }
+
+  // Q^T fragments by asm loads, issued before the tile DMAs: the compiler's own wait for a
+  // load it could see would drain every DMA issued after it.
+#pragma unroll
+  for (int dk = 0; dk < DK; dk++)
+    asm volatile("global_load_dwordx4 %0, %1, off"
+                 : "=v"(qf[dk])
+                 : "v"(qb_ + (int64_t)qi * p.qs1 + dk * 16 + 8 * hf)
+                 : "memory");
+  issue_k(0); issue_k(1); issue_k(2); issue_v(0); issue_v(1);
+  vmcnt_wait<4 * NH>();   // Q and K(0) have landed
+#pragma unroll
+  for (int dk = 0; dk < DK; dk++) asm volatile("" : "+v"(qf[dk]));
+  sacc[0] = (f32x16){};
+#pragma unroll
+  for (int dk = 0; dk < DK; dk++) sacc[0] = mfma32x(read_k(0, dk), qf[dk], sacc[0]);
+  vmcnt_wait<3 * NH>();   // K(1) has landed
+#pragma unroll
+  for (int dk = 0; dk < DK; dk++) kf[0][dk] = read_k(1, dk);
+  __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): K slots 0 and 1 are read
+  issue_k(3); issue_k(4);
+  // In flight now: K(2), V(0), V(1), K(3), K(4); step it awaits all but the last 3 * NH.
+
   constexpr float RB = 8.f;
-  auto softmax_pv = [&](int it, auto vpar_c, auto full_c, f32x16 (&s)[QB]) {
-    constexpr int VP = decltype(vpar_c)::value;
+  // Probabilities of exponent arguments sc rounded to the element type in pairs (one
+  // packed conversion each) for the PV product; the row sum adds the unrounded fp32
+  // values, as the reference's total does (_attention_half.py:84-86).
+  auto probs = [&](const f32x16& sc, E8 (&pc)[2]) {
+    float sum0, sum1;
+    unsigned pk[8];
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(sc[e]), p1 = __builtin_amdgcn_exp2f(sc[e + 1]);
+      pk[e >> 1] = __builtin_bit_cast(unsigned, __builtin_convertvector((f32x2){p0, p1}, E2));
+      sum0 = e == 0 ? p0 : sum0 + p0;
+      sum1 = e == 0 ? p1 : sum1 + p1;
+    }
+    pc[0] = __builtin_bit_cast(E8, (u32x4){pk[0], pk[1], pk[2], pk[3]});
+    pc[1] = __builtin_bit_cast(E8, (u32x4){pk[4], pk[5], pk[6], pk[7]});
+    return sum0 + sum1;
+  };
+  // Softmax of block it (scores sc) into probabilities pc; returns alpha, the factor for
+  // the accumulator (1 unless the base moved). The base moves only when the block's
+  // maximum exceeds it by more than RB (log2 units): probabilities stay small enough for
+  // the element type, and the accumulator rescale is skipped for all but the few blocks
+  // that raise the maximum that much.
+  // FULL (every key lies in the sequence, no mask, the base is finite): the
+  // probabilities are formed against the current base first, with no block maximum --
+  // each is at most its lane's sum of 16, so a sum of at most 16 * 2^RB (inf and NaN
+  // fail the test) keeps every one within 2^12, far inside the element type. Only a wave
+  // with a larger sum takes the block maximum (over the exponent arguments s * c - m,
+  // canonical FMA results), moves the base of each query whose maximum exceeds RB, and
+  // forms its probabilities again.
+  // Otherwise the block maximum comes first; a query with every key so far removed keeps
+  // m = -inf and contributes nothing.
+  auto softmax = [&](int it, auto full_c, f32x16& sc, E8 (&pc)[2]) {
     constexpr bool FULL = decltype(full_c)::value;
-    const E* Vc = vbuf + VP * HT;
-    auto read_v = [&](int ks, int db) {
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][0]));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(lds_v4(Vc + va[ks][db][1]));
-      return __builtin_bit_cast(E8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
-    };
-    // One query block: the V^T operands first, so their LDS latency runs under the softmax
-    // (two query blocks have no registers to spare for that).
-    E8 vf[2][DB];
-    if constexpr (QB == 1) {
+    float alpha = 1.f, sum;
+    if constexpr (FULL) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++)
+      for (int e = 0; e < 16; e++) sc[e] = sc[e] * p.c - m;
+      sum = probs(sc, pc);
+      if (__builtin_expect(__ballot(!(sum <= 16.f * 256.f)) != 0, 0)) {
+        const float top = halves_max(max16(sc));
+        const float dlt = top > RB ? top : 0.f;
 #pragma unroll
-        for (int db = 0; db < DB; db++) vf[ks][db] = read_v(ks, db);
-    }
-    E8 pf[QB][2];
-    float alpha[QB];
-#pragma unroll
-    for (int j = 0; j < QB; j++) {
-      // The exponent base moves only when the block's maximum exceeds it by more than RB
-      // (log2 units): probabilities stay below 2^RB (fp16-safe), and the accumulator
-      // rescale is skipped for all but the few blocks that raise the maximum that much.
-      if constexpr (FULL) {
-        // The base is finite here (each wave's first block seeds it): the exponent
-        // arguments s * c - m are formed first and their maximum taken after, over values
-        // the compiler knows to be canonical, so the raw MFMA scores need no quieting; the
-        // base moves by that maximum on the rare blocks where it exceeds RB.
-#pragma unroll
-        for (int e = 0; e < 16; e++) s[j][e] = s[j][e] * p.c - m[j];
-        const float top = halves_max(max16(s[j]));
-        alpha[j] = 1.f;
-        if (__ballot(top > RB)) {
-          const float dlt = top > RB ? top : 0.f;
-#pragma unroll
-          for (int e = 0; e < 16; e++) s[j][e] -= dlt;
-          alpha[j] = __builtin_amdgcn_exp2f(-dlt);
-          m[j] += dlt;
-        }
-      } else {
-        const int kbase = (wave + SPLIT * it) * KB;
-        float top = -INFINITY;
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
-          float t = s[j][e] * p.c;
-          if (key >= p.LK) t = -INFINITY;
-          else if (mrow[j]) t += mrow[j][(int64_t)key * p.ms3] * 1.44269504088896341f;
-          s[j][e] = t;
-          top = fmaxf(top, t);
-        }
-        top = halves_max(top);
-        // A query with every key so far removed keeps m = -inf and contributes nothing.
-        const float mn = top > m[j] + RB ? top : m[j];
-        const float base = mn == -INFINITY ? 0.f : mn;
-        alpha[j] = __builtin_amdgcn_exp2f(m[j] - base);
-        m[j] = mn;
-#pragma unroll
-        for (int e = 0; e < 16; e++) s[j][e] -= base;
+        for (int e = 0; e < 16; e++) sc[e] -= dlt;
+        alpha = __builtin_amdgcn_exp2f(-dlt);
+        m += dlt;
+        sum = probs(sc, pc);
       }
-      // Probabilities rounded to the element type in pairs (one packed conversion each),
-      // summed in fp32 by v_dot2 as the PV product will consume them.
-      float sum = 0.f;
-      unsigned pk[8];
+    } else {
+      const int kbase = (wave + SPLIT * it) * KB;
+      float top = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const E2 pr = __builtin_convertvector(
-            (f32x2){__builtin_amdgcn_exp2f(s[j][e]), __builtin_amdgcn_exp2f(s[j][e + 1])}, E2);
-        pk[e >> 1] = __builtin_bit_cast(unsigned, pr);
-        sum = dot2_e(pr, ones, sum);
+      for (int e = 0; e < 16; e++) {
+        const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
+        float t = sc[e] * p.c;
+        if (key >= p.LK) t = -INFINITY;
+        else if (mrow) t += mrow[(int64_t)key * p.ms3] * 1.44269504088896341f;
+        sc[e] = t;
+        top = fmaxf(top, t);
       }
-      pf[j][0] = __builtin_bit_cast(E8, (u32x4){pk[0], pk[1], pk[2], pk[3]});
-      pf[j][1] = __builtin_bit_cast(E8, (u32x4){pk[4], pk[5], pk[6], pk[7]});
-      l[j] = l[j] * alpha[j] + sum;
-    }
+      top = halves_max(top);
+      const float mn = top > m + RB ? top : m;
+      const float base = mn == -INFINITY ? 0.f : mn;
+      alpha = __builtin_amdgcn_exp2f(m - base);
+      m = mn;
 #pragma unroll
-    for (int j = 0; j < QB; j++) {
-      if (__ballot(alpha[j] != 1.f)) {
-#pragma unroll
-        for (int db = 0; db < DB; db++) scale_in_place(o[j][db], alpha[j]);
-      }
+      for (int e = 0; e < 16; e++) sc[e] -= base;
+      sum = probs(sc, pc);
     }
+    l = l * alpha + sum;
+    return alpha;
+  };
+
+  // One pipeline step; X = it % 2 picks the register sets (the loop runs two steps per
+  // iteration): kf[X] holds K(it + 1), pf[1 - X] / vf[1 - X] block it - 1, sacc[X] S(it).
+  auto step = [&](int it, auto x_c, auto full_c) {
+    constexpr int X = decltype(x_c)::value;
+    vmcnt_wait<3 * NH>();   // K(it + 2) and V(it) have landed
+    // S^T of block it + 1 and O^T += V^T P^T of block it - 1, the chains alternating (the
+    // PV pairs (ks, db) in the order that revisits a dims block two issues later); both
+    // are harmless when their block lies past this wave's last (tiles of zeros, zero
+    // probabilities before the first block).
+    sacc[1 - X] = (f32x16){};
+#pragma unroll
+    for (int i = 0; i < DK; i++) {
+      sacc[1 - X] = mfma32x(kf[X][i], qf[i], sacc[1 - X]);
+      o[i % DB] = mfma32x(vf[1 - X][i / DB][i % DB], pf[1 - X][i / DB], o[i % DB]);
+    }
+    // K fragments of block it + 2 and V^T fragments of block it, for the next step: read
+    // before the softmax, whose VALU work covers their latency.
+#pragma unroll
+    for (int dk = 0; dk < DK; dk++) kf[1 - X][dk] = read_k((it + 2) % 3, dk);
 #pragma unroll
     for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-      for (int db = 0; db < DB; db++) {
-        if constexpr (QB > 1) vf[ks][db] = read_v(ks, db);
+      for (int db = 0; db < DB; db++) vf[X][ks][db] = read_v(it & 1, ks, db);
+    const float alpha = softmax(it, full_c, sacc[X], pf[X]);
+    // Rescale after this step's P V (the asm waits out the MFMA results first).
+    if (__ballot(alpha != 1.f)) {
 #pragma unroll
-        for (int j = 0; j < QB; j++) o[j][db] = mfma32x(vf[ks][db], pf[j][ks], o[j][db]);
-      }
-  };
-  // One pipeline step: S of block it + 1 goes to the MFMA unit, then block it's softmax
-  // and P V; then V(it + 2) refills the V buffer just read and K(it + 3) the K buffer
-  // read one step ago. VP = it % 2 (the loop runs two steps per iteration).
-  auto step = [&](int it, auto vpar_c, auto full_c, f32x16 (&cur)[QB], f32x16 (&nxt)[QB]) {
-    // K(it + 1) and V(it) have landed once only the previous step's loads may be pending.
-    vmcnt_wait<2 * NH>();
-    if (it + 1 < nit) compute_s(it + 1, nxt);
-    softmax_pv(it, vpar_c, full_c, cur);
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): this step's V reads have returned
+      for (int db = 0; db < DB; db++) scale_in_place(o[db], alpha);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this step's fragment reads have returned
     issue_v(it + 2);
-    issue_k(it + 3);
+    issue_k(it + 5);
   };
 
-  // Q^T fragments by asm loads, issued before the tile DMAs: the compiler's own wait for a
-  // load it could see would drain every DMA issued after it. Only Q and K(0) are awaited
-  // before the first S MFMAs; the empty asm keeps every use of the fragments behind the wait.
-#pragma unroll
-  for (int j = 0; j < QB; j++)
-#pragma unroll
-    for (int dk = 0; dk < DK; dk++)
-      asm volatile("global_load_dwordx4 %0, %1, off"
-                   : "=v"(qf[j][dk])
-                   : "v"(qb_ + (int64_t)qi[j] * p.qs1 + dk * 16 + 8 * hf)
-                   : "memory");
-  issue_k(0); issue_v(0); issue_k(1); issue_v(1); issue_k(2);
-  vmcnt_wait<4 * NH>();   // Q and K(0) have landed; V(0), K(1), V(1), K(2) may be pending
-#pragma unroll
-  for (int j = 0; j < QB; j++)
-#pragma unroll
-    for (int dk = 0; dk < DK; dk++) asm volatile("" : "+v"(qf[j][dk]));
-  f32x16 sa[QB], sb[QB];
-  if (nit > 0) compute_s(0, sa);
   // Blocks before nfull are whole and unmasked (only the sequence's last block can be
-  // partial, and only the wave that owns it has it as its last).
+  // partial, and only the wave that owns it has it as its last). A wave whose first block
+  // is whole seeds its queries' bases with that block's maximum, so whole blocks always
+  // meet a finite base.
   const int nfull = p.mask ? 0 : (p.LK % KB == 0 || (nblk - 1 - wave) % SPLIT != 0 ? nit : nit - 1);
-  // A wave whose first block is whole seeds each query's exponent base with that block's
-  // maximum, so whole blocks never meet an empty (-inf) history.
-  if (nfull > 0) {
-#pragma unroll
-    for (int j = 0; j < QB; j++) m[j] = halves_max(max16(sa[j])) * p.c;
-  }
+  if (nfull > 0) m = halves_max(max16(sacc[0])) * p.c;
   using T = std::integral_constant<bool, true>;
   using F = std::integral_constant<bool, false>;
   using V0 = std::integral_constant<int, 0>;
   using V1 = std::integral_constant<int, 1>;
   int it = 0;
   for (; it + 1 < nfull; it += 2) {
-    step(it, V0(), T(), sa, sb);
-    step(it + 1, V1(), T(), sb, sa);
+    step(it, V0(), T());
+    step(it + 1, V1(), T());
   }
   for (; it < nit; it += 2) {
-    if (it < nfull) step(it, V0(), T(), sa, sb);
-    else step(it, V0(), F(), sa, sb);
-    if (it + 1 < nit) step(it + 1, V1(), F(), sb, sa);
+    if (it < nfull) step(it, V0(), T());
+    else step(it, V0(), F());
+    if (it + 1 < nit) step(it + 1, V1(), F());
+  }
+  // P V of the wave's last block (its probabilities and V^T are in set (nit - 1) % 2).
+  auto last_pv = [&](auto x_c) {
+    constexpr int X = decltype(x_c)::value;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int db = 0; db < DB; db++) o[db] = mfma32x(vf[X][ks][db], pf[X][ks], o[db]);
+  };
+  if (nit > 0) {
+    if (((nit - 1) & 1) == 0) last_pv(V0());
+    else last_pv(V1());
   }
 
   // Merge: every wave publishes its (base, sum) per query; then each scales its O^T by
@@ -708,48 +725,45 @@ void attention_pipe_kernel(AttnParams p) {
   // the SPLIT partials of 8 consecutive d of one query into one 16-byte store.
   E* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
   constexpr int RP = D + 4;
-  float* mo = reinterpret_cast<float*>(smem);            // [QB][SPLIT][32][RP] scaled partial O
-  float* ml = mo + QB * SPLIT * 32 * RP;                  // [QB][32][SPLIT] m, then the same for l
+  float* mo = reinterpret_cast<float*>(smem);            // [SPLIT][32][RP] scaled partial O
+  float* ml = mo + SPLIT * 32 * RP;                       // [32][SPLIT] m, then the same for l
   vmcnt_wait<0>();
   __syncthreads();   // every wave done with its tiles (the merge area overlaps them)
-#pragma unroll
-  for (int j = 0; j < QB; j++) {
-    const float lj = halves_sum(l[j]);
+  {
+    const float lj = halves_sum(l);
     if (hf == 0) {
-      ml[(j * 32 + col) * SPLIT + wave] = m[j];
-      ml[QB * 32 * SPLIT + (j * 32 + col) * SPLIT + wave] = lj;
+      ml[col * SPLIT + wave] = m;
+      ml[32 * SPLIT + col * SPLIT + wave] = lj;
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int j = 0; j < QB; j++) {
+  {
     float M = -INFINITY, mw[SPLIT];
 #pragma unroll
-    for (int w = 0; w < SPLIT; w++) { mw[w] = ml[(j * 32 + col) * SPLIT + w]; M = fmaxf(M, mw[w]); }
+    for (int w = 0; w < SPLIT; w++) { mw[w] = ml[col * SPLIT + w]; M = fmaxf(M, mw[w]); }
     const float bse = M == -INFINITY ? 0.f : M;
     float den = 0.f;
 #pragma unroll
-    for (int w = 0; w < SPLIT; w++)
-      den += __builtin_amdgcn_exp2f(mw[w] - bse) * ml[QB * 32 * SPLIT + (j * 32 + col) * SPLIT + w];
-    const float f = den > 0.f ? __builtin_amdgcn_exp2f(m[j] - bse) / den : 0.f;
-    float* row = mo + ((j * SPLIT + wave) * 32 + col) * RP + 4 * hf;
+    for (int w = 0; w < SPLIT; w++) den += __builtin_amdgcn_exp2f(mw[w] - bse) * ml[32 * SPLIT + col * SPLIT + w];
+    const float f = den > 0.f ? __builtin_amdgcn_exp2f(m - bse) / den : 0.f;
+    float* row = mo + (wave * 32 + col) * RP + 4 * hf;
 #pragma unroll
     for (int db = 0; db < DB; db++)
 #pragma unroll
       for (int g = 0; g < 4; g++) {
-        const f32x4 v = {o[j][db][4 * g] * f, o[j][db][4 * g + 1] * f, o[j][db][4 * g + 2] * f, o[j][db][4 * g + 3] * f};
+        const f32x4 v = {o[db][4 * g] * f, o[db][4 * g + 1] * f, o[db][4 * g + 2] * f, o[db][4 * g + 3] * f};
         *reinterpret_cast<f32x4*>(row + db * 32 + g * 8) = v;
       }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < QB * 32 * (D / 8); idx += NT) {
-    const int d8 = (idx % (D / 8)) * 8, qq = (idx / (D / 8)) % 32, j = idx / (32 * (D / 8));
-    const int qg = q0 + 32 * j + qq;
+  for (int idx = threadIdx.x; idx < 32 * (D / 8); idx += NT) {
+    const int d8 = (idx % (D / 8)) * 8, qq = idx / (D / 8);
+    const int qg = q0 + qq;
     if (qg >= p.L) continue;
     f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < SPLIT; w++) {
-      const float* r = mo + ((j * SPLIT + w) * 32 + qq) * RP + d8;
+      const float* r = mo + (w * 32 + qq) * RP + d8;
       a0 += *reinterpret_cast<const f32x4*>(r);
       a1 += *reinterpret_cast<const f32x4*>(r + 4);
     }
@@ -758,17 +772,17 @@ void attention_pipe_kernel(AttnParams p) {
   }
 }
 
-template <int D, int QB, int SPLIT>
+template <int D, int SPLIT>
 static int launch_attn_pipe(const AttnParams& p, hipStream_t st) {
-  // Tile byte offsets within a (batch, head), up to three blocks past the last, are
+  // Tile byte offsets within a (batch, head), up to five blocks past the last, are
   // 32-bit.
-  if (((int64_t)p.LK + 96 * SPLIT + 64) * (p.ks1 > p.vs1 ? p.ks1 : p.vs1) * 2 >= ((int64_t)1 << 31))
+  if (((int64_t)p.LK + 160 * SPLIT + 64) * (p.ks1 > p.vs1 ? p.ks1 : p.vs1) * 2 >= ((int64_t)1 << 31))
     return fail("attention: key range too large for the DMA kernel");
-  const int64_t n = (int64_t)((p.L + 32 * QB - 1) / (32 * QB)) * p.H * p.B;
+  const int64_t n = (int64_t)((p.L + 31) / 32) * p.H * p.B;
   if (n > 0x7fffffff) return fail("attention: grid too large");
-  constexpr size_t lds = AttnPipeLds<D, QB, SPLIT>::bytes;
+  constexpr size_t lds = AttnPipeLds<D, SPLIT>::bytes;
   static_assert(lds <= 160 * 1024, "LDS");
-  auto kern = attention_pipe_kernel<D, QB, SPLIT>;
+  auto kern = attention_pipe_kernel<D, SPLIT>;
   if (lds > 65536 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return check_launch("attention: set LDS size");
@@ -924,7 +938,6 @@ void attention_wide_kernel(AttnParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  const E2 ones = {(E)1, (E)1};
   constexpr float RB = 8.f;
   auto softmax_pv = [&](int it, auto full_c, f32x16& s) {
     constexpr bool FULL = decltype(full_c)::value;
@@ -963,15 +976,17 @@ void attention_wide_kernel(AttnParams p) {
       for (int e = 0; e < 16; e++) s[e] -= base;
     }
     E8 pf[2];
-    float sum = 0.f;
+    float sum0 = 0.f, sum1 = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; e += 2) {
-      const E2 pr = {(E)__builtin_amdgcn_exp2f(s[e]), (E)__builtin_amdgcn_exp2f(s[e + 1])};
+      const float p0 = __builtin_amdgcn_exp2f(s[e]), p1 = __builtin_amdgcn_exp2f(s[e + 1]);
+      const E2 pr = __builtin_convertvector((f32x2){p0, p1}, E2);
       pf[e >> 3][e & 7] = pr[0];
       pf[e >> 3][(e & 7) + 1] = pr[1];
-      sum = dot2_e(pr, ones, sum);
+      sum0 += p0;
+      sum1 += p1;
     }
-    l = l * alpha + sum;
+    l = l * alpha + (sum0 + sum1);
     // (Plain multiplies: the accumulators may live in AGPRs, which the rescale reaches
     // through the compiler's own moves.)
     if (__ballot(alpha != 1.f)) {
@@ -1223,8 +1238,8 @@ static int launch_d(const AttnParams& p, hipStream_t st) {
   if constexpr (D == 32 || D == 64) {
     // Long key sequences: the DMA-fed, software-pipelined four-way key split
     // (LDX_ATTN_SPLIT=-4 selects it for any length; -8 the eight-way split).
-    if (split == -4) return launch_attn_pipe<D, 1, 4>(p, st);
-    if (split == -8) return launch_attn_pipe<D, 1, 8>(p, st);
+    if (split == -4) return launch_attn_pipe<D, 4>(p, st);
+    if (split == -8) return launch_attn_pipe<D, 8>(p, st);
   }
   if constexpr (D <= 64) {
     if (split == 8) return launch_attn<D, 8>(p, st);

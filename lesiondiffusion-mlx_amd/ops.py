@@ -335,7 +335,8 @@ def nax_conv3d(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None 
         check(lib.ldx_conv3d(ctypes.byref(a), _stream()), "conv3d (fp32)")
         _set_moments(out, None)
         return out
-    want = moments == "always" or (moments is True and not ws_bytes)
+    # An inference-mode output keeps no moments (see _set_moments), so none are taken.
+    want = (moments == "always" or (moments is True and not ws_bytes)) and not out.is_inference()
     chunks = lib.ldx_conv3d_stats_chunks(ctypes.byref(a)) if want else 0
     if moments != "always" and chunks > MOMENTS_MAX_BLOCKS:
         chunks = 0
@@ -354,15 +355,19 @@ def _wrote(t: torch.Tensor) -> None:
     writes in a version counter shared by every view of the same storage, but a write by
     a kernel launched through the C ABI is invisible to it; bumping the counter here
     makes every write -- by this library or by torch -- invalidate moments kept of any
-    view of that storage."""
-    increment_version(t)
+    view of that storage. Inference tensors (``torch.inference_mode``) carry no version
+    counter; nothing is recorded for them, and no moments are kept of them."""
+    if not t.is_inference():
+        increment_version(t)
 
 
 def _set_moments(t: torch.Tensor, m: torch.Tensor | None) -> None:
     """Attach (or clear) the GroupNorm partial moments a conv kept of ``t`` as written,
-    tagged with the storage's write version after that write."""
+    tagged with the storage's write version after that write. An inference tensor has no
+    write version to validate moments against later, so none are kept of it (its
+    GroupNorm then reduces the tensor itself)."""
     _wrote(t)
-    if m is None:
+    if m is None or t.is_inference():
         if hasattr(t, "_ldx_moments"):
             del t._ldx_moments
     else:
@@ -374,7 +379,7 @@ def moments_of(t: torch.Tensor | None) -> torch.Tensor | None:
     moments=True)``), or None -- also when anything has written to ``t``'s storage since
     (a torch in-place op, another op's ``out=``, a write through another view)."""
     kept = getattr(t, "_ldx_moments", None) if t is not None else None
-    if kept is None:
+    if kept is None or t.is_inference():
         return None
     m, version = kept
     if t._version != version or t.dim() != 5 or m.shape[0] != t.shape[0] or 2 * m.shape[2] != t.shape[4]:

@@ -207,3 +207,22 @@ def test_group_norm_moments_are_dropped_after_any_later_write(pkg) -> None:
     pkg.ops._set_moments(t, m)
     pkg.ops._wrote(t.view(1, 8, 16))                           # what every out= writer does
     assert pkg.ops.moments_of(t) is None
+
+
+def test_group_norm_moments_helpers_accept_inference_tensors(pkg) -> None:
+    """Under ``torch.inference_mode`` tensors have no version counter: recording a write
+    must not raise, and no moments are kept of (or found for) such a tensor, since a later
+    torch write to it could not be detected."""
+    import torch
+
+    m = torch.zeros(1, 3, 8, 3)
+    with torch.inference_mode():
+        t = torch.zeros(1, 2, 2, 2, 16)
+        assert t.is_inference()
+        pkg.ops._wrote(t)
+        pkg.ops._set_moments(t, m)
+        assert pkg.ops.moments_of(t) is None
+        pkg.ops._set_moments(t, None)
+        assert pkg.ops.moments_of(t) is None
+    pkg.ops._set_moments(t, m)            # outside the mode the tensor is still an inference tensor
+    assert pkg.ops.moments_of(t) is None
