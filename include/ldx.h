@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (9); bumped on any change to the structs below or the entry points. */
+/* ABI version (10); bumped on any change to the structs below or the entry points. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -357,53 +357,6 @@ int ldx_vq_squared_norms4(const void* x, int64_t n, int32_t dtype, void* out, vo
 int ldx_vq_nearest4(const void* z, const void* z_norm, const void* codebook, const void* codebook_norm,
                     int64_t positions, int32_t entries, int32_t dtype, int32_t* indices,
                     void* quantized, void* stream);
-
-/* ------------------------------------------------------- token-row chains -------
- * The row-local part of the spatial transformer block (mlx_model.py:522-552) in one
- * launch per chain, the dense layers and LayerNorm of a 32-token tile kept on chip.
- * Replaces, in one call, SourceLayers.dense (mlx_model.py:204-220) and the LayerNorm
- * (mlx_model.py:360-367) sequences the block runs between its attentions:
- *   [x' = half(x * affine[b, c, 0] + affine[b, c, 1])]          (affine may be NULL)
- *   y1  = half(G1 x' + bias1 [+ res1])                           (stored to y1 if set)
- *   z   = half((y1 - mean) * rstd * gamma + beta)                (LayerNorm, eps ln_eps)
- *   h   = act2(half(G2 z + bias2))
- *   [y3 = act3(half(G3 h + bias3 + y1))]                         (has_g3)
- *   [o4 = act4(half(G4 y3 + bias4 + res4))]                      (has_g4)
- * and stores the last stage's output to out. Rows are the batch items' token sequences
- * laid end to end (rows = batch * tokens; the affine row of token row r is r / tokens);
- * every tensor is row-major with a pitch in elements. Weights are packed by
- * ldx_pack_weight with ksize 1; biases fp32, 16-byte aligned. Widths: multiples of 32;
- * G1 no wider than x, G3's width equal to G1's, G4's no wider than x; LDS holds 32 rows
- * of two x-wide tiles plus G2's output when G3 follows (at most 160 KiB). dtype:
- * LDX_DTYPE_F16 or LDX_DTYPE_BF16. Each stage rounds as a separate dense launch does. */
-typedef struct ldx_chain_gemm {
-  const void* weight;
-  const float* bias;
-  int32_t out_c;
-  int32_t act;
-} ldx_chain_gemm;
-
-typedef struct ldx_token_chain_args {
-  int32_t rows, tokens, channels, dtype;
-  const void* x;
-  int64_t x_pitch;
-  const float* affine;
-  const void* res1;
-  int64_t res1_pitch;
-  void* y1;
-  int64_t y1_pitch;
-  const float* ln_gamma;
-  const float* ln_beta;
-  float ln_eps;
-  ldx_chain_gemm g1, g2, g3, g4;
-  int32_t has_g3, has_g4;
-  const void* res4;
-  int64_t res4_pitch;
-  void* out;
-  int64_t out_pitch;
-} ldx_token_chain_args;
-
-int ldx_token_chain(const ldx_token_chain_args* args, void* stream);
 
 /* ------------------------------------------------- source-order fp16 arithmetic -------
  * The reference's "source" arithmetic, which reproduces Torch-CPU's reduction order bit

@@ -82,29 +82,6 @@ class SourceConvArgs(ctypes.Structure):
     ]
 
 
-class ChainGemm(ctypes.Structure):
-    """Mirror of ``ldx_chain_gemm``."""
-
-    _fields_ = [("weight", c_vp), ("bias", c_vp), ("out_c", c_i32), ("act", c_i32)]
-
-
-class TokenChainArgs(ctypes.Structure):
-    """Mirror of ``ldx_token_chain_args``."""
-
-    _fields_ = [
-        ("rows", c_i32), ("tokens", c_i32), ("channels", c_i32), ("dtype", c_i32),
-        ("x", c_vp), ("x_pitch", c_i64),
-        ("affine", c_vp),
-        ("res1", c_vp), ("res1_pitch", c_i64),
-        ("y1", c_vp), ("y1_pitch", c_i64),
-        ("ln_gamma", c_vp), ("ln_beta", c_vp), ("ln_eps", c_f32),
-        ("g1", ChainGemm), ("g2", ChainGemm), ("g3", ChainGemm), ("g4", ChainGemm),
-        ("has_g3", c_i32), ("has_g4", c_i32),
-        ("res4", c_vp), ("res4_pitch", c_i64),
-        ("out", c_vp), ("out_pitch", c_i64),
-    ]
-
-
 # name -> (restype, argtypes); every function declared in include/ldx.h.
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_last_error": (ctypes.c_char_p, []),
@@ -148,14 +125,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_timestep_embedding_f32": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_vq_nearest4": (c_i32, [c_vp, c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_vp, c_vp]),
     "ldx_conv3d_source_half": (c_i32, [ctypes.POINTER(SourceConvArgs), c_vp]),
-    "ldx_token_chain": (c_i32, [ctypes.POINTER(TokenChainArgs), c_vp]),
     "ldx_group_norm_source_workspace_bytes": (ctypes.c_size_t, [c_i32, c_i32, c_i64, c_i32]),
     "ldx_group_norm_source_half": (c_i32, [c_vp, c_i64, c_i64, c_i64, c_i32, c_i32, c_i64, c_i32, c_vp, c_vp,
                                            c_f32, c_vp, c_vp, c_i64, c_i64, c_i64, c_vp, ctypes.c_size_t,
                                            c_vp]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 def _load() -> ctypes.CDLL:

@@ -41,11 +41,17 @@ def groups_for(channels: int) -> int:
 
 class SourceLayers:
     """Packed, source-keyed conv / dense / norm layers on one device. ``dtype`` is the
-    network's activation and weight type: fp16 (the conditioned networks), bf16, or fp32
-    (the FP32 networks -- LMNet, the FP32 VQ decode -- on the exact split-fp16 mode)."""
+    network's activation and weight type: fp16 (the conditioned networks) or fp32 (the
+    FP32 networks -- LMNet, the FP32 VQ decode -- on the exact split-fp16 mode), the two
+    the reference's networks run in. bf16 is an op-level type (conv3d, dense, attention)
+    only: the network's GroupNorm, LayerNorm and timestep kernels take fp16 or fp32, so a
+    bf16 network is rejected here rather than on its first forward."""
 
     def __init__(self, weights: Mapping[str, torch.Tensor], *, device: torch.device | str = "cuda",
                  dtype: torch.dtype = torch.float16):
+        if dtype not in (torch.float16, torch.float32):
+            raise ValueError(f"network dtype {dtype} not supported: fp16 or fp32 (bf16 is supported by the "
+                             "conv3d / dense / attention ops, not by the network's normalisation layers)")
         self.device = torch.device(device)
         self.dtype = dtype
         self.weights = to_device_weights(weights, self.device, dtype)

@@ -20,13 +20,13 @@ import torch
 from torch.autograd.graph import increment_version
 
 from . import _lib
-from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, SourceConvArgs, TokenChainArgs, check, lib
+from ._lib import ACT_GELU, ACT_NONE, ACT_SILU, AttnArgs, ConvArgs, SourceConvArgs, check, lib
 
 __all__ = [
     "PackedWeight", "pack_weight", "pack_upsample_weight", "nax_conv3d", "conv3d", "dense",
     "group_norm_affine", "layer_norm", "attention", "flash_attention", "timestep_embedding",
     "silu", "upsample_nearest2", "resize_nearest", "output_extent", "count_flops", "squared_norms4",
-    "nearest_codebook4", "conv3d_half", "group_norm_half", "token_chain", "token_chain_fits",
+    "nearest_codebook4", "conv3d_half", "group_norm_half",
 ]
 
 
@@ -415,73 +415,6 @@ def dense(x: torch.Tensor, packed: PackedWeight, bias: torch.Tensor | None = Non
     o5 = None if out is None else out.reshape(1, 1, 1, rows, packed.out_channels)
     y = nax_conv3d(x5, packed, bias, residual=r5, act=act, out=o5, affine=affine, ln=ln)
     return y.reshape(*lead, packed.out_channels)
-
-
-# ------------------------------------------------------------ token-row chains
-
-_ACT = {None: ACT_NONE, "gelu": ACT_GELU, "silu": ACT_SILU}
-_CHAIN_LDS = 160 * 1024
-
-
-def token_chain_fits(channels: int, widths: tuple[int, ...], with_g3: bool) -> bool:
-    """Whether ``token_chain`` takes a chain over ``channels``-wide rows whose GEMMs produce
-    ``widths``: multiples of 32, and the 32-row tiles within LDS."""
-    if channels % 32 or any(w % 32 or w < 32 for w in widths):
-        return False
-    lds = 32 * (2 * (channels + 8) + ((widths[1] + 8) if with_g3 else 0)) * 2
-    return lds <= _CHAIN_LDS
-
-
-def token_chain(x: torch.Tensor, g1, ln: tuple[torch.Tensor, torch.Tensor, float], g2, *, tokens: int,
-                g3=None, g4=None, affine: torch.Tensor | None = None, res1: torch.Tensor | None = None,
-                y1: torch.Tensor | None = None, res4: torch.Tensor | None = None) -> torch.Tensor:
-    """The transformer block's row-local chain in one launch (ldx_token_chain): over the rows
-    of ``x`` (``(rows, C)``; ``tokens`` rows per batch item), ``y1 = G1(affine(x)) (+ res1)``,
-    then ``LayerNorm(y1)``, ``G2``, optionally ``G3 (+ y1)`` and ``G4 (+ res4)``. Each
-    ``g`` is ``(PackedWeight, fp32 bias or None, act)`` with act None, "gelu" or "silu";
-    ``ln = (gamma, beta, eps)`` in fp32. ``y1`` (optional) receives G1's output. Returns
-    the last stage's output ``(rows, out_c)``. Each stage rounds as ``dense`` does
-    (mlx_model.py:204-220, 360-374, 522-552)."""
-    _require_cuda(x, "x", tuple(ELEM_DTYPES))
-    if x.dim() != 2 or x.stride(1) != 1:
-        raise ValueError(f"x must be (rows, channels) with contiguous channels, got {tuple(x.shape)}")
-    rows, c = x.shape
-    if rows % tokens:
-        raise ValueError(f"{rows} rows are not whole batch items of {tokens} tokens")
-    gs = [g1, g2] + ([g3] if g3 is not None else []) + ([g4] if g4 is not None else [])
-    for g in gs:
-        if g[0].ksize != 1 or g[0].exact or g[0].data.dtype != x.dtype:
-            raise ValueError("token_chain stages are dense layers packed with pack_weight in x's dtype")
-    last = gs[-1][0].out_channels
-    out = torch.empty((rows, last), dtype=x.dtype, device=x.device)
-    a = TokenChainArgs()
-    a.rows, a.tokens, a.channels, a.dtype = rows, tokens, c, ELEM_DTYPES[x.dtype]
-    a.x, a.x_pitch = _ptr(x), x.stride(0)
-    a.affine = _ptr(affine)
-    for t, nm in ((res1, "res1"), (y1, "y1"), (res4, "res4")):
-        if t is not None:
-            _same_elem(t, nm, x.dtype)
-            if t.dim() != 2 or t.stride(1) != 1 or t.shape[0] != rows:
-                raise ValueError(f"{nm} must be ({rows}, channels) with contiguous channels")
-            setattr(a, nm, _ptr(t))
-            setattr(a, nm + "_pitch", t.stride(0))
-    a.ln_gamma, a.ln_beta, a.ln_eps = _ptr(ln[0]), _ptr(ln[1]), float(ln[2])
-    for name, g in zip(("g1", "g2", "g3", "g4"), (g1, g2, g3, g4)):
-        if g is None:
-            continue
-        st = getattr(a, name)
-        st.weight, st.bias = _ptr(g[0].data), _ptr(g[1])
-        st.out_c, st.act = g[0].out_channels, _ACT[g[2]]
-    a.has_g3, a.has_g4 = int(g3 is not None), int(g4 is not None)
-    a.out, a.out_pitch = _ptr(out), out.stride(0)
-    check(lib.ldx_token_chain(ctypes.byref(a), _stream()), "token_chain")
-    for t in (y1, out):
-        if t is not None:
-            _wrote(t)
-    if count_flops.active is not None:
-        widths = [c] + [g[0].out_channels for g in gs]
-        count_flops.active.dense += sum(2.0 * rows * widths[i] * widths[i + 1] for i in range(len(gs)))
-    return out
 
 
 # ------------------------------------------------------------ normalisation

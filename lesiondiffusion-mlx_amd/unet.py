@@ -48,15 +48,9 @@ class LdmUnet(SourceLayers):
     the reference (mlx_model.py:554-568); ``forward`` works on NDHWC."""
 
     def __init__(self, weights: Mapping[str, object], config: UnetConfig, *, device="cuda",
-                 dtype: torch.dtype = torch.float16, chain: bool = False):
+                 dtype: torch.dtype = torch.float16):
         super().__init__(weights, device=device, dtype=dtype)
         self.config = config
-        # chain: run the transformer blocks' row-local layers as token-row chains (three
-        # launches, ops.token_chain) rather than one launch per dense layer. Off by
-        # default: one workgroup streams every weight of its chain, and a CU sustains
-        # about 36 GB/s of such loads, so at 256 channels (1.25 MB for the feed-forward
-        # chain) the chains take longer than the per-layer launches they replace.
-        self.chain = chain
         # All ResBlock time projections read silu(emb): one GEMM.
         emb_keys = sorted(k[: -len(".weight")] for k in self.weights if k.endswith(".emb_layers.1.weight"))
         self.emb_slices: dict[str, tuple[int, int]] = {}
@@ -117,49 +111,6 @@ class LdmUnet(SourceLayers):
         o = ops.flash_attention(q, k, v, heads=heads, scale=(c // heads) ** -0.5)
         return self.dense(o, att + ".to_out.0", residual=residual)
 
-    def _gemm(self, key: str, act: str | None = None):
-        return (self.packed[key], self.bias32.get(key), act)
-
-    def _ln(self, key: str, eps: float = 1e-5):
-        return (self.vec32[key + ".weight"], self.vec32[key + ".bias"], eps)
-
-    def _chain_transformer(self, x: torch.Tensor, aff: torch.Tensor,
-                           context_kv: Mapping[str, tuple[torch.Tensor, torch.Tensor]] | None,
-                           key: str) -> torch.Tensor | None:
-        """The transformer block as three token-row chains around its two attentions
-        (ops.token_chain): proj_in -> norm1 -> q/k/v; to_out (+ x) -> norm2 -> to_q (or
-        q/k/v); to_out (+ x) -> norm3 -> ff GELU -> ff (+ x) -> proj_out (+ block input).
-        None when the widths do not fit the chain kernel."""
-        b, d, h, w, c = x.shape
-        t = d * h * w
-        blk = key + ".transformer_blocks.0"
-        kv = None if context_kv is None else context_kv.get(blk + ".attn2")
-        q2key = blk + ".attn2.to_q" if kv is not None else blk + ".attn2.qkv"
-        ff = blk + ".ff.net.0.0"
-        if (self.dtype == torch.float32 or not x.is_contiguous()
-                or not ops.token_chain_fits(c, (c, self.packed[blk + ".attn1.qkv"].out_channels), False)
-                or not ops.token_chain_fits(c, (c, self.packed[ff].out_channels, c, c), True)):
-            return None
-        heads = c // self.config.num_head_channels
-        rows = x.view(b * t, c)
-        tok = torch.empty_like(rows)
-        qkv = ops.token_chain(rows, self._gemm(key + ".proj_in"), self._ln(blk + ".norm1"),
-                              self._gemm(blk + ".attn1.qkv"), tokens=t, affine=aff, y1=tok)
-        o = ops.flash_attention(qkv[:, :c].view(b, t, c), qkv[:, c:2 * c].view(b, t, c),
-                                qkv[:, 2 * c:].view(b, t, c), heads=heads, scale=(c // heads) ** -0.5)
-        x1 = torch.empty_like(rows)
-        q2 = ops.token_chain(o.view(b * t, c), self._gemm(blk + ".attn1.to_out.0"), self._ln(blk + ".norm2"),
-                             self._gemm(q2key), tokens=t, res1=tok, y1=x1)
-        if kv is None:
-            q, k, v = q2[:, :c].view(b, t, c), q2[:, c:2 * c].view(b, t, c), q2[:, 2 * c:].view(b, t, c)
-        else:
-            q, (k, v) = q2.view(b, t, c), kv
-        o2 = ops.flash_attention(q, k, v, heads=heads, scale=(c // heads) ** -0.5)
-        y = ops.token_chain(o2.view(b * t, c), self._gemm(blk + ".attn2.to_out.0"), self._ln(blk + ".norm3"),
-                            self._gemm(ff, "gelu"), tokens=t, res1=x1, g3=self._gemm(blk + ".ff.net.2"),
-                            g4=self._gemm(key + ".proj_out"), res4=rows)
-        return y.view(b, d, h, w, c)
-
     def transformer(self, x: torch.Tensor, context_kv: Mapping[str, tuple[torch.Tensor, torch.Tensor]] | None,
                     key: str) -> torch.Tensor:
         """Spatial transformer (mlx_model.py:522-552) on NDHWC ``x``."""
@@ -169,10 +120,6 @@ class LdmUnet(SourceLayers):
         kv = None if context_kv is None else context_kv.get(blk + ".attn2")
         if kv is None and not self.config.skip_context and context_kv is not None:
             raise ValueError(f"missing projected context for {blk}.attn2")
-        if self.chain:
-            y = self._chain_transformer(x, aff, context_kv, key)
-            if y is not None:
-                return y
         tok = self.conv(x, key + ".proj_in", affine=aff).view(b, d * h * w, c)
         heads = c // self.config.num_head_channels
         tok = self._attend(tok, blk + ".attn1", heads, None, tok, blk + ".norm1")

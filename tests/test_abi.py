@@ -34,8 +34,7 @@ def test_library_exports_every_declared_symbol(pkg) -> None:
 def test_ctypes_structs_match_c_layout(pkg, tmp_path) -> None:
     lib = pkg._lib
     fields = {"ldx_conv3d_args": lib.ConvArgs, "ldx_attention_args": lib.AttnArgs,
-              "ldx_conv3d_source_args": lib.SourceConvArgs, "ldx_chain_gemm": lib.ChainGemm,
-              "ldx_token_chain_args": lib.TokenChainArgs}
+              "ldx_conv3d_source_args": lib.SourceConvArgs}
     src = ["#include <stdio.h>", "#include <stddef.h>", '#include "ldx.h"', "int main(void) {"]
     for cname, cls in fields.items():
         src.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
@@ -226,3 +225,15 @@ def test_group_norm_moments_helpers_accept_inference_tensors(pkg) -> None:
         assert pkg.ops.moments_of(t) is None
     pkg.ops._set_moments(t, m)            # outside the mode the tensor is still an inference tensor
     assert pkg.ops.moments_of(t) is None
+
+
+def test_network_rejects_bf16_at_construction(pkg) -> None:
+    """bf16 is an op-level type; a bf16 network (whose GroupNorm / LayerNorm / timestep
+    kernels take fp16 or fp32) fails at construction with a clear message, not on its
+    first forward."""
+    import torch
+
+    with pytest.raises(ValueError, match="network dtype"):
+        pkg.layers.SourceLayers({}, device="cpu", dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="network dtype"):
+        pkg.unet.LdmUnet({}, None, device="cpu", dtype=torch.bfloat16)
