@@ -817,10 +817,11 @@ extern "C" int ldx_group_norm_apply(const void* x, int64_t x_pitch, void* y, int
     return fail("group_norm_apply: rows, pitches and the affine must be 16-byte aligned");
   if (affine_batch_stride < 2 * (int64_t)channels && batch > 1) return fail("group_norm_apply: bad affine stride");
   const int64_t units = (int64_t)batch * voxels * (channels / 8);
-  if (units >= ((int64_t)1 << 31) || (int64_t)batch * voxels >= ((int64_t)1 << 31))
-    return fail("group_norm_apply: tensor too large");
   const int g8 = channels / 8;
   const unsigned grid = grid_cap(units, 256, 16384);
+  // The kernel's grid-stride index is 32-bit: it must not pass 2^31 - 1 on its last step.
+  if (units + (int64_t)grid * 256 >= ((int64_t)1 << 31) || (int64_t)batch * voxels >= ((int64_t)1 << 31))
+    return fail("group_norm_apply: tensor too large");
   if (dtype == LDX_DTYPE_F16)
     hipLaunchKernelGGL((gn_apply_kernel<f16, f16x8>), dim3(grid), dim3(256), 0, as_stream(stream),
                        (const f16*)x, x_pitch, (f16*)y, y_pitch, affine, affine_batch_stride, silu, (int)units,
