@@ -193,8 +193,23 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
   // u = i * NT + tid is halo row u / (HW * 8), voxel (u / 8) % HW, channel group u % 8 =
   // tid % 8 (one affine per thread). The arithmetic is the streamed kernel's (fp32 multiply-
   // add, silu_f, one rounding); voxels outside the volume are zero after the transform
-  // (the conv pads the normalised input). The loads are asm, awaited explicitly.
-  auto halo_xf = [&](int j) __attribute__((always_inline)) {
+  // (the conv pads the normalised input). The loads are asm, awaited explicitly. Units
+  // below XNA are the first TD planes (all that the taps kd = 0 read): they are staged
+  // before the tap loop; the last two planes' units are loaded with them and transformed
+  // at tap TB, beside the MFMAs, as the DMA path awaits its last planes there.
+  constexpr int XNA = TD * S::HH * S::HW * 8;            // units of the first TD planes
+  constexpr int XA = (XNA + NT - 1) / NT;                // of them per thread
+  constexpr int XL = (S::NXU - XNA + NT - 1) / NT;       // late units per thread
+  f32x4 xaf[4];
+  auto xf_affine = [&](int j) {
+    const int c0 = j * KC, q = tid & 7;
+    const i32x4 ra = dma_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine, p.affine ? (unsigned)(p.C * 8) : 0u);
+#pragma unroll
+    for (int k = 0; k < 4; k++) xaf[k] = __builtin_bit_cast(f32x4, buffer_load16_asm(ra, (unsigned)((c0 + q * 8) * 8 + k * 16)));
+  };
+  // Load unit u (u >= NXU: none) of chunk j: its value, LDS destination (-1: none) and
+  // whether it lies inside the volume.
+  auto xf_load = [&](int j, int u, E8& v, int& dst, bool& in) {
     const int c0 = j * KC;
     const bool in0 = c0 < p.C0;
     const E* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
@@ -202,47 +217,99 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     const i32x4 rs = dma_rsrc(base, (unsigned)vol * pitch2);
     const unsigned cb = (unsigned)((in0 ? c0 : c0 - p.C0) * 2);
     const int q = tid & 7;
-    const i32x4 ra = dma_rsrc(p.affine ? p.affine + (int64_t)b * p.C * 2 : p.affine, p.affine ? (unsigned)(p.C * 8) : 0u);
-    f32x4 af[4];
+    const int r = u / (S::HW * 8), hw = (u / 8) % S::HW;
+    const int hd = r / S::HH, hh = r - hd * S::HH;
+    const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
+    in = u < S::NXU && (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+    dst = u < S::NXU ? (hd * S::PSU + hh * S::RSU + hw * PU + q) * 16 : -1;
+    v = buffer_load16_asm<E8>(rs, in ? (unsigned)((id * p.H + ih) * p.W + iw) * pitch2 + cb + q * 16 : OOB);
+  };
+  // Transform a loaded unit and write it to the halo.
+  auto xf_store = [&](E8 v, int dst, bool in) {
+    pin_value(v);
+    if (dst < 0) return;
 #pragma unroll
-    for (int k = 0; k < 4; k++) af[k] = __builtin_bit_cast(f32x4, buffer_load16_asm(ra, (unsigned)((c0 + q * 8) * 8 + k * 16)));
-    // Two batches of units, so that a later chunk's staging fits beside the live
-    // accumulators.
-    constexpr int XB = (S::XPT + 1) / 2;
+    for (int e = 0; e < 8; e++) {
+      const float sc = p.affine ? xaf[e >> 1][(e & 1) * 2] : 1.f;
+      const float of = p.affine ? xaf[e >> 1][(e & 1) * 2 + 1] : 0.f;
+      float yv = (float)v[e] * sc + of;
+      if (p.silu) yv = silu_f(yv);
+      v[e] = in ? (E)yv : (E)0;
+    }
+    *reinterpret_cast<E8*>(smem + dst) = v;
+  };
+  // The first TD planes of chunk j: all at once when no accumulator is live (chunk 0),
+  // else in two batches, so that the staging fits beside the live accumulators.
+  auto xf_early = [&](int j, bool batched) __attribute__((always_inline)) {
+    constexpr int XB1 = (XA + 1) / 2;
+    if (!batched) {
+      E8 xv[XA];
+      int dst[XA];
+      bool in[XA];
 #pragma unroll
-    for (int b0 = 0; b0 < S::XPT; b0 += XB) {
-      E8 xv[XB];
-      int dst[XB];
-      bool in[XB];
-#pragma unroll
-      for (int ii = 0; ii < XB; ii++) {
-        const int u = (b0 + ii) * NT + tid;
-        const int r = u / (S::HW * 8), hw = (u / 8) % S::HW;
-        const int hd = r / S::HH, hh = r - hd * S::HH;
-        const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
-        in[ii] = b0 + ii < S::XPT && u < S::NXU && (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H &&
-                 (unsigned)iw < (unsigned)p.W;
-        dst[ii] = b0 + ii < S::XPT && u < S::NXU ? (hd * S::PSU + hh * S::RSU + hw * PU + q) * 16 : -1;
-        xv[ii] = buffer_load16_asm<E8>(rs, in[ii] ? (unsigned)((id * p.H + ih) * p.W + iw) * pitch2 + cb + q * 16 : OOB);
-      }
+      for (int i = 0; i < XA; i++) xf_load(j, i * NT + tid < XNA ? i * NT + tid : S::NXU, xv[i], dst[i], in[i]);
       vmcnt_wait<0>();
 #pragma unroll
-      for (int k = 0; k < 4; k++) pin_value(af[k]);
+      for (int k = 0; k < 4; k++) pin_value(xaf[k]);
 #pragma unroll
-      for (int ii = 0; ii < XB; ii++) {
-        pin_value(xv[ii]);
-        if (dst[ii] < 0) continue;
-        E8 v = xv[ii];
+      for (int i = 0; i < XA; i++) xf_store(xv[i], dst[i], in[i]);
+    } else {
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float sc = p.affine ? af[e >> 1][(e & 1) * 2] : 1.f;
-          const float of = p.affine ? af[e >> 1][(e & 1) * 2 + 1] : 0.f;
-          float yv = (float)v[e] * sc + of;
-          if (p.silu) yv = silu_f(yv);
-          v[e] = in[ii] ? (E)yv : (E)0;
+      for (int b0 = 0; b0 < XA; b0 += XB1) {
+        E8 xv[XB1];
+        int dst[XB1];
+        bool in[XB1];
+#pragma unroll
+        for (int ii = 0; ii < XB1; ii++) {
+          const int u = (b0 + ii) * NT + tid;
+          xf_load(j, b0 + ii < XA && u < XNA ? u : S::NXU, xv[ii], dst[ii], in[ii]);
         }
-        *reinterpret_cast<E8*>(smem + dst[ii]) = v;
+        vmcnt_wait<0>();
+#pragma unroll
+        for (int k = 0; k < 4; k++) pin_value(xaf[k]);
+#pragma unroll
+        for (int ii = 0; ii < XB1; ii++) xf_store(xv[ii], dst[ii], in[ii]);
       }
+    }
+  };
+  // The late units travel raw by DMA into a staging area over group 0's exchange slots
+  // (unused until the last chunk's tap loop ends), unit i * NT + tid of the late range at
+  // 16 (i * NT + tid): each thread reads back exactly what its own DMA wrote.
+  static_assert(S::G0X + XL * NT * 16 <= S::CNT || S::NC0 == 0, "late staging within the exchange slots");
+  auto xf_unit = [&](int u, unsigned& off, int& dst, bool& in) {
+    const int q = tid & 7;
+    const int r = u / (S::HW * 8), hw = (u / 8) % S::HW;
+    const int hd = r / S::HH, hh = r - hd * S::HH;
+    const int id = d0 - 1 + hd, ih = h0 - 1 + hh, iw = w0 - 1 + hw;
+    in = u < S::NXU && (unsigned)id < (unsigned)p.D && (unsigned)ih < (unsigned)p.H && (unsigned)iw < (unsigned)p.W;
+    dst = u < S::NXU ? (hd * S::PSU + hh * S::RSU + hw * PU + q) * 16 : -1;
+    off = (unsigned)((id * p.H + ih) * p.W + iw);
+  };
+  auto xf_late_load = [&](int j) {
+    const int c0 = j * KC;
+    const bool in0 = c0 < p.C0;
+    const E* base = in0 ? p.x0 + (int64_t)b * vol * p.x0p : p.x1 + (int64_t)b * vol * p.x1p;
+    const unsigned pitch2 = (unsigned)((in0 ? p.x0p : p.x1p) * 2);
+    const i32x4 rs = dma_rsrc(base, (unsigned)vol * pitch2);
+    const unsigned cb = (unsigned)((in0 ? c0 : c0 - p.C0) * 2);
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+      unsigned off;
+      int dst;
+      bool in;
+      xf_unit(XNA + i * NT + tid, off, dst, in);
+      dma_buffer_b128(rs, in ? off * pitch2 + cb + (tid & 7) * 16 : OOB, 0,
+                      lds_offset(smem) + (unsigned)(S::G0X + (i * NT + wave * 64) * 16));
+    }
+  };
+  auto xf_late_store = [&]() {
+#pragma unroll
+    for (int i = 0; i < XL; i++) {
+      unsigned off;
+      int dst;
+      bool in;
+      xf_unit(XNA + i * NT + tid, off, dst, in);
+      xf_store(*reinterpret_cast<const E8*>(smem + S::G0X + (i * NT + tid) * 16), dst, in);
     }
   };
 
@@ -282,9 +349,14 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
     // barrier, then the 27 taps. FIRST: the accumulators start from the first MFMA (C = 0).
     auto run_chunk = [&](int j, auto first) {
       constexpr bool FIRST = decltype(first)::value;
-      // With the input transform the halo is staged through registers first, while no
-      // weight operands are held: a later chunk's staging runs beside live accumulators.
-      if constexpr (XF) halo_xf(j);
+      // With the input transform the first TD planes are staged through registers first,
+      // while no weight operands are held (a later chunk's staging runs beside live
+      // accumulators); the last two planes' loads follow the first taps' weights and stay
+      // in flight into the tap loop.
+      if constexpr (XF) {
+        xf_affine(j);
+        xf_early(j, !FIRST);
+      }
       const int late = XF ? 0 : halo_dma(j);
       if constexpr (NC > 0) {
         // Per-chunk weight walk; the asm keeps the step opaque, so that no tap's offset is
@@ -296,7 +368,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 #pragma unroll
         for (int t = 0; t < NA - 1; t++) load_a(aq[t]);
       }
-      if constexpr (NC > 0) {
+      if constexpr (XF) xf_late_load(j);
+      if constexpr (XF) {
+        // The early planes are written (their loads awaited above); the late ones and the
+        // weight requests stay in flight.
+      } else if constexpr (NC > 0) {
         // The first TD planes of the halo have landed once at most the last planes' DMAs
         // and the weight requests are in flight (the count is wave-uniform).
         static_assert(2 * S::RDMA <= 8, "late DMA counts handled below");
@@ -307,7 +383,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         vmcnt_wait<0>();
       }
       __syncthreads();
-      if constexpr (NC == 0) __syncthreads();   // the tap loop's barrier
+      if constexpr (NC == 0) {
+        if constexpr (XF) {
+          vmcnt_wait<0>();
+          xf_late_store();
+        }
+        __syncthreads();   // the tap loop's barrier
+      }
       if constexpr (NC > 0) {
 #pragma unroll
         for (int c = 0; c < NC; c++) bq[0][c] = *reinterpret_cast<const E8*>(smem + bb[c]);
@@ -315,9 +397,11 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
         for (int t = 0; t < 27; t++) {
           if (t == TB) {
             // The last planes, first read by the taps kd = 1 (whose fragments are requested
-            // from tap 8 on): every wave's DMAs have landed once its weight requests older
-            // than tap TB's have.
+            // from tap 8 on): every wave's DMAs (or late loads) have landed once its weight
+            // requests older than tap TB's have; with the input transform each thread then
+            // writes its late units.
             vmcnt_wait<(NA - 1) * 2>();
+            if constexpr (XF) xf_late_store();
             __syncthreads();
           }
           // Issue order, pinned by scheduling barriers: per column the MFMA pair of this
