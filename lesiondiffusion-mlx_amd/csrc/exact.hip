@@ -22,6 +22,8 @@
 #include "common.h"
 
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 
 namespace ldx {
 
@@ -244,6 +246,227 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(const float* __restr
   for (int d = 0; d < D; d++) op[d] = acc[d] * inv;
 }
 
+// ------------------------------------------------------------------ attention (MFMA)
+// FP32 attention on the fp16 matrix units in the reference's split form
+// (_attention.py:19-28, 217-280): Q (scaled by scale * log2(e) in FP32), K, V and every
+// probability p become hi = half(x) and lo = half((x - hi) * 2^11); S = Qh Kh +
+// 2^-11 (Qh Kl + Ql Kh) and O = Ph Vh + 2^-11 (Ph Vl + Pl Vh), each in two FP32
+// accumulators -- three fp16 products per FP32 product, only lo x lo dropped (about
+// 2^-22 relative). The online softmax is FP32: running maximum (the exact base, moved
+// every block it rises), exp2 of the log2-scaled scores, the row sum over the unrounded
+// probabilities.
+//
+// Workgroup: 4 waves x 32 queries of one (batch, head); each wave computes S^T = K Q^T
+// for a 32-key block (rows = keys permuted by split_key_row, columns = queries), so the
+// lane's 16 scores are the B operand of O^T = V^T P^T as they lie, as in the fp16 kernels.
+// 32-key tiles of K and V are loaded as FP32 into registers one block ahead, split, and
+// stored as four fp16 planes (Kh, Kl rows permuted; Vh, Vl) in LDS, double-buffered with
+// one barrier per block; the V^T operands are read with the transposing LDS read.
+struct SplitAttnParams {
+  int B, H, L, LK;
+  const float* q; int64_t qs0, qs1, qs2;
+  const float* k; int64_t ks0, ks1, ks2;
+  const float* v; int64_t vs0, vs1, vs2;
+  float* o; int64_t os0, os1, os2;
+  float c;  // scale * log2(e)
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// The key permutation of the fp16 kernels: bits 2 and 3 of the row swapped, so that a
+// lane's eight probabilities of one PV k-step are eight consecutive keys.
+__device__ __forceinline__ int split_key_row(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
+__device__ __forceinline__ float split_halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float split_halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+__device__ __forceinline__ f32x16 mfma_h(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <int D>
+__global__ __launch_bounds__(256) void attention_split_kernel(SplitAttnParams p) {
+  constexpr int KB = 32;                 // keys per block
+  constexpr int DK = D / 16, DB = D / 32;
+  constexpr int KP = D + 8;              // plane pitch (halves)
+  constexpr int PL = KB * KP;            // halves per plane
+  constexpr int CH = KB * D / 4;         // 4-float chunks of an FP32 tile
+  constexpr int CPT = CH / 256;          // of them per thread, for K and for V
+  static_assert(D == 32 || D == 64, "head widths 32 and 64");
+  static_assert(CH % 256 == 0, "whole chunks per thread");
+  __shared__ __attribute__((aligned(16))) f16 smem[2 * 4 * PL];   // [buffer][Kh, Kl, Vh, Vl]
+
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hf = lane >> 5, col = lane & 31;
+  int wg;
+  {
+    const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
+    wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
+  }
+  const int nqb = (p.L + 127) / 128;
+  const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
+  const int q0 = qblk * 128 + wave * 32;
+  const float* qb = p.q + (int64_t)b * p.qs0 + (int64_t)h * p.qs2;
+  const float* kb_ = p.k + (int64_t)b * p.ks0 + (int64_t)h * p.ks2;
+  const float* vb_ = p.v + (int64_t)b * p.vs0 + (int64_t)h * p.vs2;
+
+  // Q^T fragments, scaled and split: lane holds query q0 + col, dims 16 dk + 8 hf .. + 7.
+  const int qi = min(q0 + col, p.L - 1);
+  f16x8 qh[DK], ql[DK];
+#pragma unroll
+  for (int dk = 0; dk < DK; dk++) {
+    const float* src = qb + (int64_t)qi * p.qs1 + dk * 16 + 8 * hf;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src), c4 = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      // The product is pinned as one fp32 value: left to contraction, the compiler rounds
+      // q * c to fp16 once for one use (v_fma_mix) and via fp32 for the other, and where
+      // the two roundings differ, hi and lo no longer split the same value.
+      float x = (e < 4 ? a[e] : c4[e - 4]) * p.c;
+      asm volatile("" : "+v"(x));
+      const f16 hi = (f16)x;
+      qh[dk][e] = hi;
+      ql[dk][e] = (f16)((x - (float)hi) * 2048.0f);
+    }
+  }
+
+  // The thread's chunks of a tile: chunk i covers key (tid + 256 i) / (D / 4), dims
+  // 4 ((tid + 256 i) % (D / 4)) .. + 3; loads through buffer resources ending at the last
+  // key, so rows past the sequence read zeros.
+  f32x4 kst[CPT], vst[CPT];
+  auto load_tile = [&](int kbase) {
+    const int rows = min(KB, p.LK - kbase);
+    const auto kr = make_rsrc(kb_ + (int64_t)kbase * p.ks1, (unsigned)(((rows - 1) * p.ks1 + D) * 4));
+    const auto vr = make_rsrc(vb_ + (int64_t)kbase * p.vs1, (unsigned)(((rows - 1) * p.vs1 + D) * 4));
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int ch = threadIdx.x + 256 * i, key = ch / (D / 4), d0 = (ch % (D / 4)) * 4;
+      kst[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, (int)((key * p.ks1 + d0) * 4), 0, 0));
+      vst[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, (int)((key * p.vs1 + d0) * 4), 0, 0));
+    }
+  };
+  auto store_tile = [&](int buf) {
+    f16* base = smem + buf * 4 * PL;
+#pragma unroll
+    for (int i = 0; i < CPT; i++) {
+      const int ch = threadIdx.x + 256 * i, key = ch / (D / 4), d0 = (ch % (D / 4)) * 4;
+      f16x4 kh, kl, vh, vl;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        kh[e] = (f16)kst[i][e];
+        kl[e] = (f16)((kst[i][e] - (float)kh[e]) * 2048.0f);
+        vh[e] = (f16)vst[i][e];
+        vl[e] = (f16)((vst[i][e] - (float)vh[e]) * 2048.0f);
+      }
+      const int kr = split_key_row(key) * KP + d0, vrow = key * KP + d0;
+      *reinterpret_cast<f16x4*>(base + kr) = kh;
+      *reinterpret_cast<f16x4*>(base + PL + kr) = kl;
+      *reinterpret_cast<f16x4*>(base + 2 * PL + vrow) = vh;
+      *reinterpret_cast<f16x4*>(base + 3 * PL + vrow) = vl;
+    }
+  };
+  // V^T operand of a PV k-step (rows = dims): in each 16-lane group g, lane i reads row
+  // 8 (g / 2) + i / 4 (+ 4 for the second half, + 16 per k-step) at dims 16 (g % 2) +
+  // 4 (i % 4) (+ 32 per block of O^T rows).
+  const int vtr0 = (8 * (lane >> 5) + ((lane & 15) >> 2)) * KP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  auto read_vt = [&](const f16* plane, int ks, int db) {
+    const f16* va = plane + vtr0 + ks * 16 * KP + db * 32;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)((__attribute__((address_space(3))) char*)(va)));
+    const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (lds_s16x4*)((__attribute__((address_space(3))) char*)(va + 4 * KP)));
+    return __builtin_bit_cast(f16x8, (s16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]});
+  };
+
+  f32x16 oh[DB], ox[DB];
+#pragma unroll
+  for (int i = 0; i < DB; i++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) { oh[i][e] = 0.f; ox[i][e] = 0.f; }
+  float m = -INFINITY, l = 0.f;
+  const int nblk = (p.LK + KB - 1) / KB;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int it = 0; it < nblk; it++) {
+    const int kbase = it * KB;
+    if (it + 1 < nblk) load_tile(kbase + KB);
+    const f16* Kh = smem + (it & 1) * 4 * PL;
+    const f16* Kl = Kh + PL;
+    const f16* Vh = Kh + 2 * PL;
+    const f16* Vl = Kh + 3 * PL;
+    f32x16 sh = {}, sx = {};
+#pragma unroll
+    for (int dk = 0; dk < DK; dk++) {
+      const int d = dk * 16 + 8 * hf;
+      const f16x8 kh = *reinterpret_cast<const f16x8*>(Kh + col * KP + d);
+      const f16x8 kl = *reinterpret_cast<const f16x8*>(Kl + col * KP + d);
+      sh = mfma_h(kh, qh[dk], sh);
+      sx = mfma_h(kh, ql[dk], sx);
+      sx = mfma_h(kl, qh[dk], sx);
+    }
+    // Lane holds keys kbase + 16 (e / 8) + 8 hf + e % 8 of query q0 + col (log2-scaled).
+    float s[16], top = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int key = kbase + 16 * (e >> 3) + 8 * hf + (e & 7);
+      s[e] = key < p.LK ? sh[e] + sx[e] * (1.0f / 2048.0f) : -INFINITY;
+      top = fmaxf(top, s[e]);
+    }
+    const float mn = fmaxf(m, split_halves_max(top));
+    const float alpha = exp2f(m - mn);
+    m = mn;
+    f16x8 ph[2], plo[2];
+    float sum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const float pv = exp2f(s[e] - mn);
+      sum += pv;
+      const f16 hi = (f16)pv;
+      ph[e >> 3][e & 7] = hi;
+      plo[e >> 3][e & 7] = (f16)((pv - (float)hi) * 2048.0f);
+    }
+    l = l * alpha + sum;
+    if (__ballot(alpha != 1.f)) {
+#pragma unroll
+      for (int db = 0; db < DB; db++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) { oh[db][e] *= alpha; ox[db][e] *= alpha; }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int db = 0; db < DB; db++) {
+        const f16x8 vh = read_vt(Vh, ks, db), vl = read_vt(Vl, ks, db);
+        oh[db] = mfma_h(vh, ph[ks], oh[db]);
+        ox[db] = mfma_h(vh, plo[ks], ox[db]);
+        ox[db] = mfma_h(vl, ph[ks], ox[db]);
+      }
+    if (it + 1 < nblk) store_tile((it + 1) & 1);
+    __syncthreads();
+  }
+  l = split_halves_sum(l);
+  const int qo = q0 + col;
+  if (qo < p.L) {
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    float* orow = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2 + (int64_t)qo * p.os1;
+#pragma unroll
+    for (int db = 0; db < DB; db++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        f32x4 out;
+#pragma unroll
+        for (int r = 0; r < 4; r++) out[r] = (oh[db][j * 4 + r] + ox[db][j * 4 + r] * (1.0f / 2048.0f)) * inv;
+        *reinterpret_cast<f32x4*>(orow + db * 32 + j * 8 + 4 * hf) = out;
+      }
+  }
+}
+
 static unsigned grid_for(int64_t n) {
   const int64_t g = (n + 255) / 256;
   return (unsigned)(g < 8192 ? g : 8192);
@@ -341,9 +564,39 @@ int attention_f32(const ldx_attention_args* a, void* stream) {
   if (a->batch < 1 || a->heads < 1 || a->q_len < 1 || a->kv_len < 1) return fail("attention (fp32): empty input");
   if (a->mask) return fail("attention (fp32): masks are not supported");
   if ((int64_t)a->batch * a->heads > 65535) return fail("attention (fp32): too many (batch, head) pairs");
-  const dim3 grid((unsigned)((a->q_len + 255) / 256), (unsigned)(a->batch * a->heads));
   const float c = a->scale * 1.44269504088896341f;
   hipStream_t st = as_stream(stream);
+  // Head widths 32 and 64 with 16-byte rows run on the matrix units in the split form
+  // (LDX_ATTN_F32=valu keeps the VALU kernel, for comparison); width 16 and other
+  // layouts on the VALU kernel.
+  const int D = a->head_dim;
+  bool aligned = true;
+  const int64_t* ss[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+  const void* ps[4] = {a->q, a->k, a->v, a->o};
+  for (int i = 0; i < 4; i++) {
+    if ((uintptr_t)ps[i] % 16) aligned = false;
+    for (int j = 0; j < 3; j++)
+      if (ss[i][j] % 4) aligned = false;
+  }
+  const char* env = getenv("LDX_ATTN_F32");
+  if ((D == 32 || D == 64) && aligned && !(env && strcmp(env, "valu") == 0)) {
+    // In-tile offsets are 32-bit: 32 key rows of K and of V.
+    for (int i = 1; i < 3; i++)
+      if (ss[i][1] < 0 || ss[i][1] > (1 << 24)) return fail("attention (fp32): key stride out of range");
+    const int64_t n = (int64_t)((a->q_len + 127) / 128) * a->heads * a->batch;
+    if (n > 0x7fffffff) return fail("attention (fp32): grid too large");
+    SplitAttnParams sp{};
+    sp.B = a->batch; sp.H = a->heads; sp.L = a->q_len; sp.LK = a->kv_len;
+    sp.q = (const float*)a->q; sp.qs0 = a->q_stride[0]; sp.qs1 = a->q_stride[1]; sp.qs2 = a->q_stride[2];
+    sp.k = (const float*)a->k; sp.ks0 = a->k_stride[0]; sp.ks1 = a->k_stride[1]; sp.ks2 = a->k_stride[2];
+    sp.v = (const float*)a->v; sp.vs0 = a->v_stride[0]; sp.vs1 = a->v_stride[1]; sp.vs2 = a->v_stride[2];
+    sp.o = (float*)a->o; sp.os0 = a->o_stride[0]; sp.os1 = a->o_stride[1]; sp.os2 = a->o_stride[2];
+    sp.c = c;
+    if (D == 32) hipLaunchKernelGGL(attention_split_kernel<32>, dim3((unsigned)n), dim3(256), 0, st, sp);
+    else hipLaunchKernelGGL(attention_split_kernel<64>, dim3((unsigned)n), dim3(256), 0, st, sp);
+    return check_launch("attention (fp32, split)");
+  }
+  const dim3 grid((unsigned)((a->q_len + 255) / 256), (unsigned)(a->batch * a->heads));
 #define LDX_ATT32(D_)                                                                                           \
   hipLaunchKernelGGL(attention_f32_kernel<D_>, grid, dim3(256), 0, st, (const float*)a->q, a->q_stride[0],     \
                      a->q_stride[1], a->q_stride[2], (const float*)a->k, a->k_stride[0], a->k_stride[1],       \

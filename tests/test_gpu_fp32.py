@@ -162,6 +162,51 @@ def test_fp32_attention_matches_float64(pkg, dev, lq, lk, d) -> None:
     np.testing.assert_allclose(host(o), oatt.attention(q, k, v, d ** -0.5), rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize(("batch", "length", "keys", "heads"), [(1, 96, 64, 2), (2, 32, 160, 1), (1, 1056, 96, 2)])
+def test_fp32_attention_reference_cases(pkg, dev, batch, length, keys, heads) -> None:
+    """The reference's FP32 flash-attention cases (tests/test_native_kernels.py:395-458:
+    32-wide heads, q and k scaled by 2 for peaked rows that move the running maximum) at
+    its FP32 bound, atol 2e-5 -- here on the split-fp16 MFMA kernel."""
+    rng = np.random.default_rng(length + keys)
+    q, k, v = ((rng.normal(size=(batch, heads, n, 32)) * sc).astype(np.float32).astype(np.float64)
+               for n, sc in ((length, 2.0), (keys, 2.0), (keys, 1.0)))
+    o = pkg.ops.attention(dev32(q, dev), dev32(k, dev), dev32(v, dev), 32 ** -0.5)
+    torch.cuda.synchronize()
+    got = host(o)
+    assert np.all(np.isfinite(got))
+    np.testing.assert_allclose(got, oatt.attention(q, k, v, 32 ** -0.5), rtol=0, atol=2e-5)
+
+
+def test_fp32_attention_lmnet_length(pkg, dev) -> None:
+    """LMNet's 23,104-token FP32 self-attention (two 32-wide heads; mlx_model.py:74-76,
+    _attention.py:27-28) on the split-fp16 MFMA kernel, every 97th query row against float64
+    at the reference's FP32 bound (atol 2e-5)."""
+    n, heads = 23104, 2
+    rng = np.random.default_rng(23104)
+    q, k, v = ((rng.normal(size=(1, heads, n, 32)) * sc).astype(np.float32) for sc in (2.0, 2.0, 1.0))
+    print(f"fp32 attention {n} tokens x {heads} heads", flush=True)
+    o = pkg.ops.attention(dev32(q, dev), dev32(k, dev), dev32(v, dev), 32 ** -0.5)
+    torch.cuda.synchronize()
+    rows = np.arange(0, n, 97)
+    got = host(o)[:, :, rows]
+    want = oatt.attention(q[:, :, rows].astype(np.float64), k.astype(np.float64), v.astype(np.float64), 32 ** -0.5)
+    np.testing.assert_allclose(got, want, rtol=0, atol=2e-5)
+
+
+@pytest.mark.parametrize("d", [32, 64])
+def test_fp32_attention_split_kernel_agrees_with_the_valu_kernel(pkg, dev, monkeypatch, d) -> None:
+    """The split-fp16 MFMA kernel and the FP32 VALU flash kernel (LDX_ATTN_F32=valu) on the
+    same ragged inputs: both within FP32 error of each other."""
+    rng = np.random.default_rng(d)
+    q, k, v = (rng.normal(size=(2, 3, n, d)).astype(np.float32) for n in (257, 333, 333))
+    args = [dev32(t, dev) for t in (q, k, v)]
+    mfma = host(pkg.ops.attention(*args, d ** -0.5))
+    monkeypatch.setenv("LDX_ATTN_F32", "valu")
+    valu = host(pkg.ops.attention(*args, d ** -0.5))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(mfma, valu, rtol=2e-5, atol=2e-6)
+
+
 def test_fp32_unet_matches_recorded_torch(pkg, dev) -> None:
     """LMNet's FP32 network (the ``unet_mask`` recording: cross attention to a context, 16-wide
     heads) at the reference's FP32 bound, atol 2e-6, rtol 2e-5."""
