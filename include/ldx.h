@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (10); bumped on any change to the structs below or the entry points. */
+/* ABI version (11); bumped on any change to the structs below or the entry points. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -131,14 +131,18 @@ int ldx_dense_ln(const ldx_conv3d_args* args, const float* gamma, const float* b
  * (only lo x lo is dropped, about 2^-22 relative; |v| < 65504). The weight is the stacked
  * split of ldx_pack_weight_exact; the prologue (affine, SiLU), the epilogue (bias + shift,
  * scale, residual, GELU / SiLU) and y are FP32, with no rounding to 16 bits. upsample = 1
- * takes the unfolded 3x3x3 weight (the conv runs on the upsampled grid). A workspace of
- * ldx_conv3d_workspace_bytes() bytes is required (the split input and the FP32 products).
- * ldx_conv3d_stats and ldx_dense_ln take fp16 / bf16 only. */
+ * takes the unfolded 3x3x3 weight (the conv runs on the upsampled grid). One launch, no
+ * workspace (ldx_conv3d_workspace_bytes() is 0). ldx_conv3d_stats and ldx_dense_ln take
+ * fp16 / bf16 only. */
 int ldx_pack_weight_exact(const float* weight, int32_t out_c, int32_t in_c, int32_t ksize, void* packed,
                           void* stream);
 /* ldx_pack_weight_exact: a Torch-layout FP32 (O, C, K, K, K) (or dense (O, C), K = 1) weight
- * as the fp16 fragment-major packing (ldx_pack_weight) of 2O x 2C rows [[hi(W), 0],
- * [lo(W), hi(W)]]: ldx_packed_weight_elems(2 O, 2 C, K, 0) halves. */
+ * (_nax_conv.py:343-364 splits the same values) as two fp16 planes, hi(W) then
+ * lo(W) = half((W - hi(W)) * 2^11), each [NRB][NKC][K^3][64][8] with NRB = 2*ceil(O/64),
+ * NKC = 2*ceil(C/32): fragment ((rb*NKC + kc)*K^3 + tap) holds lane l's eight values
+ * W[rb*32 + l%32, kc*16 + 8*(l/32) + e, tap] at l*8 (zero past O or C).
+ * ldx_packed_weight_exact_elems(O, C, K) halves in all (0 for a bad shape). */
+size_t ldx_packed_weight_exact_elems(int32_t out_c, int32_t in_c, int32_t ksize);
 
 /* Pack a Torch-layout fp16 or bf16 weight (O, C, K, K, K) (K = 3 or 1; a dense (O, C)
  * weight is K = 1; a pure rearrangement of 16-bit values, the same for both types) into

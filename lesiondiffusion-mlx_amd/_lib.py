@@ -119,6 +119,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_step_advance": (c_i32, [c_vp, c_vp]),
     "ldx_vq_squared_norms4": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_vp]),
     "ldx_pack_weight_exact": (c_i32, [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp]),
+    "ldx_packed_weight_exact_elems": (ctypes.c_size_t, [c_i32, c_i32, c_i32]),
     "ldx_group_norm_affine_f32": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32, c_i64, c_i32,
                                           c_vp, c_vp, c_f32, c_vp, c_vp]),
     "ldx_layer_norm_f32": (c_i32, [c_vp, c_i64, c_i64, c_i32, c_vp, c_vp, c_f32, c_vp, c_i64, c_vp]),
@@ -131,7 +132,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            c_vp]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 def _load() -> ctypes.CDLL:

@@ -50,9 +50,7 @@ struct ConvParams {
   int NKC;                 // 16-channel K fragments of the packed weight
   int NOB;                 // 32-row output blocks of the packed weight
   int split, cps;          // split-K: channel-chunk ranges of cps chunks each
-  float* part;             // split > 1 or raw: fp32 partial sums [split][B * output voxels][O]
-  int raw;                 // 1: the epilogue leaves the raw fp32 sums in part (plane sidx) even
-                           // unsplit -- the products of the exact fp32 mode, finished elsewhere
+  float* part;             // split > 1: fp32 partial sums [split][B * output voxels][O]
   const E* x0; int64_t x0p;
   const E* x1; int64_t x1p;
   const E* w;
@@ -278,7 +276,7 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
   const int o = ec.o, nch = ec.nch;
   const bool vec8 = ec.vec8;
   const int ovol = p.OD * p.OH * p.OW;
-  const bool partial = p.split > 1 || p.raw;
+  const bool partial = p.split > 1;
   const bool pref_res = p.res && vec8 && !partial;
   // One copy of the store loop per activation: no per-element branch on it.
   auto finish = [&](auto act_c) {
@@ -1542,7 +1540,7 @@ static int launch_dense(ConvParams p, hipStream_t st) {
   p.rTW = 1.0f / (float)BV; p.rTH = 1.0f;
   p.NBD = 1; p.NBH = 1; p.NBW = (NV + BV - 1) / BV;
   p.split = 1;
-  if (!p.raw) p.part = nullptr;
+  p.part = nullptr;
   const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
   if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
   const size_t lds = (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
@@ -1561,7 +1559,7 @@ static int launch_dense_ksplit(ConvParams p, hipStream_t st) {
   p.rTW = 1.0f / (float)BV; p.rTH = 1.0f;
   p.NBD = 1; p.NBH = 1; p.NBW = (NV + BV - 1) / BV;
   p.split = 1;
-  if (!p.raw) p.part = nullptr;
+  p.part = nullptr;
   const int64_t nwg = (int64_t)p.NBW * ((p.O + BO - 1) / BO) * p.B;
   if (nwg > 0x7fffffff) return fail("conv3d: grid too large");
   const size_t lds = (size_t)(3 * FO * FV * 1024 + 32 * (FO * 32 + 4) + (LN ? 256 + 1024 : 0)) * sizeof(float);
@@ -1625,8 +1623,7 @@ static int launch_reduce(ConvParams& p, hipStream_t st, const char* what) {
 // One conv, as planned for these arguments. stats: also the GroupNorm partial moments of
 // the output (null: none). With dry, nothing is launched: *chunks receives the voxel
 // blocks per batch item the moments are kept for (0: this plan keeps none).
-static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t* chunks, void* stream,
-                      float* raw_part = nullptr) {
+static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t* chunks, void* stream) {
   ConvParams p;
   Tile t;
   size_t lds;
@@ -1636,33 +1633,6 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
   int rc = plan_conv(a, p, t, lds, vec, ws);
   if (rc != LDX_OK) return rc;
   hipStream_t st = as_stream(stream);
-  if (raw_part) {
-    // Raw fp32 sums into raw_part ([B * output voxels][O]), one pass (no split-K, no moments).
-    p.raw = 1;
-    p.part = raw_part;
-    p.split = 1;
-    p.cps = (p.C + t.CC - 1) / t.CC;
-    if (use_dense(a, vec)) return run_dense(p, st);
-    StreamParams sp;
-    if (conv3d_stream_plan(a, &sp, false) && sp.split == 1) {
-      sp.raw = 1;
-      sp.part = raw_part;
-      return conv3d_stream_launch(sp, st);
-    }
-    const int grid_z = p.B * (p.upsample ? 8 : 1);
-#define LDX_TILE(WO_, WV_, FO_, FV_, KSPL_)                                             \
-  if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_ && t.KSPL == KSPL_) \
-    return dispatch_k<WO_, WV_, FO_, FV_, KSPL_>(p, t.CC, vec, grid_z, st, lds);
-    LDX_TILE(1, 4, 1, 2, 1)
-    LDX_TILE(1, 4, 1, 1, 1)
-    LDX_TILE(1, 4, 2, 2, 1)
-    LDX_TILE(1, 4, 2, 1, 1)
-    LDX_TILE(2, 2, 2, 2, 1)
-    LDX_TILE(2, 2, 1, 1, 1)
-    LDX_TILE(1, 4, 2, 2, 2)
-#undef LDX_TILE
-    return fail("conv3d: no kernel for tile");
-  }
   const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
   // Moments need the 16-byte epilogue; the split-K reduce keeps them for O <= 512.
   const bool can_stats = p.O % 8 == 0 && p.ep_vec;
@@ -1734,13 +1704,6 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
 #undef LDX_TILE
   if (rc != LDX_OK || p.split == 1) return rc;
   return launch_reduce(p, st, "conv3d: split reduce");
-}
-
-// The conv's raw fp32 sums (no bias, shift, scale, residual, rounding or activation) into
-// part [batch * output voxels][out_c]: the product pass of the exact fp32 mode.
-int conv3d_raw(const ldx_conv3d_args* a, float* part, void* stream) {
-  if (!part) return fail("conv3d (raw): null partial buffer");
-  return conv3d_run(a, nullptr, false, nullptr, stream, part);
 }
 
 int conv3d_entry(const ldx_conv3d_args* a, void* stream) {

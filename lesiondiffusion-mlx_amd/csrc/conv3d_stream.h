@@ -17,8 +17,7 @@ struct StreamParams {
   UDiv dv_nob, dv_nbr, dv_nbw, dv_nbh, dv_g1;
   int split, cps;           // split-K: workgroup ranges of cps channel chunks (split > 1)
   int g1;                   // workgroups per split: bricks x output blocks x batch items
-  float* part;              // split > 1 or raw: fp32 partial sums [split][B * D * H * W][O]
-  int raw;                  // 1: leave the raw fp32 sums in part even unsplit (exact fp32 mode)
+  float* part;              // split > 1: fp32 partial sums [split][B * D * H * W][O]
   const E* x0; int64_t x0p;
   const E* x1; int64_t x1p;
   const E* w;

@@ -394,7 +394,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // The epilogue operands of these rows -- bias (+ per-batch-item bias), fp16 shift and
   // residual -- requested before the partial rows are written, which hides their latency
   // (and none of these loads delays the prologue's DMA).
-  const bool partial = p.split > 1 || p.raw;
+  const bool partial = p.split > 1;
   f32x4 bv0 = {0.f, 0.f, 0.f, 0.f}, bv1 = {0.f, 0.f, 0.f, 0.f};
   E8 sv = {};
   E8 res[4];

@@ -4,20 +4,21 @@
 // * conv3d / dense layers in the split-FP16 form of _nax_conv.py:26-34, 210-237: each FP32
 //   value v becomes hi = half(v) and lo = half((v - hi) * 2^11); hi x hi products go to one
 //   FP32 sum, hi x lo + lo x hi to another, scaled back by 2^-11 (only lo x lo is dropped:
-//   about 2^-22 relative). The products run on this library's fp16 conv kernels -- the
-//   input as 2C fp16 channels [hi | lo], the weights stacked into 2O rows [[W_hi, 0],
-//   [W_lo, W_hi]] (one block of zero products: four fp16 products per FP32 product
-//   instead of three, for reuse of the tuned kernels), their FP32 sums left raw -- and
-//   exact_combine_kernel finishes y = ((S_hh + S_x * 2^-11) + (bias + shift)) * scale +
-//   residual in FP32. The input split applies the GroupNorm affine and SiLU in FP32 first
-//   (_nax_conv.py:128-136) and, for a conv of a nearest-2x upsampling, the upsampling (the
-//   conv then runs on the upsampled grid with the unfolded weights, so no folded weight is
-//   re-split: the reference folds in FP32 before splitting, the same sums in another order).
+//   about 2^-22 relative). conv3d_exact_kernel does it in one launch: the FP32 input is
+//   prepared (GroupNorm affine and SiLU in FP32, _nax_conv.py:128-136; a second input;
+//   for a conv of a nearest-2x upsampling the upsampling, so that the conv runs on the
+//   upsampled grid with the unfolded weights and no folded weight is re-split -- the
+//   reference folds in FP32 before splitting, the same sums in another order), split into
+//   hi / lo planes in LDS, three MFMAs per fragment pair accumulate the two sums, and the
+//   epilogue y = ((S_hh + S_x * 2^-11) + (bias + shift)) * scale + residual (then GELU or
+//   SiLU) runs in FP32 on the accumulators.
 // * GroupNorm statistics and LayerNorm of FP32 tensors, FP32 timestep features.
-// * attention in FP32 for head widths 16 / 32 / 64: a flash kernel on the VALU (the
-//   reference's FP32 SIMD kernel, _attention.py:52-145): one query per lane, 64-key K/V
-//   tiles in LDS shared by the workgroup's four waves, scores and P V as FP32 fused
-//   multiply-adds, online softmax with exp2 of log2(e)-scaled scores.
+// * attention in FP32: for head widths 32 / 64 on the matrix units in the reference's split
+//   form (_attention.py:19-28, 217-280; attention_split_kernel), else (width 16, unaligned
+//   tensors) a flash kernel on the VALU (the reference's FP32 SIMD kernel,
+//   _attention.py:52-145): one query per lane, 64-key K/V tiles in LDS shared by the
+//   workgroup's four waves, scores and P V as FP32 fused multiply-adds, online softmax
+//   with exp2 of log2(e)-scaled scores.
 
 #include "common.h"
 
@@ -28,84 +29,38 @@
 namespace ldx {
 
 // ------------------------------------------------------------------ weights
-// The stacked split weight in the fragment-major layout of ldx_pack_weight for 2O rows and
-// 2C channels: row o < O holds [hi(W[o, c]) (c < C), 0]; row O + o holds [lo(W[o, c]),
-// hi(W[o, c])].
-__device__ __forceinline__ f16 split_hi(float v) { return (f16)v; }
-__device__ __forceinline__ f16 split_lo(float v) { return (f16)((v - (float)(f16)v) * 2048.0f); }
-
-__global__ void pack_weight_exact_kernel(const float* __restrict__ w, int O, int C, int taps, f16* __restrict__ out) {
-  const int O2 = 2 * O, C2 = 2 * C;
-  const int NOB = (O2 + 127) / 128 * 4, NKC = (C2 + 63) / 64 * 4;
-  const int64_t n = (int64_t)NOB * taps * NKC * 512;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int e = (int)(i & 7), l = (int)((i >> 3) & 63);
-    const int64_t frag = i >> 9;
-    const int kc = (int)(frag % NKC), tap = (int)((frag / NKC) % taps);
-    const int64_t ob = frag / ((int64_t)NKC * taps);
-    const int o2 = (int)ob * 32 + (l & 31);
-    const int c2 = kc * 16 + 8 * (l >> 5) + e;
-    f16 v = (f16)0.f;
-    if (o2 < O2 && c2 < C2) {
-      const int o = o2 < O ? o2 : o2 - O, c = c2 < C ? c2 : c2 - C;
-      const float wv = w[((int64_t)o * C + c) * taps + tap];
-      if (o2 < O) v = c2 < C ? split_hi(wv) : (f16)0.f;
-      else v = c2 < C ? split_lo(wv) : split_hi(wv);
-    }
-    out[i] = v;
-  }
+// The split weight as two fp16 planes, hi(W) then lo(W), each [NRB][NKC][taps][64][8]:
+// row block rb (32 output channels), 16-channel chunk kc and tap t hold one MFMA A
+// fragment -- lane l has row rb * 32 + l % 32, channels kc * 16 + 8 * (l / 32) + e -- so a
+// wave reads a fragment as one 1 KiB run and a chunk's taps lie one after another.
+// NRB = 2 * ceil(O / 64) (whole 64-row tiles), NKC = 4 * ceil(C / 64) (whole chunks of
+// every k-grouping); zero outside O x C.
+__host__ __device__ inline int64_t exact_plane_elems(int O, int C, int taps) {
+  return (int64_t)((O + 63) / 64 * 2) * ((C + 63) / 64 * 4) * taps * 512;
 }
 
-// ------------------------------------------------------------------ input split
-// out (fp16, NDHWC of the row grid, 2C channels, pitch 2C): [hi | lo] of the prepared input
-// prep(x) = silu(x * scale + offset) (as set), read from x0 (channels [0, C0)) and x1 (the
-// rest); with up, grid voxel (d, h, w) reads source voxel (d / 2, h / 2, w / 2).
-__global__ void split_exact_kernel(const float* __restrict__ x0, int64_t p0, int C0, const float* __restrict__ x1,
-                                   int64_t p1, int C, int B, int D, int H, int W, int up, const float* __restrict__ affine,
-                                   int silu, f16* __restrict__ out) {
-  const int RD = up ? 2 * D : D, RH = up ? 2 * H : H, RW = up ? 2 * W : W;
-  const int64_t n = (int64_t)B * RD * RH * RW * C;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % C);
-    int64_t r = i / C;
-    const int w = (int)(r % RW); r /= RW;
-    const int h = (int)(r % RH); r /= RH;
-    const int d = (int)(r % RD);
-    const int b = (int)(r / RD);
-    const int sd = up ? d >> 1 : d, sh = up ? h >> 1 : h, sw = up ? w >> 1 : w;
-    const int64_t sv = (((int64_t)b * D + sd) * H + sh) * W + sw;
-    float v = c < C0 ? x0[sv * p0 + c] : x1[sv * p1 + (c - C0)];
-    if (affine) v = v * affine[((int64_t)b * C + c) * 2] + affine[((int64_t)b * C + c) * 2 + 1];
-    if (silu) v = v / (1.0f + expf(-v));
-    const int64_t ov = (((int64_t)b * RD + d) * RH + h) * RW + w;
-    out[ov * 2 * C + c] = split_hi(v);
-    out[ov * 2 * C + C + c] = split_lo(v);
+__global__ void pack_weight_exact_kernel(const float* __restrict__ w, int O, int C, int taps, f16* __restrict__ out) {
+  const int NKC = (C + 63) / 64 * 4;
+  const int64_t plane = exact_plane_elems(O, C, taps);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < plane; i += (int64_t)gridDim.x * blockDim.x) {
+    const int e = (int)(i & 7), l = (int)((i >> 3) & 63);
+    const int64_t frag = i >> 9;
+    const int tap = (int)(frag % taps), kc = (int)((frag / taps) % NKC);
+    const int rb = (int)(frag / ((int64_t)taps * NKC));
+    const int o = rb * 32 + (l & 31), c = kc * 16 + 8 * (l >> 5) + e;
+    f16 hi = (f16)0.f, lo = (f16)0.f;
+    if (o < O && c < C) {
+      float wv = w[((int64_t)o * C + c) * taps + tap];
+      asm volatile("" : "+v"(wv));  // one rounding of wv feeds both halves
+      hi = (f16)wv;
+      lo = (f16)((wv - (float)hi) * 2048.0f);
+    }
+    out[i] = hi;
+    out[plane + i] = lo;
   }
 }
 
 __device__ __forceinline__ float gelu_erf32(float v) { return v * (1.0f + erff(v * 0.70710678118654752f)) * 0.5f; }
-
-// y[b, v, o] = act(((S[v, o] + S[v, O + o] * 2^-11) + (bias + shift)) * scale + res), FP32.
-__global__ void exact_combine_kernel(const float* __restrict__ part, int64_t nvox_b, int B, int O,
-                                     const float* __restrict__ bias, int bias_batched, const float* __restrict__ shift,
-                                     int64_t shiftp, float scale, const float* __restrict__ res, int64_t resp, int act,
-                                     float* __restrict__ y, int64_t yp) {
-  const int64_t n = (int64_t)B * nvox_b * O;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-    const int o = (int)(i % O);
-    const int64_t v = i / O;
-    const int b = (int)(v / nvox_b);
-    const float* s = part + v * 2 * O;
-    const float sum = s[o] + s[O + o] * (1.0f / 2048.0f);
-    float add = bias ? bias[(bias_batched ? (int64_t)b * O : 0) + o] : 0.f;
-    if (shift) add += shift[(int64_t)b * shiftp + o];
-    float t = (sum + add) * scale;
-    if (res) t += res[v * resp + o];
-    if (act == LDX_ACT_GELU) t = gelu_erf32(t);
-    else if (act == LDX_ACT_SILU) t = t / (1.0f + expf(-t));
-    y[v * yp + o] = t;
-  }
-}
 
 // ------------------------------------------------------------------ GroupNorm / LayerNorm
 // Per (group, batch item): Welford (count, mean, M2) per thread over its strided elements,
@@ -467,6 +422,382 @@ __global__ __launch_bounds__(256) void attention_split_kernel(SplitAttnParams p)
   }
 }
 
+// ------------------------------------------------------------------ conv (one pass)
+// y = act(((W_h x_h + (W_h x_l + W_l x_h) 2^-11) + (bias + shift)) * scale + residual) in one
+// launch: the FP32 input is read, prepared (GroupNorm affine, SiLU, nearest-2x upsampling,
+// concatenation of x1) and split into hi / lo planes in LDS; three MFMAs per fragment pair
+// (hi x hi into one FP32 accumulator, hi x lo and lo x hi into the other) and the FP32
+// epilogue on the accumulators. No workspace, no intermediate tensor.
+//
+// Workgroup: a brick of BD x BH x BW output voxels (whole 32-voxel MFMA columns) of one
+// batch item by 64 output channels, in KG k-groups (1, 2 or 4) of 2 x NCOL / NCW waves.
+// Wave (kg, w) owns row block w % 2 and NCW columns from w / 2 on, for the 16 channels kg
+// of each chunk of 16 KG channels. The brick's input halo, a chunk at a time, is staged as
+// hi / lo fp16 sub-planes ([k-group][halo voxel][16], 32 B per voxel), double-buffered:
+// the FP32 loads of the next chunk are issued at the chunk's first tap, and prepared and
+// stored one item every other tap from tap 4 on, beside the MFMAs; one barrier per
+// chunk. Weight fragments stream from the two-plane packing two taps ahead through a ring
+// of three register slots (27 taps: the slot of a tap is fixed). At the end the k-groups'
+// partial sums meet in LDS: with two groups of two columns per wave each wave hands one
+// column to its partner and finishes the other; otherwise groups 1.. hand over and group
+// 0 finishes. A sum over groups is S_g0 + S_g1 (+ S_g2 + S_g3), in that order. ksize 1
+// (FLAT) treats the voxels of all batch items as one row of 128-voxel bricks.
+struct ExactConvParams {
+  const float* x0; const float* x1;
+  int64_t p0, p1;
+  int C0, C, O;
+  int NCH;          // chunks of 16 KG channels
+  int NKC;          // 16-channel chunks of the packed weight (a multiple of 4)
+  int RD, RH, RW;   // row grid (the upsampled grid with up)
+  int ID, IH, IW;   // source grid
+  int OD, OH, OW;   // output grid
+  int up, vec_in, vec_out;
+  int nbd, nbh, nbw;  // bricks per output dimension (FLAT: nbw over all voxels)
+  int64_t nvox;       // FLAT: batch * voxels
+  const f16* w; int64_t wplane;  // two-plane weight, plane stride in halves
+  const float* affine; int silu;
+  const float* bias; int bias_batched;
+  const float* shift; int64_t shiftp;
+  float scale;
+  const float* res; int64_t resp;
+  int act;
+  float* y; int64_t yp;
+};
+
+template <int KS, int S, int BD, int BH, int BW, int KG, int NCW>
+struct ExactConvShape {
+  static constexpr bool FLAT = KS == 1;
+  static constexpr int PAD = KS / 2, TAPS = KS * KS * KS;
+  static constexpr int HD = (BD - 1) * S + KS, HH = (BH - 1) * S + KS, HW = (BW - 1) * S + KS;
+  static constexpr int NHV = HD * HH * HW;   // halo voxels
+  static constexpr int NCOL = BD * BH * BW / 32;
+  static constexpr int WPG = 2 * NCOL / NCW;  // waves per k-group: 2 row blocks x column sets
+  static constexpr int NT = 64 * WPG * KG;    // threads
+  static constexpr int GPV = 4 * KG;         // 4-channel groups per halo voxel and chunk
+  static constexpr int PL = NHV * 16;        // halves per sub-plane
+  static constexpr int BUF = 2 * KG * PL;    // halves per buffer (hi, lo x k-groups)
+  static constexpr int NIT = (NHV * GPV + NT - 1) / NT;  // staging items per thread
+  static constexpr int XCH = KG > 1 ? (KG == 2 ? NCW : KG - 1) * WPG * 2 * 16 * 64 * 4 : 0;  // exchange bytes
+  static constexpr int LDS = 2 * BUF * 2 > XCH ? 2 * BUF * 2 : XCH;
+  static_assert(BD * BH * BW % 32 == 0 && NCOL % NCW == 0, "whole columns per wave");
+  static_assert(NT <= 1024, "workgroup size");
+  static_assert(TAPS % 3 == 0 || TAPS == 1, "weight ring");
+  static_assert(KG == 1 || (KG == 2 && NCW <= 2 && !FLAT) || (KG == 4 && NCW == 1 && !FLAT), "k-group exchange");
+  static_assert(NT % GPV == 0, "a thread's channel group is fixed");
+};
+
+template <int KS, int S, int BD, int BH, int BW, int KG, int NCW>
+__global__ __launch_bounds__((ExactConvShape<KS, S, BD, BH, BW, KG, NCW>::NT)) void conv3d_exact_kernel(
+    ExactConvParams p) {
+  using SH = ExactConvShape<KS, S, BD, BH, BW, KG, NCW>;
+  constexpr int TAPS = SH::TAPS, NIT = SH::NIT, PL = SH::PL, GPV = SH::GPV, WPG = SH::WPG;
+  constexpr int CSETS = WPG / 2;   // column sets: wave w has columns w / 2 + CSETS j
+  extern __shared__ __align__(16) f16 smem[];   // [2 buffers][hi, lo][k-group][PL]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int kg = tid / (64 * WPG), wave = (tid >> 6) % WPG;
+  const int rb = wave & 1;
+  const int oblk = blockIdx.y;
+
+  // Brick origin (output grid) and batch item.
+  int b = 0, od0 = 0, oh0 = 0, ow0 = 0;
+  int64_t v0 = 0;   // FLAT: first voxel of the brick
+  if constexpr (SH::FLAT) {
+    v0 = (int64_t)blockIdx.x * 128;
+  } else {
+    int r = blockIdx.x;
+    const int bw = r % p.nbw; r /= p.nbw;
+    const int bh = r % p.nbh; r /= p.nbh;
+    const int bd = r % p.nbd;
+    b = r / p.nbd;
+    od0 = bd * BD; oh0 = bh * BH; ow0 = bw * BW;
+  }
+
+  // Staging: item i = tid + NT k covers halo voxel i / GPV, channels 4 (i % GPV) .. + 3 of
+  // the chunk (sub-plane (i % GPV) / 4); i % GPV is the same for all of a thread's items.
+  const int g = tid % GPV;
+  f32x4 pre[NIT];
+  f32x4 aff_s = {1.f, 1.f, 1.f, 1.f}, aff_o = {0.f, 0.f, 0.f, 0.f};
+  // Source voxel of each item's halo voxel, or -1 in the padding (or past the last FLAT
+  // voxel); the same for every chunk.
+  int sv[NIT];
+#pragma unroll
+  for (int k = 0; k < NIT; k++) {
+    const int i = tid + SH::NT * k, hv = i / GPV;
+    sv[k] = -1;
+    if (i >= SH::NHV * GPV) continue;
+    if constexpr (SH::FLAT) {
+      if (v0 + hv < p.nvox) sv[k] = (int)(v0 + hv);
+    } else {
+      const int hd = hv / (SH::HH * SH::HW), hh = (hv / SH::HW) % SH::HH, hw = hv % SH::HW;
+      const int rd = od0 * S - SH::PAD + hd, rh = oh0 * S - SH::PAD + hh, rw = ow0 * S - SH::PAD + hw;
+      if (rd < 0 || rd >= p.RD || rh < 0 || rh >= p.RH || rw < 0 || rw >= p.RW) continue;
+      const int sd = p.up ? rd >> 1 : rd, sh = p.up ? rh >> 1 : rh, sw = p.up ? rw >> 1 : rw;
+      sv[k] = ((b * p.ID + sd) * p.IH + sh) * p.IW + sw;
+    }
+  }
+  auto load_affine = [&](int bi, int c) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const bool in = c + e < p.C;
+      const float* af = p.affine + ((int64_t)bi * p.C + (in ? c + e : 0)) * 2;
+      aff_s[e] = in ? af[0] : 1.f;
+      aff_o[e] = in ? af[1] : 0.f;
+    }
+  };
+  auto load_chunk = [&](int kc) {
+    const int c = kc * 16 * KG + g * 4;
+    if (!SH::FLAT && p.affine) load_affine(b, c);
+    const bool in0 = c < p.C0;
+    const float* base = in0 ? p.x0 + c : p.x1 + (c - p.C0);
+    const int64_t pitch = in0 ? p.p0 : p.p1;
+#pragma unroll
+    for (int k = 0; k < NIT; k++) {
+      pre[k] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      if (sv[k] < 0 || c >= p.C) continue;
+      if (p.vec_in) {
+        pre[k] = *reinterpret_cast<const f32x4*>(base + sv[k] * pitch);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (c + e < p.C) pre[k][e] = c + e < p.C0 ? p.x0[sv[k] * p.p0 + c + e] : p.x1[sv[k] * p.p1 + (c + e - p.C0)];
+      }
+    }
+  };
+  // Prepare (affine, SiLU), split and store item k of the loaded chunk into buffer buf.
+  // Padding and channels past C stay zero (the conv pads the prepared input).
+  auto store_item = [&](int k, int kc, int buf) {
+    const int i = tid + SH::NT * k;
+    if (i >= SH::NHV * GPV) return;
+    const int hv = i / GPV;
+    const int c = kc * 16 * KG + g * 4;
+    const bool ok = sv[k] >= 0 && c < p.C;
+    if (SH::FLAT && ok && p.affine) load_affine((int)(sv[k] / ((int64_t)p.OD * p.OH * p.OW)), c);
+    f16x4 h4, l4;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      float v = pre[k][e];
+      if (p.affine) v = v * aff_s[e] + aff_o[e];
+      if (p.silu) v = v / (1.0f + expf(-v));
+      if (!ok || c + e >= p.C) v = 0.f;
+      asm volatile("" : "+v"(v));  // one value feeds both halves
+      const f16 vh = (f16)v;
+      h4[e] = vh;
+      l4[e] = (f16)((v - (float)vh) * 2048.0f);
+    }
+    f16* dst = smem + buf * SH::BUF + (g >> 2) * PL + hv * 16 + (g & 3) * 4;
+    *reinterpret_cast<f16x4*>(dst) = h4;
+    *reinterpret_cast<f16x4*>(dst + KG * PL) = l4;
+  };
+
+  // Columns of this wave: brick-local voxel of the lane and its halo voxel.
+  int hb[NCW];
+#pragma unroll
+  for (int j = 0; j < NCW; j++) {
+    const int v = ((wave >> 1) + CSETS * j) * 32 + (lane & 31);
+    if constexpr (SH::FLAT) {
+      hb[j] = v;
+    } else {
+      const int ld = v / (BH * BW), lh = (v / BW) % BH, lw = v % BW;
+      hb[j] = (ld * S * SH::HH + lh * S) * SH::HW + lw * S;
+    }
+  }
+
+  // Weight fragments: row block 2 * oblk + rb, 16-channel chunk KG kc + kg; (chunk, tap)
+  // runs consecutively.
+  const f16* wrow = p.w + ((int64_t)(2 * oblk + rb) * p.NKC + kg) * TAPS * 512 + lane * 8;
+  constexpr int R = TAPS == 1 ? 2 : 3;
+  f16x8 ah[R], al[R];
+  auto load_w = [&](int kc, int t, int slot) {
+    const f16* q = wrow + ((int64_t)kc * KG * TAPS + t) * 512;
+    ah[slot] = *reinterpret_cast<const f16x8*>(q);
+    al[slot] = *reinterpret_cast<const f16x8*>(q + p.wplane);
+  };
+
+  f32x16 acc_h[NCW], acc_x[NCW];
+#pragma unroll
+  for (int j = 0; j < NCW; j++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc_h[j][e] = acc_x[j][e] = 0.f;
+
+  // Prologue: chunk 0 staged, the first weight fragments in flight.
+  load_chunk(0);
+  load_w(0, 0, 0);
+  if constexpr (TAPS > 1) load_w(0, 1, 1);
+#pragma unroll
+  for (int k = 0; k < NIT; k++) store_item(k, 0, 0);
+  __syncthreads();
+
+  // First tap that stores a staged item of the next chunk (one every other tap).
+  constexpr int T0 = 4 + 2 * (NIT - 1) < TAPS ? 4 : TAPS - 1 - 2 * (NIT - 1);
+  static_assert(TAPS == 1 || T0 >= 1, "staging fits the tap loop");
+  const int half = 8 * (lane >> 5);
+  for (int kc = 0; kc < p.NCH; kc++) {
+    const int buf = kc & 1;
+    const bool more = kc + 1 < p.NCH;
+    const f16* xb = smem + buf * SH::BUF + kg * PL + half;
+    if constexpr (TAPS == 1) {
+      if (more) load_w(kc + 1, 0, 1);
+      if (more) load_chunk(kc + 1);
+      f16x8 xh[NCW], xl[NCW];
+#pragma unroll
+      for (int j = 0; j < NCW; j++) {
+        xh[j] = *reinterpret_cast<const f16x8*>(xb + hb[j] * 16);
+        xl[j] = *reinterpret_cast<const f16x8*>(xb + KG * PL + hb[j] * 16);
+      }
+#pragma unroll
+      for (int j = 0; j < NCW; j++) acc_h[j] = mfma_h(ah[0], xh[j], acc_h[j]);
+#pragma unroll
+      for (int j = 0; j < NCW; j++) acc_x[j] = mfma_h(ah[0], xl[j], acc_x[j]);
+#pragma unroll
+      for (int j = 0; j < NCW; j++) acc_x[j] = mfma_h(al[0], xh[j], acc_x[j]);
+      ah[0] = ah[1];
+      al[0] = al[1];
+      if (more) {
+#pragma unroll
+        for (int k = 0; k < NIT; k++) store_item(k, kc + 1, buf ^ 1);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < TAPS; t++) {
+        // Weights two taps ahead (into the slot tap t - 1 used), the next chunk's input
+        // after the first of them.
+        if (t + 2 < TAPS) load_w(kc, t + 2, (t + 2) % 3);
+        else if (more) load_w(kc + 1, t + 2 - TAPS, (t + 2) % 3);
+        if (t == 0 && more) load_chunk(kc + 1);
+        const int toff = ((t / 9) * SH::HH + (t / 3) % 3) * SH::HW + t % 3;
+        f16x8 xh[NCW], xl[NCW];
+#pragma unroll
+        for (int j = 0; j < NCW; j++) {
+          xh[j] = *reinterpret_cast<const f16x8*>(xb + (hb[j] + toff) * 16);
+          xl[j] = *reinterpret_cast<const f16x8*>(xb + KG * PL + (hb[j] + toff) * 16);
+        }
+        const int s = t % 3;
+#pragma unroll
+        for (int j = 0; j < NCW; j++) acc_h[j] = mfma_h(ah[s], xh[j], acc_h[j]);
+#pragma unroll
+        for (int j = 0; j < NCW; j++) acc_x[j] = mfma_h(ah[s], xl[j], acc_x[j]);
+#pragma unroll
+        for (int j = 0; j < NCW; j++) acc_x[j] = mfma_h(al[s], xh[j], acc_x[j]);
+        if (more && t >= T0 && (t - T0) % 2 == 0 && (t - T0) / 2 < NIT) store_item((t - T0) / 2, kc + 1, buf ^ 1);
+      }
+    }
+    __syncthreads();
+  }
+
+  // Two k-groups: with two columns per wave, wave (kg, w) leaves its partial sums of
+  // column 1 - kg in LDS (the halo buffers are free after the loop's last barrier) and
+  // finishes column kg with its partner's; with one, group 1 hands over and group 0
+  // finishes. Either way a sum is S_g0 + S_g1, in that order.
+  if constexpr (KG == 4) {
+    // Groups 1-3 hand over; group 0 adds ((S_g0 + S_g1) + S_g2) + S_g3.
+    float* xs = reinterpret_cast<float*>(smem);
+    auto slot = [&](int g1, int acc, int e) { return ((((g1 * WPG + wave) * 2 + acc) * 16 + e) * 64) + lane; };
+    if (kg > 0) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        xs[slot(kg - 1, 0, e)] = acc_h[0][e];
+        xs[slot(kg - 1, 1, e)] = acc_x[0][e];
+      }
+    }
+    __syncthreads();
+    if (kg > 0) return;
+#pragma unroll
+    for (int g1 = 0; g1 < 3; g1++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        acc_h[0][e] = acc_h[0][e] + xs[slot(g1, 0, e)];
+        acc_x[0][e] = acc_x[0][e] + xs[slot(g1, 1, e)];
+      }
+  }
+  if constexpr (KG == 2) {
+    float* xs = reinterpret_cast<float*>(smem);
+    auto slot = [&](int j, int acc, int e) { return ((((j * WPG + wave) * 2 + acc) * 16 + e) * 64) + lane; };
+    if constexpr (NCW == 2) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        xs[slot(1 - kg, 0, e)] = kg ? acc_h[0][e] : acc_h[1][e];
+        xs[slot(1 - kg, 1, e)] = kg ? acc_x[0][e] : acc_x[1][e];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float ph = xs[slot(kg, 0, e)], px = xs[slot(kg, 1, e)];
+        if (kg == 0) {
+          acc_h[0][e] = acc_h[0][e] + ph;
+          acc_x[0][e] = acc_x[0][e] + px;
+        } else {
+          acc_h[0][e] = ph + acc_h[1][e];
+          acc_x[0][e] = px + acc_x[1][e];
+        }
+      }
+    } else {
+      if (kg == 1) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          xs[slot(0, 0, e)] = acc_h[0][e];
+          xs[slot(0, 1, e)] = acc_x[0][e];
+        }
+      }
+      __syncthreads();
+      if (kg == 1) return;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        acc_h[0][e] = acc_h[0][e] + xs[slot(0, 0, e)];
+        acc_x[0][e] = acc_x[0][e] + xs[slot(0, 1, e)];
+      }
+    }
+  }
+
+  // Epilogue: lane (half, col) holds voxel col of each of its columns, channels
+  // 64 oblk + 32 rb + 8 q + 4 (lane / 32) + r in element 4 q + r.
+  const int64_t ovol = (int64_t)p.OD * p.OH * p.OW;
+  constexpr int NFIN = KG > 1 ? 1 : NCW;   // columns this wave finishes
+#pragma unroll
+  for (int j = 0; j < NFIN; j++) {
+    const int col = (wave >> 1) + CSETS * (KG == 2 && NCW == 2 ? kg : j);
+    const int v = col * 32 + (lane & 31);
+    int64_t ov;
+    int bi = b;
+    bool ok;
+    if constexpr (SH::FLAT) {
+      ov = v0 + v;
+      ok = ov < p.nvox;
+      bi = ok ? (int)(ov / ovol) : 0;
+    } else {
+      const int od = od0 + v / (BH * BW), oh = oh0 + (v / BW) % BH, ow = ow0 + v % BW;
+      ok = od < p.OD && oh < p.OH && ow < p.OW;
+      ov = (((int64_t)b * p.OD + od) * p.OH + oh) * p.OW + ow;
+    }
+    if (!ok) continue;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int o0 = oblk * 64 + rb * 32 + 8 * q + 4 * (lane >> 5);
+      if (o0 >= p.O) continue;
+      f32x4 t;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int o = o0 + r < p.O ? o0 + r : p.O - 1;
+        const float sum = acc_h[j][4 * q + r] + acc_x[j][4 * q + r] * (1.0f / 2048.0f);
+        float add = p.bias ? p.bias[(p.bias_batched ? (int64_t)bi * p.O : 0) + o] : 0.f;
+        if (p.shift) add += p.shift[(int64_t)bi * p.shiftp + o];
+        float u = (sum + add) * p.scale;
+        if (p.res) u += p.res[ov * p.resp + o];
+        if (p.act == LDX_ACT_GELU) u = gelu_erf32(u);
+        else if (p.act == LDX_ACT_SILU) u = u / (1.0f + expf(-u));
+        t[r] = u;
+      }
+      float* yo = p.y + ov * p.yp + o0;
+      if (p.vec_out && o0 + 3 < p.O) {
+        *reinterpret_cast<f32x4*>(yo) = t;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (o0 + r < p.O) yo[r] = t[r];
+      }
+    }
+  }
+}
+
 static unsigned grid_for(int64_t n) {
   const int64_t g = (n + 255) / 256;
   return (unsigned)(g < 8192 ? g : 8192);
@@ -478,22 +809,25 @@ using namespace ldx;
 
 // ------------------------------------------------------------------ entry points
 
+extern "C" size_t ldx_packed_weight_exact_elems(int32_t O, int32_t C, int32_t k) {
+  if (O < 1 || C < 1 || (k != 1 && k != 3)) return 0;
+  return (size_t)(2 * exact_plane_elems(O, C, k * k * k));
+}
+
 extern "C" int ldx_pack_weight_exact(const float* weight, int32_t O, int32_t C, int32_t k, void* packed, void* stream) {
   if (!weight || !packed) return fail("pack_weight_exact: null pointer");
   if (O < 1 || C < 1 || (k != 1 && k != 3)) return fail("pack_weight_exact: bad shape O=%d C=%d k=%d", O, C, k);
-  const int64_t n = (int64_t)ldx_packed_weight_elems(2 * O, 2 * C, k, 0);
+  const int64_t n = exact_plane_elems(O, C, k * k * k);
   hipLaunchKernelGGL(pack_weight_exact_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), weight, O, C,
                      k * k * k, (f16*)packed);
   return check_launch("pack_weight_exact");
 }
 
 namespace ldx {
-namespace f16_path {
-int conv3d_raw(const ldx_conv3d_args* a, float* part, void* stream);
-}  // namespace f16_path
 
-// Geometry of an exact-mode conv: the row grid the fp16 conv reads and its output voxels.
-static int exact_geometry(const ldx_conv3d_args* a, int64_t& row_vox, int64_t& out_vox) {
+// Geometry of an exact-mode conv: its row grid (the upsampled grid with upsample) and
+// output grid.
+static int exact_geometry(const ldx_conv3d_args* a, int64_t rg[3], int64_t og[3]) {
   if (!a) return fail("conv3d (fp32): null args");
   if (a->batch < 1 || a->in_d < 1 || a->in_h < 1 || a->in_w < 1 || a->c0 < 1 || a->c1 < 0 || a->out_c < 1)
     return fail("conv3d (fp32): bad shape");
@@ -502,26 +836,33 @@ static int exact_geometry(const ldx_conv3d_args* a, int64_t& row_vox, int64_t& o
   if ((a->ksize == 1 || a->upsample) && a->stride != 1) return fail("conv3d (fp32): stride 2 needs a 3x3x3 conv");
   if (a->ksize == 1 && a->upsample) return fail("conv3d (fp32): upsampling needs a 3x3x3 conv");
   const int f = a->upsample ? 2 : 1;
-  const int64_t rd = (int64_t)a->in_d * f, rh = (int64_t)a->in_h * f, rw = (int64_t)a->in_w * f;
-  row_vox = rd * rh * rw;
-  const int s = a->stride;
-  auto ext = [&](int64_t n) { return s == 1 ? n : (n - 1) / 2 + 1; };
-  out_vox = ext(rd) * ext(rh) * ext(rw);
+  rg[0] = (int64_t)a->in_d * f; rg[1] = (int64_t)a->in_h * f; rg[2] = (int64_t)a->in_w * f;
+  for (int i = 0; i < 3; i++) og[i] = a->stride == 1 ? rg[i] : (rg[i] - 1) / 2 + 1;
+  if (rg[0] * rg[1] * rg[2] * a->batch >= (1ll << 31) || (int64_t)a->c0 + a->c1 >= (1 << 24))
+    return fail("conv3d (fp32): tensor too large");
   return LDX_OK;
 }
 
-static size_t al256(size_t n) { return (n + 255) & ~(size_t)255; }
+size_t conv3d_exact_workspace_bytes(const ldx_conv3d_args*) { return 0; }
 
-size_t conv3d_exact_workspace_bytes(const ldx_conv3d_args* a) {
-  int64_t rv, ov;
-  if (exact_geometry(a, rv, ov) != LDX_OK) return 0;
-  const int C = a->c0 + a->c1;
-  return al256((size_t)a->batch * rv * 2 * C * sizeof(f16)) + (size_t)a->batch * ov * 2 * a->out_c * sizeof(float);
+template <int KS, int S, int BD, int BH, int BW, int KG, int NCW>
+static int launch_exact(ExactConvParams p, int64_t bricks, hipStream_t st) {
+  using SH = ExactConvShape<KS, S, BD, BH, BW, KG, NCW>;
+  auto kern = conv3d_exact_kernel<KS, S, BD, BH, BW, KG, NCW>;
+  const int lds = SH::LDS;
+  p.NCH = (p.C + 16 * KG - 1) / (16 * KG);
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+    return fail("conv3d (fp32): cannot reserve %d bytes of LDS", lds);
+  if (bricks >= (1ll << 31) || (p.O + 63) / 64 > 65535) return fail("conv3d (fp32): grid too large");
+  hipLaunchKernelGGL(kern, dim3((unsigned)bricks, (unsigned)((p.O + 63) / 64)), dim3(SH::NT), lds, st, p);
+  return check_launch("conv3d (fp32)");
 }
 
+static bool al16(const void* q) { return ((uintptr_t)q & 15) == 0; }
+
 int conv3d_exact(const ldx_conv3d_args* a, void* stream) {
-  int64_t rv, ov;
-  if (int rc = exact_geometry(a, rv, ov)) return rc;
+  int64_t rg[3], og[3];
+  if (int rc = exact_geometry(a, rg, og)) return rc;
   if (!a->x0 || !a->weight || !a->y) return fail("conv3d (fp32): null x0 / weight / y");
   if (a->c1 > 0 && !a->x1) return fail("conv3d (fp32): c1 > 0 but x1 is null");
   if (a->x0_pitch < a->c0 || (a->c1 > 0 && a->x1_pitch < a->c1) || a->y_pitch < a->out_c)
@@ -529,34 +870,50 @@ int conv3d_exact(const ldx_conv3d_args* a, void* stream) {
   if (a->residual && a->residual_pitch < a->out_c) return fail("conv3d (fp32): residual pitch < out_c");
   if (a->act != LDX_ACT_NONE && a->act != LDX_ACT_GELU && a->act != LDX_ACT_SILU)
     return fail("conv3d (fp32): unknown act %d", a->act);
-  const size_t need = conv3d_exact_workspace_bytes(a);
-  if (!a->workspace || a->workspace_bytes < need)
-    return fail("conv3d (fp32): needs %zu bytes of workspace (ldx_conv3d_workspace_bytes)", need);
-  const int C = a->c0 + a->c1, O = a->out_c, B = a->batch;
-  f16* xs = (f16*)a->workspace;
-  float* part = (float*)((char*)a->workspace + al256((size_t)B * rv * 2 * C * sizeof(f16)));
+  const int C = a->c0 + a->c1, O = a->out_c, K = a->ksize;
+  ExactConvParams p{};
+  p.x0 = (const float*)a->x0; p.p0 = a->x0_pitch; p.C0 = a->c0;
+  p.x1 = a->c1 > 0 ? (const float*)a->x1 : p.x0; p.p1 = a->c1 > 0 ? a->x1_pitch : a->x0_pitch;
+  p.C = C; p.O = O; p.NKC = (C + 63) / 64 * 4;
+  p.RD = (int)rg[0]; p.RH = (int)rg[1]; p.RW = (int)rg[2];
+  p.ID = a->in_d; p.IH = a->in_h; p.IW = a->in_w;
+  p.OD = (int)og[0]; p.OH = (int)og[1]; p.OW = (int)og[2];
+  p.up = a->upsample;
+  p.vec_in = C % 4 == 0 && a->c0 % 4 == 0 && a->x0_pitch % 4 == 0 && al16(p.x0) &&
+             (a->c1 == 0 || (a->x1_pitch % 4 == 0 && al16(p.x1)));
+  p.vec_out = a->y_pitch % 4 == 0 && al16(a->y);
+  p.w = (const f16*)a->weight; p.wplane = exact_plane_elems(O, C, K * K * K);
+  p.affine = a->affine; p.silu = a->silu;
+  p.bias = a->bias; p.bias_batched = a->bias_batched;
+  p.shift = (const float*)a->shift; p.shiftp = a->shift_pitch;
+  p.scale = a->output_scale;
+  p.res = (const float*)a->residual; p.resp = a->residual_pitch;
+  p.act = a->act;
+  p.y = (float*)a->y; p.yp = a->y_pitch;
   hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(split_exact_kernel, dim3(grid_for((int64_t)B * rv * C)), dim3(256), 0, st, (const float*)a->x0,
-                     a->x0_pitch, a->c0, a->c1 > 0 ? (const float*)a->x1 : (const float*)a->x0,
-                     a->c1 > 0 ? a->x1_pitch : a->x0_pitch, C, B, a->in_d, a->in_h, a->in_w, a->upsample, a->affine,
-                     a->silu, xs);
-  if (int rc = check_launch("conv3d (fp32): split")) return rc;
-  // The products: an fp16 conv of the 2C split channels with the 2O stacked weight rows.
-  ldx_conv3d_args ia{};
-  const int f = a->upsample ? 2 : 1;
-  ia.batch = B; ia.in_d = a->in_d * f; ia.in_h = a->in_h * f; ia.in_w = a->in_w * f;
-  ia.c0 = 2 * C; ia.c1 = 0; ia.out_c = 2 * O; ia.ksize = a->ksize; ia.stride = a->stride; ia.upsample = 0;
-  ia.x0 = xs; ia.x0_pitch = 2 * C;
-  ia.weight = a->weight;
-  ia.output_scale = 1.0f;
-  ia.act = LDX_ACT_NONE;
-  ia.y = part; ia.y_pitch = 2 * O;   // not written: the raw sums go to part
-  ia.dtype = LDX_DTYPE_F16;
-  if (int rc = f16_path::conv3d_raw(&ia, part, stream)) return rc;
-  hipLaunchKernelGGL(exact_combine_kernel, dim3(grid_for((int64_t)B * ov * O)), dim3(256), 0, st, part, ov, B, O,
-                     a->bias, a->bias_batched, (const float*)a->shift, a->shift_pitch, a->output_scale,
-                     (const float*)a->residual, a->residual_pitch, a->act, (float*)a->y, a->y_pitch);
-  return check_launch("conv3d (fp32): combine");
+  if (K == 1) {
+    p.nvox = (int64_t)a->batch * og[0] * og[1] * og[2];
+    return launch_exact<1, 1, 1, 1, 128, 1, 2>(p, ceil_div64(p.nvox, 128), st);
+  }
+  auto bricks = [&](int bd, int bh, int bw) {
+    p.nbd = (int)ceil_div64(og[0], bd); p.nbh = (int)ceil_div64(og[1], bh); p.nbw = (int)ceil_div64(og[2], bw);
+    return (int64_t)a->batch * p.nbd * p.nbh * p.nbw;
+  };
+  // Tile choice (measured on MI355X at LMNet's grids): the 128-voxel brick with two
+  // k-groups while it gives at least 128 workgroups (half
+  // the CUs); below that the 32-voxel brick with four k-groups (3,040 voxels x 128
+  // channels: 21.7 us against 50.5 us); stride 2 the 32-voxel brick with two k-groups
+  // (its 5x9x9 halo leaves no room for four).
+  const int64_t oblocks = (O + 63) / 64;
+  int64_t nb;   // (the brick counts go into p before p is passed on)
+  if (a->stride == 2) {
+    nb = bricks(2, 4, 4);
+    return launch_exact<3, 2, 2, 4, 4, 2, 1>(p, nb, st);
+  }
+  nb = bricks(4, 4, 8);
+  if (nb * oblocks >= 128) return launch_exact<3, 1, 4, 4, 8, 2, 2>(p, nb, st);
+  nb = bricks(2, 4, 4);
+  return launch_exact<3, 1, 2, 4, 4, 4, 1>(p, nb, st);
 }
 
 int attention_f32(const ldx_attention_args* a, void* stream) {

@@ -560,7 +560,7 @@ __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict_
 using namespace ldx;
 
 extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
-extern "C" int ldx_abi_version(void) { return 10; }
+extern "C" int ldx_abi_version(void) { return 11; }
 
 extern "C" size_t ldx_packed_weight_elems(int32_t O, int32_t C, int32_t k, int32_t upsample) {
   if (O < 1 || C < 1 || (k != 1 && k != 3) || (upsample && k != 3)) return 0;

@@ -127,8 +127,9 @@ class PackedWeight:
     in_channels: int
     ksize: int
     upsample: bool = False
-    # FP32 weight in the exact mode's stacked split (2 O x 2 C fp16 rows; an upsample conv
-    # keeps its unfolded 3x3x3 taps and runs on the upsampled grid).
+    # FP32 weight in the exact mode's split: hi and lo fp16 planes
+    # (``ldx_packed_weight_exact_elems`` values; an upsample conv keeps its unfolded 3x3x3
+    # taps and runs on the upsampled grid).
     exact: bool = False
 
 
@@ -153,7 +154,7 @@ def pack_weight(weight: torch.Tensor) -> PackedWeight:
 
 
 def _pack_exact(w: torch.Tensor, o: int, c: int, k: int, upsample: bool) -> PackedWeight:
-    out = torch.empty(lib.ldx_packed_weight_elems(2 * o, 2 * c, k, 0), dtype=torch.float16, device=w.device)
+    out = torch.empty(lib.ldx_packed_weight_exact_elems(o, c, k), dtype=torch.float16, device=w.device)
     check(lib.ldx_pack_weight_exact(_ptr(w), o, c, k, _ptr(out), _stream()), "pack_weight_exact")
     return PackedWeight(out, o, c, k, upsample, exact=True)
 

@@ -55,7 +55,8 @@ def group_norm(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, *, groups: in
 def silu(x: np.ndarray) -> np.ndarray:
     """``x / (1 + exp(-x))`` (_nax_conv.py:134)."""
     x = np.asarray(x, dtype=np.float64)
-    return x / (1.0 + np.exp(-x))
+    with np.errstate(over="ignore"):   # exp(-x) = inf for x < -709 gives the limit -0
+        return x / (1.0 + np.exp(-x))
 
 
 def layer_norm(x: np.ndarray, gamma: np.ndarray, beta: np.ndarray, eps: float = 1e-5) -> np.ndarray:

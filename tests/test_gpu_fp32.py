@@ -116,6 +116,51 @@ def test_fp32_fused_prologue_shift_scale_and_concat(pkg, dev) -> None:
     assert_near_fp32(host(y).transpose(0, 4, 1, 2, 3), expected, mag, extra=4 * 2.0 ** -23)
 
 
+@pytest.mark.parametrize(("shape", "out_c"), [
+    ((1, 64, 19, 32, 38), 64),    # LMNet's full-resolution grid: 128-voxel bricks, two k-groups
+    ((1, 40, 16, 24, 32), 72),    # the same tiling with a partial chunk and partial row block
+    ((2, 136, 3, 5, 6), 40),      # a small grid: 32-voxel bricks, four k-groups, 3 chunks
+])
+def test_fp32_exact_conv_tilings_with_group_norm_prologue(pkg, dev, shape, out_c) -> None:
+    """The one-pass exact conv's tilings (chosen by grid size) through the fp32 GroupNorm
+    affine + SiLU prologue and a residual, against float64 at the exact-mode bound."""
+    x, w, b = fp32_case(shape, out_c, sum(shape) + out_c)
+    rng = np.random.default_rng(out_c)
+    c = shape[1]
+    aff = np.stack([rng.normal(size=(shape[0], c)), rng.normal(size=(shape[0], c)) * 0.3], -1)
+    aff = aff.astype(np.float32).astype(np.float64)
+    res = rng.normal(size=(shape[0], out_c) + shape[2:]).astype(np.float32).astype(np.float64)
+    y = pkg.ops.nax_conv3d(dev32(ndhwc(x), dev), pkg.ops.pack_weight(dev32(w, dev)), dev32(b, dev),
+                           affine=dev32(aff, dev), silu=True, residual=dev32(ndhwc(res), dev))
+    torch.cuda.synchronize()
+    prep = onm.silu(onm.apply_affine(x, aff))
+    expected = ocv.conv3d(prep, w, b) + res
+    mag = ocv.conv3d_magnitude(prep, w, b) + np.abs(res)
+    assert_near_fp32(host(y).transpose(0, 4, 1, 2, 3), expected, mag, extra=4 * 2.0 ** -23)
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_fp32_unaligned_concat_with_batched_affine(pkg, dev, k) -> None:
+    """Channel counts that are not multiples of 4 (element-wise input reads), two batch items
+    with their own GroupNorm affine and bias through the pointwise (flattened) and 3x3x3
+    tilings, a y slice of a wider tensor."""
+    rng = np.random.default_rng(40 + k)
+    x, w, _ = fp32_case((2, 19, 3, 9, 11), 37, 40 + k, k=k)
+    aff = np.stack([rng.normal(size=(2, 19)), rng.normal(size=(2, 19)) * 0.3], -1).astype(np.float32)
+    bias = rng.normal(size=(2, 37)).astype(np.float32).astype(np.float64)
+    xd = ndhwc(x)
+    out = torch.zeros((2, 3, 9, 11, 40), dtype=torch.float32, device=dev)
+    pkg.ops.nax_conv3d(dev32(xd[..., :6], dev), pkg.ops.pack_weight(dev32(w, dev)), dev32(bias, dev),
+                       x1=dev32(xd[..., 6:], dev), affine=dev32(aff, dev), silu=True, out=out[..., 1:38])
+    torch.cuda.synchronize()
+    prep = onm.silu(onm.apply_affine(x, aff.astype(np.float64)))
+    expected = ocv.conv3d(prep, w, bias)
+    mag = ocv.conv3d_magnitude(prep, w, bias)
+    got = host(out)
+    assert np.all(got[..., 0] == 0) and np.all(got[..., 38:] == 0)
+    assert_near_fp32(got[..., 1:38].transpose(0, 4, 1, 2, 3), expected, mag, extra=4 * 2.0 ** -23)
+
+
 @pytest.mark.parametrize("act", [None, "gelu", "silu"])
 def test_fp32_dense(pkg, dev, act) -> None:
     """Dense layers in the exact mode, with the fp32 GELU / SiLU epilogue."""
