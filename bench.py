@@ -55,19 +55,91 @@ def profiled_traffic() -> tuple[float | None, str | None]:
     return float(m.group(1)), f"{CONV_PROFILE.relative_to(REPO)} @ {m.group(2)}"
 
 
+class SclkSampler:
+    """The GPU's shader clock while a figure is measured: a thread reads the device's
+    ``pp_dpm_sclk`` (sysfs; the level marked ``*`` is the current clock) every
+    ``interval_s`` between ``__enter__`` and ``__exit__``. Figures from different boxes differ with it
+    (the same kernel runs ~12 % slower at 1.95 GHz than at 2.2 GHz), so each figure carries
+    the median, min and max MHz it ran at (``None`` where sysfs is not readable)."""
+
+    def __init__(self, interval_s: float = 0.002):
+        self.interval = interval_s
+        self.path = self._find()
+        self.samples: list[int] = []
+        self._stop = None
+        self._thread = None
+
+    @staticmethod
+    def _find():
+        import glob
+
+        import torch
+
+        p = torch.cuda.get_device_properties(0)
+        cand = Path(f"/sys/bus/pci/devices/{p.pci_domain_id:04x}:{p.pci_bus_id:02x}:{p.pci_device_id:02x}.0"
+                    "/pp_dpm_sclk")
+        if cand.exists():
+            return cand
+        found = glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")
+        return Path(found[0]) if len(found) == 1 else None
+
+    def _read(self):
+        import re
+
+        try:
+            for line in self.path.read_text().splitlines():
+                if line.rstrip().endswith("*"):
+                    m = re.search(r"(\d+)\s*[Mm]hz", line)
+                    return int(m.group(1)) if m else None
+        except OSError:
+            return None
+        return None
+
+    def __enter__(self):
+        import threading
+
+        if self.path is None:
+            return self
+        self._stop = threading.Event()
+
+        def run():
+            while not self._stop.is_set():
+                v = self._read()
+                if v is not None:
+                    self.samples.append(v)
+                self._stop.wait(self.interval)
+
+        self._thread = threading.Thread(target=run, daemon=True)
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        if self._thread is not None:
+            self._stop.set()
+            self._thread.join()
+        return False
+
+    def summary(self):
+        if not self.samples:
+            return None
+        return {"median": int(np.median(self.samples)), "min": min(self.samples), "max": max(self.samples),
+                "samples": len(self.samples)}
+
+
 # Each timed region is one replay of the K captured launches; the reported figure is the
 # median over this many such regions. A replay occasionally stalls for a few hundred
 # microseconds while the host is still submitting its packets (seen in kernel traces as a
 # run of idle gaps inside one replay), and the median keeps that out of the per-launch time.
-TIMED_REPLAYS = 3
+TIMED_REPLAYS = 5
 # The 200-step config-5 loop is timed this many times; the median is reported.
 CONFIG5_RUNS = 5
 
 
-def _graph_time(launch, steps: int, warmup: int) -> float:
+def _graph_time(launch, steps: int, warmup: int, clock: "SclkSampler | None" = None, settle_s: float = 0.5) -> float:
     """Per-launch ms: ``warmup`` eager launches, then ``steps`` launches captured in one
-    graph, replayed untimed for about 0.2 s, then TIMED_REPLAYS times between HIP events;
-    the median replay time divided by ``steps``."""
+    graph, replayed untimed for ``settle_s`` seconds, then TIMED_REPLAYS times between HIP
+    events (``clock`` samples the shader clock over those); the median replay time divided
+    by ``steps``."""
     import torch
 
     for _ in range(max(warmup, 1)):
@@ -83,15 +155,18 @@ def _graph_time(launch, steps: int, warmup: int) -> float:
     with torch.cuda.graph(g):
         for _ in range(steps):
             launch()
-    # Untimed replays for about 0.2 s first: the clocks settle to their loaded steady state
-    # (a cold start measured ~10 % slower per launch on the short workloads).
+    # Untimed replays first: the clocks climb to their loaded steady state. From idle that
+    # takes several hundred ms (the first figure of a process, sampled over 0.2 s of
+    # replays, ran at a median 1,370 MHz and 30 % slower).
     t0 = time.perf_counter()
     while True:
         g.replay()
         torch.cuda.synchronize()
-        if time.perf_counter() - t0 > 0.2:
+        if time.perf_counter() - t0 > settle_s:
             break
     times = []
+    if clock is not None:
+        clock.__enter__()
     for _ in range(TIMED_REPLAYS):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -101,6 +176,8 @@ def _graph_time(launch, steps: int, warmup: int) -> float:
         end.record()
         torch.cuda.synchronize()
         times.append(start.elapsed_time(end) / steps)
+    if clock is not None:
+        clock.__exit__(None, None, None)
     return float(np.median(times))
 
 
@@ -126,10 +203,11 @@ def bench_conv(pkg, steps: int, warmup: int) -> dict:
     def launch():
         lib.check(lib.lib.ldx_conv3d(ref, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "conv3d")
 
-    ms = _graph_time(launch, steps, warmup)
+    clk = SclkSampler(0.0005)
+    ms = _graph_time(launch, steps, warmup, clk, settle_s=1.5)   # the first figure: the GPU starts idle
     flop = 2.0 * 51200 * 64 * 64 * 27
     tflops = flop / (ms * 1e-3) / 1e12
-    return {"ms": ms, "tflops": tflops, "flop": flop,
+    return {"ms": ms, "tflops": tflops, "flop": flop, "sclk_mhz": clk.summary(),
             "bytes": (51200 * 64 * 2) * 2 + 64 * 64 * 27 * 2, "x": x, "w": w, "b": b}
 
 
@@ -158,10 +236,11 @@ def bench_attention(pkg, steps: int, warmup: int) -> dict:
             lib.check(lib.lib.ldx_attention(ref, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
                       "attention")
 
-        ms = _graph_time(launch, steps, warmup)
+        clk = SclkSampler(0.0005)
+        ms = _graph_time(launch, steps, warmup, clk)
         flop = 4.0 * 8 * 1600 * lk * 64
         byts = 2.0 * (2 * 8 * 1600 * 64 + 2 * 8 * lk * 64)
-        out[name] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop,
+        out[name] = {"ms": ms, "tflops": flop / (ms * 1e-3) / 1e12, "flop": flop, "sclk_mhz": clk.summary(),
                      "frac_peak": flop / (ms * 1e-3) / 1e12 / PEAK_FP16_TFLOPS,
                      "gbs": byts / (ms * 1e-3) / 1e9}
     out["_tensors"] = (q, k, v)
@@ -252,8 +331,10 @@ def bench_config3(pkg, reps: int) -> dict:
     t = torch.tensor([500], dtype=torch.int32, device="cuda")
     with pkg.ops.count_flops() as fc:
         net.encoder_stack(x, t)
-    ms = _graph_replay_ms(lambda: net.encoder_stack(x, t), reps)
-    return {"ms": round(ms, 4), "conv_gflop": round(fc.conv / 1e9, 2), "tflops": round(fc.total / ms / 1e9, 1),
+    with SclkSampler() as clk:
+        ms = _graph_replay_ms(lambda: net.encoder_stack(x, t), reps)
+    return {"ms": round(ms, 4), "sclk_mhz": clk.summary(), "conv_gflop": round(fc.conv / 1e9, 2),
+            "tflops": round(fc.total / ms / 1e9, 1),
             "frac_peak": round(fc.total / ms / 1e9 / PEAK_FP16_TFLOPS, 4),
             "config": "config 3: encoder stack 4->64/128/256/256 at 32x40x40 .. 4x5x5, 2 ResBlocks per level, "
                       "fp16, random init"}
@@ -280,13 +361,15 @@ def bench_config4(pkg, reps: int) -> dict:
     end = torch.cuda.Event(enable_timing=True)
     dec.decode(z, quantize=False)
     torch.cuda.synchronize()
-    start.record()
-    for _ in range(reps):
-        dec.decode(z, quantize=False)
-    end.record()
-    torch.cuda.synchronize()
+    with SclkSampler() as clk:
+        start.record()
+        for _ in range(reps):
+            dec.decode(z, quantize=False)
+        end.record()
+        torch.cuda.synchronize()
     ms = start.elapsed_time(end) / reps
-    return {"ms": round(ms, 3), "conv_gflop": round(fc.conv / 1e9, 1), "attention_gflop": round(fc.attention / 1e9, 1),
+    return {"ms": round(ms, 3), "sclk_mhz": clk.summary(), "conv_gflop": round(fc.conv / 1e9, 1),
+            "attention_gflop": round(fc.attention / 1e9, 1),
             "tflops": round(fc.total / ms / 1e9, 1), "frac_peak": round(fc.total / ms / 1e9 / PEAK_FP16_TFLOPS, 4),
             "config": "config 4: VQ decoder 8x32x40x40 -> 1x128x160x160, channels 256/128/64/32, mid attention "
                       "51,200 tokens x 256, fp16, random init, eager launches"}
@@ -330,6 +413,7 @@ def bench_config5(pkg, steps: int = 200) -> dict:
     prep.run()  # warm replay
     torch.cuda.synchronize()
     totals = []
+    clk = SclkSampler().__enter__()
     for _ in range(CONFIG5_RUNS):
         prep.set_noise(init, noise)
         start = torch.cuda.Event(enable_timing=True)
@@ -341,9 +425,11 @@ def bench_config5(pkg, steps: int = 200) -> dict:
         torch.cuda.synchronize()
         totals.append(start.elapsed_time(end))
         assert bool(torch.isfinite(out).all())
+    clk.__exit__(None, None, None)
     total = float(np.median(totals))
     per = total / prep.num_steps
     return {"ms_per_step": round(per, 4), "total_ms": round(total, 2), "steps": prep.num_steps,
+            "sclk_mhz": clk.summary(),
             "total_ms_runs": [round(t, 2) for t in totals],
             "step_gflop": round(fc.total / 1e9, 1), "step_conv_gflop": round(fc.conv / 1e9, 1),
             "step_attention_gflop": round(fc.attention / 1e9, 2),
@@ -539,6 +625,8 @@ def main() -> int:
         run = {3: lambda: bench_config3(pkg, max(args.steps // 5, 5)), 4: lambda: bench_config4(pkg, 3),
                5: lambda: bench_config5(pkg, args.steps)}[args.only]
         print(json.dumps(run()))
+        if args.copy_calibration:
+            copy_calibration()
         return 0
     conv = bench_conv(pkg, args.steps, args.warmup)
     traffic, traffic_src = profiled_traffic()
@@ -560,6 +648,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": "config 1: conv3d 3x3x3 stride 1 pad 1, NDHWC fp16, N=1, C_in=C_out=64, "
                                "D x H x W = 32 x 40 x 40, seed 0", "global_batch": 1},
+        "sclk_mhz": conv["sclk_mhz"],
         "roofline": {"bound": "mfma", "achieved": round(conv["tflops"], 2), "peak": PEAK_FP16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(conv["tflops"] / PEAK_FP16_TFLOPS, 4),
                      "traffic": traffic, "traffic_source": traffic_src},
@@ -568,8 +657,9 @@ def main() -> int:
             "self_frac_peak": round(att["self"]["frac_peak"], 4),
             "cross_tflops": round(att["cross"]["tflops"], 2), "cross_ms": round(att["cross"]["ms"], 5),
             "cross_gbs": round(att["cross"]["gbs"], 1),
+            "self_sclk_mhz": att["self"]["sclk_mhz"], "cross_sclk_mhz": att["cross"]["sclk_mhz"],
             "config": "config 2: fp16, B=1, 8 heads x 64, 1600 queries; self 1600 keys, cross 77 keys "
-                      "(context 77x768 projected by to_k/to_v)"},
+                      "(context 77x768 projected by to_k/to_v once, outside the timed launches)"},
     }
     line["source_order"] = bench_source(pkg, args.steps, args.warmup, not args.skip_cpu)
     if not args.skip_model:
