@@ -131,13 +131,16 @@ class SclkSampler:
 # microseconds while the host is still submitting its packets (seen in kernel traces as a
 # run of idle gaps inside one replay), and the median keeps that out of the per-launch time.
 TIMED_REPLAYS = 5
+# Seconds of untimed replays before each figure (the first figure of a process takes 3x);
+# --settle sets it (short for profiling runs, whose every replay is traced).
+SETTLE_S = [0.5]
 # The 200-step config-5 loop is timed this many times; the median is reported.
 CONFIG5_RUNS = 5
 
 
-def _graph_time(launch, steps: int, warmup: int, clock: "SclkSampler | None" = None, settle_s: float = 0.5) -> float:
+def _graph_time(launch, steps: int, warmup: int, clock: "SclkSampler | None" = None, settle: float = 1.0) -> float:
     """Per-launch ms: ``warmup`` eager launches, then ``steps`` launches captured in one
-    graph, replayed untimed for ``settle_s`` seconds, then TIMED_REPLAYS times between HIP
+    graph, replayed untimed for ``settle`` x SETTLE_S seconds, then TIMED_REPLAYS times between HIP
     events (``clock`` samples the shader clock over those); the median replay time divided
     by ``steps``."""
     import torch
@@ -162,7 +165,7 @@ def _graph_time(launch, steps: int, warmup: int, clock: "SclkSampler | None" = N
     while True:
         g.replay()
         torch.cuda.synchronize()
-        if time.perf_counter() - t0 > settle_s:
+        if time.perf_counter() - t0 > settle * SETTLE_S[0]:
             break
     times = []
     if clock is not None:
@@ -204,7 +207,7 @@ def bench_conv(pkg, steps: int, warmup: int) -> dict:
         lib.check(lib.lib.ldx_conv3d(ref, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "conv3d")
 
     clk = SclkSampler(0.0005)
-    ms = _graph_time(launch, steps, warmup, clk, settle_s=1.5)   # the first figure: the GPU starts idle
+    ms = _graph_time(launch, steps, warmup, clk, settle=3.0)   # the first figure: the GPU starts idle
     flop = 2.0 * 51200 * 64 * 64 * 27
     tflops = flop / (ms * 1e-3) / 1e12
     return {"ms": ms, "tflops": tflops, "flop": flop, "sclk_mhz": clk.summary(),
@@ -608,9 +611,12 @@ def main() -> int:
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 512 MiB device copy (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE counters to bytes)")
+    ap.add_argument("--settle", type=float, default=SETTLE_S[0],
+                    help="seconds of untimed replays before each figure (0.05 for profiling runs)")
     ap.add_argument("--only", type=int, choices=(3, 4, 5),
                     help="run just model config 3, 4 or 5 and print its figures (profiling runs)")
     args = ap.parse_args()
+    SETTLE_S[0] = args.settle
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(collectives and sharding are out of scope); run with --gpus 1.", file=sys.stderr)
