@@ -40,7 +40,7 @@ extern "C" {
 
 /* Message of the calling thread's most recent failure ("" if none). */
 const char* ldx_last_error(void);
-/* ABI version (11); bumped on any change to the structs below or the entry points. */
+/* ABI version (12); bumped on any change to the structs below or the entry points. */
 int ldx_abi_version(void);
 
 /* ---------------------------------------------------------------- conv3d -------
@@ -284,21 +284,6 @@ int ldx_timestep_embedding_f32(const int32_t* timesteps, int32_t batch, int32_t 
 /* y = half(silu(float(x))) elementwise over n fp16 values (LdmUnet.silu,
  * mlx_model.py:409-413). */
 int ldx_silu(const void* x, int64_t n, void* y, void* stream);
-
-/* y = half(silu(x * scale + offset)) per channel (silu = 0: the affine alone), for
- * `batch` items of `voxels` NDHWC voxels of `channels` channels (a multiple of 8; x, y
- * and the pitches 16-byte aligned): the GroupNorm-normalised conv input stored once.
- * `affine` holds (scale, offset) fp32 pairs per channel, `affine_batch_stride` floats
- * apart per batch item -- the ldx_group_norm_affine* output, or a channel slice of it for
- * the second input of a concat. dtype: LDX_DTYPE_F16 or LDX_DTYPE_BF16. The arithmetic is
- * the fused conv prologue's (ldx_conv3d with affine/silu), so a conv of y equals the fused
- * conv of x on the same kernel path; callers of large tensors use it to move the
- * normalisation out of every conv workgroup's halo staging. Replaces the reference's
- * pack kernel `_PACK` (src/lesiondiffusion_mlx/_nax_conv.py:109-155), which stores the
- * same normalised input (padded) before its conv. */
-int ldx_group_norm_apply(const void* x, int64_t x_pitch, void* y, int64_t y_pitch, int32_t batch,
-                         int64_t voxels, int32_t channels, const float* affine,
-                         int64_t affine_batch_stride, int32_t silu, int32_t dtype, void* stream);
 
 /* Copy a channel slice: dst[v, dst_off + c] = src[v, src_off + c], c < channels,
  * for `voxels` voxels of fp16 NDHWC tensors (concat / split without torch). */

@@ -110,8 +110,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ldx_timestep_embedding": (c_i32, [c_vp, c_i32, c_i32, c_vp, c_vp]),
     "ldx_silu": (c_i32, [c_vp, c_i64, c_vp, c_vp]),
     "ldx_copy_channels": (c_i32, [c_vp, c_i64, c_i32, c_vp, c_i64, c_i32, c_i64, c_i32, c_vp]),
-    "ldx_group_norm_apply": (c_i32, [c_vp, c_i64, c_vp, c_i64, c_i32, c_i64, c_i32, c_vp, c_i64, c_i32, c_i32,
-                                     c_vp]),
     "ldx_upsample_nearest2": (c_i32, [c_vp, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "ldx_ddim_prepare": (c_i32, [c_vp, c_vp, c_vp, c_i64, c_i32, c_i32, c_vp, c_i64, c_vp]),
     "ldx_ddim_update": (c_i32, [c_vp, c_vp, c_i64, c_vp, c_vp, c_vp, c_i64, c_i32, c_vp]),
@@ -132,7 +130,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            c_vp]),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 
 def _load() -> ctypes.CDLL:

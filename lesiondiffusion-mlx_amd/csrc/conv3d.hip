@@ -379,10 +379,6 @@ __device__ __forceinline__ void conv_epilogue(const ConvParams& p, const EpiCons
   else finish(std::integral_constant<int, LDX_ACT_NONE>());
 }
 
-// KSPL K-groups of 4 waves each: group g takes k-steps [g * KS / KSPL, (g + 1) * KS /
-// KSPL) of every tap (its own weight ring, the shared halo), so KSPL = 2 puts two waves
-// on every SIMD for the same output tile; the groups' partial sums meet in LDS at the
-// end (fixed order: group 0 + group 1).
 // Scheduling hint: spread NR LDS reads between NM MFMAs (one MFMA, then its share of
 // the reads) so the next tap's operands stream in while the current tap's MFMAs run.
 template <int NR, int NM, int I = 0>
@@ -409,8 +405,12 @@ constexpr int NHL = NHMAX + 4;   // loads per thread of one planned halo request
 // TPS = KSZ (a whole kw row per stage) takes two thirds of the barriers out of the tap loop
 // for a ring three times the size, which pays where one workgroup per CU is all the grid
 // has (the coarse UNet levels).
-template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, bool PLAN, int KSPL, int TPS>
-__global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
+template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, bool PLAN, int TPS>
+__global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
+  // One K-group of four waves takes every k-step of a tap (the indexing below keeps the
+  // group variables: a two-group variant, two waves per SIMD on one output tile, measured
+  // no faster and was taken out).
+  constexpr int KSPL = 1;
   static_assert(!PLAN || VEC, "the planned halo needs 16-byte channel groups");
   constexpr int NT = 256 * KSPL;
   constexpr int BO = WO * FO * 32;
@@ -694,45 +694,13 @@ __global__ __launch_bounds__(256 * KSPL) void conv3d_kernel(ConvParams p) {
   vmcnt_wait<0>();
 
   constexpr int EPW = FO * 32 + 4;   // epilogue staging pitch (floats)
-  constexpr int RED = 4 * FO * FV * 1024;  // floats of the K-group reduction buffer
   float* stg;
-  if constexpr (KSPL == 2) {
-    __syncthreads();  // every wave is done with the halo and the weight rings
-    // Group 1 hands its partial sums to group 0 (same wave slot, lane-major layout).
-    float* red = reinterpret_cast<float*>(smem) + w4 * (FO * FV * 1024);
-    if (kg == 1) {
-#pragma unroll
-      for (int fo = 0; fo < FO; fo++)
-#pragma unroll
-        for (int fv = 0; fv < FV; fv++)
-#pragma unroll
-          for (int e4 = 0; e4 < 4; e4++) {
-            const f32x4 q = {acc[fo][fv][e4 * 4], acc[fo][fv][e4 * 4 + 1], acc[fo][fv][e4 * 4 + 2],
-                             acc[fo][fv][e4 * 4 + 3]};
-            *reinterpret_cast<f32x4*>(red + ((fo * FV + fv) * 4 + e4) * 256 + lane * 4) = q;
-          }
-    }
-    __syncthreads();
-    if (kg == 1) return;
-#pragma unroll
-    for (int fo = 0; fo < FO; fo++)
-#pragma unroll
-      for (int fv = 0; fv < FV; fv++)
-#pragma unroll
-        for (int e4 = 0; e4 < 4; e4++) {
-          const f32x4 q = *reinterpret_cast<const f32x4*>(red + ((fo * FV + fv) * 4 + e4) * 256 + lane * 4);
-#pragma unroll
-          for (int r = 0; r < 4; r++) acc[fo][fv][e4 * 4 + r] += q[r];
-        }
-    stg = reinterpret_cast<float*>(smem) + RED + w4 * 32 * EPW;
+  if (p.stg_off > 0) {
+    // A staging area of its own past the halo: no wait for the other waves.
+    stg = reinterpret_cast<float*>(smem) + p.stg_off + w4 * 32 * EPW;
   } else {
-    if (p.stg_off > 0) {
-      // A staging area of its own past the halo: no wait for the other waves.
-      stg = reinterpret_cast<float*>(smem) + p.stg_off + w4 * 32 * EPW;
-    } else {
-      __syncthreads();  // every wave is done with the halo and the weight rings
-      stg = reinterpret_cast<float*>(smem) + w4 * 32 * EPW;
-    }
+    __syncthreads();  // every wave is done with the halo and the weight rings
+    stg = reinterpret_cast<float*>(smem) + w4 * 32 * EPW;
   }
   conv_epilogue<FO, FV>(p, ec, acc, stg, lane, wv, b, sidx, pd, ph, pw, d0, h0, w0,
                         (parity * p.nbr + brick) * (WV * FV) + wv * FV);
@@ -1227,13 +1195,9 @@ __global__ __launch_bounds__(RS_THREADS) void conv_reduce_stats_kernel(ConvParam
 
 struct Tile {
   int WO, WV, FO, FV, CC;
-  int KSPL = 1;  // K-groups of 4 waves
   int BO() const { return WO * FO * 32; }
   int BV() const { return WV * FV * 32; }
 };
-
-// Tiles instantiated with two K-groups (the dispatch list in ldx_conv3d).
-static bool kspl2_tile(const Tile& t) { return t.WO == 1 && t.WV == 4 && t.FO == 2 && t.FV == 2; }
 
 static void pick_brick(const ConvParams& p, int BV, int s, int ks, int& TD, int& TH, int& TW) {
   // Minimise launched voxel slots (partial-brick waste), then the halo volume.
@@ -1254,26 +1218,23 @@ static void pick_brick(const ConvParams& p, int BV, int s, int ks, int& TD, int&
     }
 }
 
-template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, int KSPL>
+template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC>
 static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t halo_bytes) {
   constexpr int BO = WO * FO * 32;
-  constexpr int NT = 256 * KSPL, VPI = NT / (CC / 8);
+  constexpr int NT = 256, VPI = NT / (CC / 8);
   auto al16 = [](size_t n) { return (n + 15) & ~(size_t)15; };
   const int hvox = p.HD * p.HH * p.HW;
   p.nh = VEC ? (hvox + VPI - 1) / VPI : 0;
   if (p.nh > NHMAX) p.nh = 0;
   // Whole kw rows per weight stage on the planned halo path when the planner asks.
   const int tps = VEC && p.nh > 0 && p.tps > 1 ? KSZ : 1;
-  // LDS: weight rings (all K-groups) and the halo; then the epilogue (K-group partial
-  // sums and the staging).
+  // LDS: the weight ring and the halo; then the epilogue staging.
   const size_t ring = (size_t)WRING * tps * (BO / 32) * (CC / 16) * 1024;
   const size_t main_bytes = ring + al16(halo_bytes);
   const size_t stg = (size_t)4 * 32 * (FO * 32 + 4) * sizeof(float);
   size_t lds;
   p.stg_off = 0;
-  if constexpr (KSPL == 2) {
-    lds = std::max(main_bytes, (size_t)4 * FO * FV * 1024 * sizeof(float) + stg);
-  } else {
+  {
     // The staging gets an area of its own (no barrier before the epilogue) unless that
     // costs a workgroup per CU.
     const size_t overlap = std::max(main_bytes, stg), sep = main_bytes + stg;
@@ -1298,42 +1259,38 @@ static int launch(ConvParams& p, int grid_z, hipStream_t stream, size_t halo_byt
   dim3 grid((unsigned)nwg);
   void (*kern)(ConvParams);
   if constexpr (VEC) {
-    kern = p.nh == 0   ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, false, KSPL, 1>
-           : tps > 1 ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, KSPL, KSZ>
-                     : conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, KSPL, 1>;
+    kern = p.nh == 0   ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, false, 1>
+           : tps > 1 ? conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, KSZ>
+                     : conv3d_kernel<WO, WV, FO, FV, CC, KSZ, true, true, 1>;
   } else {
-    kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, false, false, KSPL, 1>;
+    kern = conv3d_kernel<WO, WV, FO, FV, CC, KSZ, false, false, 1>;
   }
   if (lds > 65536) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)lds) != hipSuccess)
       return check_launch("conv3d: set LDS size");
   }
-  hipLaunchKernelGGL(kern, grid, dim3(256 * KSPL), lds, stream, p);
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds, stream, p);
   return check_launch("conv3d");
 }
 
-template <int WO, int WV, int FO, int FV, int KSZ, int KSPL>
+template <int WO, int WV, int FO, int FV, int KSZ>
 static int dispatch_cc(ConvParams& p, int cc, bool vec, int grid_z, hipStream_t stream, size_t lds) {
-  if (!vec) {
-    if constexpr (KSPL == 1) return launch<WO, WV, FO, FV, 32, KSZ, false, 1>(p, grid_z, stream, lds);
-    return fail("conv3d: K-groups need 16-byte channel groups");
-  }
+  if (!vec) return launch<WO, WV, FO, FV, 32, KSZ, false>(p, grid_z, stream, lds);
   if constexpr (KSZ == 1) {
     // Pointwise convs with 16-byte channel groups run as dense_kernel; this path only
     // serves the remaining ones, through the scalar staging loop.
     return fail("conv3d: vectorised pointwise conv belongs to the dense path");
   } else {
-    if (cc == 64) return launch<WO, WV, FO, FV, 64, KSZ, true, KSPL>(p, grid_z, stream, lds);
-    return launch<WO, WV, FO, FV, 32, KSZ, true, KSPL>(p, grid_z, stream, lds);
+    if (cc == 64) return launch<WO, WV, FO, FV, 64, KSZ, true>(p, grid_z, stream, lds);
+    return launch<WO, WV, FO, FV, 32, KSZ, true>(p, grid_z, stream, lds);
   }
 }
-
-template <int WO, int WV, int FO, int FV, int KSPL>
+template <int WO, int WV, int FO, int FV>
 static int dispatch_k(ConvParams& p, int cc, bool vec, int grid_z, hipStream_t stream, size_t lds) {
-  if (p.taps == 27) return dispatch_cc<WO, WV, FO, FV, 3, KSPL>(p, cc, vec, grid_z, stream, lds);
-  if (p.taps == 8) return dispatch_cc<WO, WV, FO, FV, 2, KSPL>(p, cc, vec, grid_z, stream, lds);
-  return dispatch_cc<WO, WV, FO, FV, 1, KSPL>(p, cc, false, grid_z, stream, lds);
+  if (p.taps == 27) return dispatch_cc<WO, WV, FO, FV, 3>(p, cc, vec, grid_z, stream, lds);
+  if (p.taps == 8) return dispatch_cc<WO, WV, FO, FV, 2>(p, cc, vec, grid_z, stream, lds);
+  return dispatch_cc<WO, WV, FO, FV, 1>(p, cc, false, grid_z, stream, lds);
 }
 
 
@@ -1420,10 +1377,8 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   bool forced = false;
   if (const char* env = getenv("LDX_CONV_TILE")) {
     Tile o{};
-    const int got = sscanf(env, "%d,%d,%d,%d,%d,%d", &o.WO, &o.WV, &o.FO, &o.FV, &o.CC, &o.KSPL);
-    if (got == 5) o.KSPL = 1;
-    if (got >= 5 && o.WO * o.WV == 4 && (o.CC == 32 || (o.CC == 64 && p.C % 64 == 0 && vec)) &&
-        (o.KSPL == 1 || (o.KSPL == 2 && vec && kspl2_tile(o)))) {
+    const int got = sscanf(env, "%d,%d,%d,%d,%d", &o.WO, &o.WV, &o.FO, &o.FV, &o.CC);
+    if (got == 5 && o.WO * o.WV == 4 && (o.CC == 32 || (o.CC == 64 && p.C % 64 == 0 && vec))) {
       t = o;
       forced = true;
     }
@@ -1434,7 +1389,6 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
     if (p.C0 % 32 == 0) t.CC = 32;
     else vec = false;
   }
-  if (!vec) t.KSPL = 1;
   const int ks = a->ksize;
   const int s = p.stride;
   int TD = 1, TH = 1, TW = 1;
@@ -1460,7 +1414,6 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
     if (lds + wbytes <= (forced ? 160u * 1024 : 80u * 1024) || (t.CC == 32 && t.FV == 1)) break;
     if (t.CC == 64) t.CC = 32;
     else t.FV = 1;
-    if (!kspl2_tile(t)) t.KSPL = 1;
   }
   if (lds + (size_t)WRING * (t.BO() / 32) * (t.CC / 16) * 1024 > 160 * 1024)
     return fail("conv3d: halo of %zu bytes exceeds LDS", lds);
@@ -1689,17 +1642,16 @@ static int conv3d_run(const ldx_conv3d_args* a, float* stats, bool dry, int64_t*
   }
   const int grid_z = p.B * (p.upsample ? 8 : 1) * p.split;
 
-#define LDX_TILE(WO_, WV_, FO_, FV_, KSPL_)                                             \
-  if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_ && t.KSPL == KSPL_) \
-    rc = dispatch_k<WO_, WV_, FO_, FV_, KSPL_>(p, t.CC, vec, grid_z, st, lds);     \
+#define LDX_TILE(WO_, WV_, FO_, FV_)                                      \
+  if (t.WO == WO_ && t.WV == WV_ && t.FO == FO_ && t.FV == FV_)           \
+    rc = dispatch_k<WO_, WV_, FO_, FV_>(p, t.CC, vec, grid_z, st, lds);   \
   else
-  LDX_TILE(1, 4, 1, 2, 1)
-  LDX_TILE(1, 4, 1, 1, 1)
-  LDX_TILE(1, 4, 2, 2, 1)
-  LDX_TILE(1, 4, 2, 1, 1)
-  LDX_TILE(2, 2, 2, 2, 1)
-  LDX_TILE(2, 2, 1, 1, 1)
-  LDX_TILE(1, 4, 2, 2, 2)
+  LDX_TILE(1, 4, 1, 2)
+  LDX_TILE(1, 4, 1, 1)
+  LDX_TILE(1, 4, 2, 2)
+  LDX_TILE(1, 4, 2, 1)
+  LDX_TILE(2, 2, 2, 2)
+  LDX_TILE(2, 2, 1, 1)
   return fail("conv3d: no kernel for tile");
 #undef LDX_TILE
   if (rc != LDX_OK || p.split == 1) return rc;

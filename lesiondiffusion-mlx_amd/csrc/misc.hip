@@ -455,32 +455,6 @@ __global__ void silu_kernel(const f16* __restrict__ x, int64_t n, f16* __restric
   }
 }
 
-// y = E(silu(x * scale + offset)) per channel, 8 channels (one 16-byte vector) per unit:
-// the normalised conv input that the fused conv prologue forms on the fly, stored once.
-// The arithmetic is the prologue's (fp32 multiply-add, silu_f, one rounding), so a conv of
-// y equals the fused conv of x bit for bit on the same kernel path. affine: (scale, offset)
-// pairs, ab floats from one batch item to the next.
-template <typename EE, typename EE8>
-__global__ void gn_apply_kernel(const EE* __restrict__ x, int64_t xp, EE* __restrict__ y, int64_t yp,
-                                const float* __restrict__ affine, int64_t ab, int silu, int units, UDiv dg,
-                                int g8, UDiv dvol) {
-  for (int u = blockIdx.x * blockDim.x + threadIdx.x; u < units; u += gridDim.x * blockDim.x) {
-    const int v = udiv(u, dg), g = u - v * g8, bi = udiv(v, dvol);
-    const f32x4* a = reinterpret_cast<const f32x4*>(affine + bi * ab + g * 16);
-    EE8 xv = *reinterpret_cast<const EE8*>(x + (int64_t)v * xp + g * 8);
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const f32x4 aq = a[q];
-#pragma unroll
-      for (int e = 0; e < 2; e++) {
-        float yv = (float)xv[2 * q + e] * aq[2 * e] + aq[2 * e + 1];
-        if (silu) yv = silu_f(yv);
-        xv[2 * q + e] = (EE)yv;
-      }
-    }
-    *reinterpret_cast<EE8*>(y + (int64_t)v * yp + g * 8) = xv;
-  }
-}
 
 __global__ void copy_channels_kernel(const f16* __restrict__ src, int64_t sp, int so,
                                      f16* __restrict__ dst, int64_t dp, int dof, int64_t V, int C) {
@@ -560,7 +534,7 @@ __global__ void ddim_update_kernel(float* __restrict__ x, const f16* __restrict_
 using namespace ldx;
 
 extern "C" const char* ldx_last_error(void) { return g_error.c_str(); }
-extern "C" int ldx_abi_version(void) { return 11; }
+extern "C" int ldx_abi_version(void) { return 12; }
 
 extern "C" size_t ldx_packed_weight_elems(int32_t O, int32_t C, int32_t k, int32_t upsample) {
   if (O < 1 || C < 1 || (k != 1 && k != 3) || (upsample && k != 3)) return 0;
@@ -803,34 +777,6 @@ extern "C" int ldx_silu(const void* x, int64_t n, void* y, void* stream) {
   hipLaunchKernelGGL(silu_kernel, dim3(grid_cap(n, 256, 4096)), dim3(256), 0,
                      as_stream(stream), (const f16*)x, n, (f16*)y);
   return check_launch("silu");
-}
-
-extern "C" int ldx_group_norm_apply(const void* x, int64_t x_pitch, void* y, int64_t y_pitch, int32_t batch,
-                                    int64_t voxels, int32_t channels, const float* affine,
-                                    int64_t affine_batch_stride, int32_t silu, int32_t dtype, void* stream) {
-  if (!x || !y || !affine) return fail("group_norm_apply: null pointer");
-  if (dtype != LDX_DTYPE_F16 && dtype != LDX_DTYPE_BF16) return fail("group_norm_apply: fp16 or bf16 only");
-  if (batch < 1 || voxels < 1 || channels < 8 || channels % 8 || x_pitch < channels || y_pitch < channels)
-    return fail("group_norm_apply: bad shape");
-  if (x_pitch % 8 || y_pitch % 8 || (uintptr_t)x % 16 || (uintptr_t)y % 16 || (uintptr_t)affine % 16 ||
-      affine_batch_stride % 4)
-    return fail("group_norm_apply: rows, pitches and the affine must be 16-byte aligned");
-  if (affine_batch_stride < 2 * (int64_t)channels && batch > 1) return fail("group_norm_apply: bad affine stride");
-  const int64_t units = (int64_t)batch * voxels * (channels / 8);
-  const int g8 = channels / 8;
-  const unsigned grid = grid_cap(units, 256, 16384);
-  // The kernel's grid-stride index is 32-bit: it must not pass 2^31 - 1 on its last step.
-  if (units + (int64_t)grid * 256 >= ((int64_t)1 << 31) || (int64_t)batch * voxels >= ((int64_t)1 << 31))
-    return fail("group_norm_apply: tensor too large");
-  if (dtype == LDX_DTYPE_F16)
-    hipLaunchKernelGGL((gn_apply_kernel<f16, f16x8>), dim3(grid), dim3(256), 0, as_stream(stream),
-                       (const f16*)x, x_pitch, (f16*)y, y_pitch, affine, affine_batch_stride, silu, (int)units,
-                       make_udiv((unsigned)g8), g8, make_udiv((unsigned)voxels));
-  else
-    hipLaunchKernelGGL((gn_apply_kernel<bf16, bf16x8>), dim3(grid), dim3(256), 0, as_stream(stream),
-                       (const bf16*)x, x_pitch, (bf16*)y, y_pitch, affine, affine_batch_stride, silu, (int)units,
-                       make_udiv((unsigned)g8), g8, make_udiv((unsigned)voxels));
-  return check_launch("group_norm_apply");
 }
 
 extern "C" int ldx_copy_channels(const void* src, int64_t sp, int32_t so, void* dst, int64_t dp,

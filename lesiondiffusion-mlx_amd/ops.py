@@ -466,32 +466,6 @@ def group_norm_affine(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, 
     return out
 
 
-def group_norm_apply(x: torch.Tensor, affine: torch.Tensor, *, silu: bool = True, channel_offset: int = 0,
-                     out: torch.Tensor | None = None) -> torch.Tensor:
-    """``half(silu(x * scale + offset))`` per channel of NDHWC fp16/bf16 ``x``, with the
-    ``(scale, offset)`` pairs of channels ``channel_offset ..`` of the ``(B, C, 2)`` fp32
-    ``affine`` (group_norm_affine's output): the normalised input of a fused GroupNorm +
-    SiLU conv, stored (the reference's pack kernel, _nax_conv.py:109-155). A conv of it
-    equals the fused conv of ``x`` on the same kernel path. (Measured on MI355X: the
-    config-4 decode with every input over 32 MB normalised this way ran 18.6 -> 19.8 ms,
-    so the model layers keep the fused prologue.)"""
-    _require_cuda(x, "x", (torch.float16, torch.bfloat16))
-    xp = voxel_pitch(x, "x")
-    b, d, h, w, c = (int(s) for s in x.shape)
-    if affine.dtype != torch.float32 or not affine.is_cuda or affine.dim() != 3 or affine.shape[0] != b \
-            or affine.shape[2] != 2 or affine.stride(2) != 1 or affine.stride(1) != 2 \
-            or channel_offset < 0 or channel_offset + c > affine.shape[1]:
-        raise ValueError(f"affine must be fp32 (B, >= {channel_offset + c}, 2) with contiguous pairs")
-    if out is None:
-        out = torch.empty((b, d, h, w, c), dtype=x.dtype, device=x.device)
-    yp = voxel_pitch(out, "out")
-    a = affine[:, channel_offset:]
-    check(lib.ldx_group_norm_apply(_ptr(x), xp, _ptr(out), yp, b, d * h * w, c, a.data_ptr(), int(affine.stride(0)),
-                                   1 if silu else 0, ELEM_DTYPES[x.dtype], _stream()), "group_norm_apply")
-    _wrote(out)
-    return out
-
-
 def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5,
                out: torch.Tensor | None = None) -> torch.Tensor:
     """LayerNorm over the last axis of fp16 or fp32 ``x`` (mx.fast.layer_norm,

@@ -501,38 +501,3 @@ def test_group_norm_of_a_concat_from_moments(pkg, dev) -> None:
     scale = gamma[None] / np.sqrt(np.repeat(gv, 10, axis=1) + 1e-5)
     np.testing.assert_allclose(aff[..., 0], scale, rtol=2e-5, atol=1e-6)
     np.testing.assert_allclose(aff[..., 1], beta[None] - scale * np.repeat(gm, 10, axis=1), rtol=2e-5, atol=2e-5)
-
-
-@pytest.mark.parametrize(("shape", "c0", "out_c"), [((2, 64, 6, 9, 11), 64, 64), ((1, 192, 8, 10, 10), 128, 64)])
-def test_group_norm_apply_then_conv_equals_the_fused_conv(pkg, dev, conv_path, shape, c0, out_c) -> None:
-    """ldx_group_norm_apply stores what the fused conv prologue forms on the fly: against
-    float64 GroupNorm + SiLU (one fp16 rounding); a plain conv of it equals the fused conv
-    of the raw input bit for bit on the same kernel -- the streamed kernel, forced -- and
-    within the conv's error model on the library's own choice (x1: the concat's second
-    input, normalised with the affine's channel slice)."""
-    rng = np.random.default_rng(sum(shape))
-    x, w, b = case(shape, out_c, 3, 7)
-    c = shape[1]
-    gamma = rng.normal(size=(c,)).astype(np.float32)
-    beta = rng.normal(size=(c,)).astype(np.float32)
-    x0t, x1t = to_dev(ndhwc(x[:, :c0]), dev), to_dev(ndhwc(x[:, c0:]), dev) if c0 < c else None
-    aff = pkg.ops.group_norm_affine(x0t, to_dev(gamma, dev), to_dev(beta, dev), groups=16, eps=1e-5, x1=x1t)
-    t0 = pkg.ops.group_norm_apply(x0t, aff)
-    t1 = pkg.ops.group_norm_apply(x1t, aff, channel_offset=c0) if x1t is not None else None
-    pk = pkg.ops.pack_weight(to_dev(w, dev))
-    fused = pkg.ops.nax_conv3d(x0t, pk, to_dev(b, dev), x1=x1t, affine=aff, silu=True)
-    split = pkg.ops.nax_conv3d(t0, pk, to_dev(b, dev), x1=t1)
-    torch.cuda.synchronize()
-    a = aff.cpu().numpy().astype(np.float64)
-    xx = x.astype(np.float64)
-    want = onm.silu(xx * a[:, :, 0, None, None, None] + a[:, :, 1, None, None, None])
-    got = np.concatenate([ncdhw(host(t0))] + ([ncdhw(host(t1))] if t1 is not None else []), axis=1)
-    assert np.all(np.abs(got - want) <= 2 * half_spacing(want) + 1e-7)
-    if conv_path in ("streamed", "streamed-split", "quad"):
-        assert torch.equal(fused, split)
-    tt = got.astype(np.float16).astype(np.float64)
-    w64 = w.astype(np.float64)
-    expected = ocv.conv3d(tt, w64, b.astype(np.float64))
-    bound = half_spacing(expected) + ACCUMULATION_EPS * ocv.conv3d_magnitude(tt, w64, b.astype(np.float64))
-    for y in (fused, split):
-        assert np.all(np.abs(ncdhw(host(y)) - expected) <= bound)
