@@ -128,7 +128,7 @@ int ldx_dense_ln(const ldx_conv3d_args* args, const float* gamma, const float* b
 /* FP32 mode (dtype LDX_DTYPE_F32) -- the reference's exact split-FP16 mode for FP32 networks
  * (_nax_conv.py:26-34, 210-237, 343-364): every FP32 value v is split into hi = half(v) and
  * lo = half((v - hi) * 2^11), and y = hi x hi + (hi x lo + lo x hi) * 2^-11 with FP32 sums
- * (only lo x lo is dropped, about 2^-22 relative; |v| < 65504). The weight is the stacked
+ * (only lo x lo is dropped, about 2^-22 relative; |v| < 65504). The weight is the two-plane
  * split of ldx_pack_weight_exact; the prologue (affine, SiLU), the epilogue (bias + shift,
  * scale, residual, GELU / SiLU) and y are FP32, with no rounding to 16 bits. upsample = 1
  * takes the unfolded 3x3x3 weight (the conv runs on the upsampled grid). One launch, no
