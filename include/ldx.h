@@ -139,7 +139,7 @@ int ldx_pack_weight_exact(const float* weight, int32_t out_c, int32_t in_c, int3
 /* ldx_pack_weight_exact: a Torch-layout FP32 (O, C, K, K, K) (or dense (O, C), K = 1) weight
  * (_nax_conv.py:343-364 splits the same values) as two fp16 planes, hi(W) then
  * lo(W) = half((W - hi(W)) * 2^11), each [NRB][NKC][K^3][64][8] with NRB = 2*ceil(O/64),
- * NKC = 2*ceil(C/32): fragment ((rb*NKC + kc)*K^3 + tap) holds lane l's eight values
+ * NKC = 4*ceil(C/64): fragment ((rb*NKC + kc)*K^3 + tap) holds lane l's eight values
  * W[rb*32 + l%32, kc*16 + 8*(l/32) + e, tap] at l*8 (zero past O or C).
  * ldx_packed_weight_exact_elems(O, C, K) halves in all (0 for a bad shape). */
 size_t ldx_packed_weight_exact_elems(int32_t out_c, int32_t in_c, int32_t ksize);
