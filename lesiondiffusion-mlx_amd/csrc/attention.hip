@@ -443,37 +443,41 @@ void attention_kernel(AttnParams p) {
 // alternating -- then reads the K fragments of block it + 2 and the V^T fragments of
 // block it, whose latency the softmax of block it covers. No MFMA waits on an LDS read or
 // on the softmax it runs beside; two register sets alternate with the step's parity.
-template <int D, int SPLIT>
+template <int D, int SPLIT, int QG>
 struct AttnPipeLds {
   static constexpr int HT = 32 * D;                              // halves per K or V tile
-  static constexpr int MERGE = SPLIT * 32 * (D + 4) + 2 * 32 * SPLIT;   // floats for the merge
-  static constexpr size_t bytes = (size_t)(SPLIT * 5 * HT * 2 > MERGE * 4 ? SPLIT * 5 * HT * 2 : MERGE * 4);
+  static constexpr int MERGE = QG * (SPLIT * 32 * (D + 4) + 2 * 32 * SPLIT);   // floats for the merge
+  static constexpr int RING = QG * SPLIT * 5 * HT * 2;                          // bytes of the tile rings
+  static constexpr size_t bytes = (size_t)(RING > MERGE * 4 ? RING : MERGE * 4);
 };
 
-template <int D, int SPLIT>
-__global__ __launch_bounds__(64 * SPLIT) __attribute__((amdgpu_waves_per_eu(2, 8)))
+template <int D, int SPLIT, int QG>
+__global__ __launch_bounds__(64 * SPLIT * QG) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void attention_pipe_kernel(AttnParams p) {
-  constexpr int NT = 64 * SPLIT;
+  constexpr int NT = 64 * SPLIT * QG;
   constexpr int KB = 32;
   constexpr int DK = D / 16, DB = D / 32, KG = D / 8;
-  constexpr int HT = AttnPipeLds<D, SPLIT>::HT;
+  constexpr int HT = AttnPipeLds<D, SPLIT, QG>::HT;
   constexpr int NH = HT * 2 / 1024;           // 1 KB DMA instructions per K or V tile
   constexpr int RPD = 1024 / (D * 2);
   static_assert(D == 32 || D == 64, "DMA tiles for head widths 32 and 64");
   static_assert(DK == 2 * DB, "one PV (k-step, dims block) pair per S k-step");
   extern __shared__ __attribute__((aligned(16))) E smem[];
 
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hf = lane >> 5, col = lane & 31;
+  // Wave wv takes query block qg of the workgroup's QG and key share `wave`: the QG waves
+  // of a key share (neighbours, on different SIMDs) stream the same tiles together.
+  const int qg = wv % QG, wave = wv / QG;
   int wg;
   {
     const int n = gridDim.x, l = blockIdx.x, per = n >> 3, rem = n & 7, x = l & 7, k = l >> 3;
     wg = x < rem ? x * (per + 1) + k : rem * (per + 1) + (x - rem) * per + k;
   }
-  const int nqb = (p.L + 31) / 32;
+  const int nqb = (p.L + 32 * QG - 1) / (32 * QG);
   const int qblk = wg % nqb, h = (wg / nqb) % p.H, b = wg / nqb / p.H;
-  const int q0 = qblk * 32;
-  E* kbuf = smem + wave * 5 * HT;           // three K tiles, then two V tiles
+  const int q0 = (qblk * QG + qg) * 32;
+  E* kbuf = smem + wv * 5 * HT;             // three K tiles, then two V tiles
   E* vbuf = kbuf + 3 * HT;
   const unsigned kbuf_lds = lds_offset(kbuf), vbuf_lds = lds_offset(vbuf);
 
@@ -725,7 +729,8 @@ void attention_pipe_kernel(AttnParams p) {
   // the SPLIT partials of 8 consecutive d of one query into one 16-byte store.
   E* ob = p.o + (int64_t)b * p.os0 + (int64_t)h * p.os2;
   constexpr int RP = D + 4;
-  float* mo = reinterpret_cast<float*>(smem);            // [SPLIT][32][RP] scaled partial O
+  constexpr int MG = SPLIT * 32 * RP + 2 * 32 * SPLIT;   // floats of one query block's merge
+  float* mo = reinterpret_cast<float*>(smem) + qg * MG;  // [SPLIT][32][RP] scaled partial O
   float* ml = mo + SPLIT * 32 * RP;                       // [32][SPLIT] m, then the same for l
   vmcnt_wait<0>();
   __syncthreads();   // every wave done with its tiles (the merge area overlaps them)
@@ -756,37 +761,38 @@ void attention_pipe_kernel(AttnParams p) {
       }
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < 32 * (D / 8); idx += NT) {
-    const int d8 = (idx % (D / 8)) * 8, qq = idx / (D / 8);
-    const int qg = q0 + qq;
-    if (qg >= p.L) continue;
+  for (int idx = threadIdx.x; idx < QG * 32 * (D / 8); idx += NT) {
+    const int d8 = (idx % (D / 8)) * 8, qq = (idx / (D / 8)) % 32, g = idx / (32 * (D / 8));
+    const int qr = (qblk * QG + g) * 32 + qq;
+    if (qr >= p.L) continue;
+    const float* mg = reinterpret_cast<const float*>(smem) + g * MG;
     f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int w = 0; w < SPLIT; w++) {
-      const float* r = mo + (w * 32 + qq) * RP + d8;
+      const float* r = mg + (w * 32 + qq) * RP + d8;
       a0 += *reinterpret_cast<const f32x4*>(r);
       a1 += *reinterpret_cast<const f32x4*>(r + 4);
     }
     const E8 out = {(E)a0[0], (E)a0[1], (E)a0[2], (E)a0[3], (E)a1[0], (E)a1[1], (E)a1[2], (E)a1[3]};
-    *reinterpret_cast<E8*>(ob + (int64_t)qg * p.os1 + d8) = out;
+    *reinterpret_cast<E8*>(ob + (int64_t)qr * p.os1 + d8) = out;
   }
 }
 
-template <int D, int SPLIT>
+template <int D, int SPLIT, int QG = 1>
 static int launch_attn_pipe(const AttnParams& p, hipStream_t st) {
   // Tile byte offsets within a (batch, head), up to five blocks past the last, are
   // 32-bit.
   if (((int64_t)p.LK + 160 * SPLIT + 64) * (p.ks1 > p.vs1 ? p.ks1 : p.vs1) * 2 >= ((int64_t)1 << 31))
     return fail("attention: key range too large for the DMA kernel");
-  const int64_t n = (int64_t)((p.L + 31) / 32) * p.H * p.B;
+  const int64_t n = (int64_t)((p.L + 32 * QG - 1) / (32 * QG)) * p.H * p.B;
   if (n > 0x7fffffff) return fail("attention: grid too large");
-  constexpr size_t lds = AttnPipeLds<D, SPLIT>::bytes;
+  constexpr size_t lds = AttnPipeLds<D, SPLIT, QG>::bytes;
   static_assert(lds <= 160 * 1024, "LDS");
-  auto kern = attention_pipe_kernel<D, SPLIT>;
+  auto kern = attention_pipe_kernel<D, SPLIT, QG>;
   if (lds > 65536 &&
       hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
     return check_launch("attention: set LDS size");
-  hipLaunchKernelGGL(kern, dim3((unsigned)n), dim3(64 * SPLIT), lds, st, p);
+  hipLaunchKernelGGL(kern, dim3((unsigned)n), dim3(64 * SPLIT * QG), lds, st, p);
   return check_launch("attention");
 }
 
@@ -1232,13 +1238,28 @@ static bool attn_wide(const AttnParams& p) {
   return (D == 128 || D == 256) && (split == -1 || (split == 1 && getenv("LDX_ATTN_SPLIT") == nullptr));
 }
 
+// Whether the four-way key split pairs query blocks in eight-wave workgroups: when there
+// are more 32-query workgroups than CUs, a CU would hold two, each streaming its head's K
+// and V through L2 separately (the per-CU L2 rate bounds those CUs); a pair's two waves
+// of a key share request the same tiles back to back, the second mostly from L1.
+static bool pipe_pairs(const AttnParams& p) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+    return false;
+  return (int64_t)((p.L + 31) / 32) * p.H * p.B > cus;
+}
+
 template <int D>
 static int launch_d(const AttnParams& p, hipStream_t st) {
   const int split = attn_split<D>(p);
   if constexpr (D == 32 || D == 64) {
     // Long key sequences: the DMA-fed, software-pipelined four-way key split
-    // (LDX_ATTN_SPLIT=-4 selects it for any length; -8 the eight-way split).
+    // (LDX_ATTN_SPLIT=-4 selects it for any length, -42 with query-block pairs; -8 the
+    // eight-way split).
+    if (split == -4 && !getenv("LDX_ATTN_SPLIT") && pipe_pairs(p)) return launch_attn_pipe<D, 4, 2>(p, st);
     if (split == -4) return launch_attn_pipe<D, 4>(p, st);
+    if (split == -42) return launch_attn_pipe<D, 4, 2>(p, st);
     if (split == -8) return launch_attn_pipe<D, 8>(p, st);
   }
   if constexpr (D <= 64) {

@@ -95,18 +95,18 @@ def test_attention_large_magnitudes_keep_running_max(pkg, dev) -> None:
     np.testing.assert_allclose(host(out), oatt.attention(q, k, v, 0.125), rtol=2e-3, atol=2e-3)
 
 
-@pytest.mark.parametrize("split", ["1", "4", "8", "-4", "-8"])
+@pytest.mark.parametrize("split", ["1", "4", "8", "-4", "-42", "-8"])
 @pytest.mark.parametrize(("b", "h", "lq", "lk", "d", "masked"), [
     (1, 8, 1600, 1600, 64, False),   # config 2 self-attention
     (2, 3, 100, 77, 32, False),      # ragged last key block
     (1, 2, 33, 5, 64, False),        # fewer key blocks than waves
-    (2, 3, 40, 77, 64, True),        # additive mask
+    (2, 3, 70, 77, 64, True),        # additive mask; three query blocks (a half pair)
 ])
 def test_attention_key_split_variants_match_float64(pkg, dev, monkeypatch, split, b, h, lq, lk, d,
                                                      masked) -> None:
     """Every kernel the launcher can pick (LDX_ATTN_SPLIT: 128 queries per workgroup,
-    four- and eight-way key splits, the DMA-fed pipelined four- and eight-way splits) on
-    the same inputs."""
+    four- and eight-way key splits, the DMA-fed pipelined four-way split with one or two
+    query blocks per workgroup and eight-way split) on the same inputs."""
     monkeypatch.setenv("LDX_ATTN_SPLIT", split)
     rng = np.random.default_rng(lq + 3 * lk + d)
     q, k, v = (rng.normal(size=(b, h, n, d)).astype(np.float16) for n in (lq, lk, lk))
