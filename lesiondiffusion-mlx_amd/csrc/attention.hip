@@ -52,6 +52,11 @@ struct AttnParams {
   // state in part ([tile][piece]) for attention_wide_merge_kernel.
   float* part; int pmax;
   size_t part_bytes;   // host only: the caller's workspace size
+  // Key shares of attention_pipe_kernel: the key blocks repeat in periods of kper; share w
+  // takes kcnt[w] of each period, at the positions held in the bytes of kslot[w] (in
+  // increasing order), knit[w] blocks in all.
+  int kper, kcnt[8], knit[8];
+  unsigned kslot[8][4];
 };
 
 __device__ __forceinline__ f32x16 mfma32x(E8 a, E8 b, f32x16 c) {
@@ -505,18 +510,38 @@ void attention_pipe_kernel(AttnParams p) {
   const i32x4 krs = dma_rsrc(kb_, (unsigned)(((int64_t)(p.LK - 1) * p.ks1 + D) * 2));
   const i32x4 vrs = dma_rsrc(vb_, (unsigned)(((int64_t)(p.LK - 1) * p.vs1 + D) * 2));
   const int nblk = (p.LK + KB - 1) / KB;
-  const int nit = (nblk - wave + SPLIT - 1) / SPLIT;   // this wave's blocks: wave + SPLIT * it
+  // This wave's key blocks: the share's positions of each period, period after period.
+  // (Selected with constant indices: a kernel argument indexed at run time would be
+  // copied to scratch memory.)
+  int kcnt = p.kcnt[0], nit = p.knit[0];
+  unsigned ksl0 = p.kslot[0][0], ksl1 = p.kslot[0][1], ksl2 = p.kslot[0][2], ksl3 = p.kslot[0][3];
+#pragma unroll
+  for (int w = 1; w < SPLIT; w++)
+    if (wave == w) {
+      kcnt = p.kcnt[w]; nit = p.knit[w];
+      ksl0 = p.kslot[w][0]; ksl1 = p.kslot[w][1]; ksl2 = p.kslot[w][2]; ksl3 = p.kslot[w][3];
+    }
+  const int kper = p.kper;
+  const uint64_t kslo = ((uint64_t)ksl1 << 32) | ksl0, kshi = ((uint64_t)ksl3 << 32) | ksl2;
+  auto slot = [&](int r) {   // position r of the share's period (two shifts, no table)
+    return (int)(((r < 8 ? kslo : kshi) >> ((r & 7) * 8)) & 0xffu);
+  };
+  auto block_of = [&](int it) { const int q = it / kcnt; return q * kper + slot(it - q * kcnt); };
+  // The K and V requests walk the blocks in order: one (period, position) cursor each.
+  int kq = 0, kr = 0, vq = 0, vr = 0;
   // Tiles past this wave's blocks are loaded too (their rows lie past the sequence and
   // read zeros), so every pipeline step issues the same number of loads.
   auto issue_k = [&](int it) {
-    const unsigned ks = (unsigned)((wave + SPLIT * it) * KB * p.ks1) * 2u;
-    const unsigned dst = kbuf_lds + (unsigned)((it % 3) * HT * 2);
+    const unsigned ks = __builtin_amdgcn_readfirstlane((unsigned)((kq * kper + slot(kr)) * KB * p.ks1) * 2u);
+    if (++kr == kcnt) { kr = 0; kq++; }
+    const unsigned dst = __builtin_amdgcn_readfirstlane(kbuf_lds + (unsigned)((it % 3) * HT * 2));
 #pragma unroll
     for (int j = 0; j < NH; j++) dma_buffer_b128(krs, koff[j], ks, dst + j * 1024);
   };
   auto issue_v = [&](int it) {
-    const unsigned vs = (unsigned)((wave + SPLIT * it) * KB * p.vs1) * 2u;
-    const unsigned dst = vbuf_lds + (unsigned)((it & 1) * HT * 2);
+    const unsigned vs = __builtin_amdgcn_readfirstlane((unsigned)((vq * kper + slot(vr)) * KB * p.vs1) * 2u);
+    if (++vr == kcnt) { vr = 0; vq++; }
+    const unsigned dst = __builtin_amdgcn_readfirstlane(vbuf_lds + (unsigned)((it & 1) * HT * 2));
 #pragma unroll
     for (int j = 0; j < NH; j++) dma_buffer_b128(vrs, voff[j], vs, dst + j * 1024);
   };
@@ -632,7 +657,7 @@ void attention_pipe_kernel(AttnParams p) {
         sum = probs(sc, pc);
       }
     } else {
-      const int kbase = (wave + SPLIT * it) * KB;
+      const int kbase = block_of(it) * KB;
       float top = -INFINITY;
 #pragma unroll
       for (int e = 0; e < 16; e++) {
@@ -694,7 +719,7 @@ void attention_pipe_kernel(AttnParams p) {
   // partial, and only the wave that owns it has it as its last). A wave whose first block
   // is whole seeds its queries' bases with that block's maximum, so whole blocks always
   // meet a finite base.
-  const int nfull = p.mask ? 0 : (p.LK % KB == 0 || (nblk - 1 - wave) % SPLIT != 0 ? nit : nit - 1);
+  const int nfull = p.mask ? 0 : (p.LK % KB == 0 || nit == 0 || block_of(nit - 1) != nblk - 1 ? nit : nit - 1);
   if (nfull > 0) m = halves_max(max16(sacc[0])) * p.c;
   using T = std::integral_constant<bool, true>;
   using F = std::integral_constant<bool, false>;
@@ -778,11 +803,69 @@ void attention_pipe_kernel(AttnParams p) {
   }
 }
 
+// The key-share pattern of attention_pipe_kernel for cnt[w] blocks of share w per period:
+// the period's positions go to the shares in the order of their due times (k + 1/2) /
+// cnt[w], so that every share's blocks spread evenly over the period and all shares
+// sweep the key range together.
+static int share_pattern(AttnParams& q, int split, const int* cnt) {
+  int per = 0;
+  for (int w = 0; w < split; w++) {
+    if (cnt[w] < 1 || cnt[w] > 16) return fail("attention: key share counts must lie in 1..16");
+    per += cnt[w];
+  }
+  if (per > 64) return fail("attention: key share period above 64 blocks");
+  int order[64], n = 0;
+  for (int w = 0; w < split; w++)
+    for (int k = 0; k < cnt[w]; k++) order[n++] = w * 16 + k;
+  // insertion sort by due time, ties by share
+  auto due_lt = [&](int a, int b) {
+    const int wa = a / 16, ka = a % 16, wb = b / 16, kb = b % 16;
+    const long l = (long)(2 * ka + 1) * cnt[wb], r = (long)(2 * kb + 1) * cnt[wa];
+    return l < r || (l == r && wa < wb);
+  };
+  for (int i = 1; i < n; i++)
+    for (int j = i; j > 0 && due_lt(order[j], order[j - 1]); j--) std::swap(order[j], order[j - 1]);
+  const int nblk = (q.LK + 31) / 32, full = nblk / per, rem = nblk % per;
+  q.kper = per;
+  for (int w = 0; w < 8; w++) {
+    q.kcnt[w] = w < split ? cnt[w] : 1;
+    q.knit[w] = 0;
+    for (int r = 0; r < 4; r++) q.kslot[w][r] = 0;
+  }
+  for (int i = 0; i < n; i++) {
+    const int w = order[i] / 16, k = order[i] % 16;
+    q.kslot[w][k / 4] |= (unsigned)i << (8 * (k % 4));
+  }
+  for (int w = 0; w < split; w++) {
+    q.knit[w] = full * cnt[w];
+    for (int k = 0; k < cnt[w]; k++)
+      if ((int)((q.kslot[w][k / 4] >> (8 * (k % 4))) & 0xffu) < rem) q.knit[w]++;
+  }
+  return 0;
+}
+
 template <int D, int SPLIT, int QG = 1>
-static int launch_attn_pipe(const AttnParams& p, hipStream_t st) {
-  // Tile byte offsets within a (batch, head), up to five blocks past the last, are
+static int launch_attn_pipe(const AttnParams& p0, hipStream_t st) {
+  AttnParams p = p0;
+  // Blocks per period of each key share: with two query blocks per workgroup a SIMD holds
+  // two waves, and the one of the lower key share (the older wave) issues first whenever
+  // both are ready, so with equal shares it ends well before the other, which then runs
+  // alone; the lower shares take two blocks per period to the upper shares' one (config 2:
+  // 12.96 -> 12.46 us; 3:2 the same, 7:3 12.6, 3:1 13.2). LDX_ATTN_SHARES="c0,c1,..."
+  // overrides (sweeps).
+  int cnt[SPLIT];
+  for (int w = 0; w < SPLIT; w++) cnt[w] = QG == 2 ? (w < SPLIT / 2 ? 2 : 1) : 1;
+  if (const char* e = getenv("LDX_ATTN_SHARES")) {
+    for (int w = 0; w < SPLIT; w++) {
+      char* end = nullptr;
+      cnt[w] = (int)strtol(e, &end, 10);
+      e = *end == ',' ? end + 1 : end;
+    }
+  }
+  if (int rc = share_pattern(p, SPLIT, cnt)) return rc;
+  // Tile byte offsets within a (batch, head), up to six periods past the last block, are
   // 32-bit.
-  if (((int64_t)p.LK + 160 * SPLIT + 64) * (p.ks1 > p.vs1 ? p.ks1 : p.vs1) * 2 >= ((int64_t)1 << 31))
+  if (((int64_t)p.LK + 32 * 6 * p.kper + 64) * (p.ks1 > p.vs1 ? p.ks1 : p.vs1) * 2 >= ((int64_t)1 << 31))
     return fail("attention: key range too large for the DMA kernel");
   const int64_t n = (int64_t)((p.L + 32 * QG - 1) / (32 * QG)) * p.H * p.B;
   if (n > 0x7fffffff) return fail("attention: grid too large");

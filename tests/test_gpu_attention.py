@@ -123,6 +123,33 @@ def test_attention_key_split_variants_match_float64(pkg, dev, monkeypatch, split
     assert_fp16_bar(act, exp)
 
 
+@pytest.mark.parametrize("shares", ["1,1,1,1", "5,1,3,2", "16,1,1,1"])
+@pytest.mark.parametrize("split", ["-4", "-42"])
+@pytest.mark.parametrize(("b", "h", "lq", "lk", "d", "masked"), [
+    (1, 4, 96, 1000, 64, False),     # long keys: several periods and a ragged last block
+    (2, 3, 70, 77, 32, True),        # additive mask; fewer blocks than one period
+])
+def test_attention_key_share_patterns_match_float64(pkg, dev, monkeypatch, shares, split, b, h, lq, lk, d,
+                                                    masked) -> None:
+    """The pipelined key split with uneven key shares (LDX_ATTN_SHARES: blocks per period of
+    each share, interleaved by due time) gives the same attention."""
+    monkeypatch.setenv("LDX_ATTN_SPLIT", split)
+    monkeypatch.setenv("LDX_ATTN_SHARES", shares)
+    rng = np.random.default_rng(lk + d)
+    q, k, v = (rng.normal(size=(b, h, n, d)).astype(np.float16) for n in (lq, lk, lk))
+    m_host = m_dev = None
+    if masked:
+        m_host = rng.normal(size=(b, 1, lq, lk)).astype(np.float32)
+        m_host[..., 3:11] = -np.inf
+        m_dev = to_dev(m_host, dev)
+    out = pkg.ops.attention(to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), d ** -0.5, m_dev)
+    torch.cuda.synchronize()
+    exp = oatt.attention(q, k, v, d ** -0.5, m_host)
+    act = host(out)
+    np.testing.assert_allclose(act, exp, rtol=2e-3, atol=2e-3)
+    assert_fp16_bar(act, exp)
+
+
 @pytest.mark.parametrize("split", ["default", "1", "-1"])
 @pytest.mark.parametrize(("b", "h", "lq", "lk", "d", "masked", "mag"), [
     (1, 1, 300, 300, 256, False, 1.0),   # VQ mid-attention width, ragged query and key blocks
