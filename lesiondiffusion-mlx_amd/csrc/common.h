@@ -146,6 +146,31 @@ __device__ __forceinline__ Moments merge(Moments a, Moments b) {
   return {n, a.mean + d * fb, a.m2 + b.m2 + d * d * a.n * fb};
 }
 
+// merge with the weight b.n / n from the hardware reciprocal (within 1 ulp; no IEEE
+// division sequence) -- for the short epilogue folds of a brick's partial moments.
+__device__ __forceinline__ Moments merge_rcp(Moments a, Moments b) {
+  const float n = a.n + b.n;
+  if (n == 0.0f) return a;
+  const float d = b.mean - a.mean;
+  const float fb = b.n * __builtin_amdgcn_rcpf(n);
+  return {n, a.mean + d * fb, a.m2 + b.m2 + d * d * a.n * fb};
+}
+
+// Fold of N (2, 4 or 8) partial moments e[0..N-1] held at stride `stride` floats from q:
+// all loaded first, then merged as a fixed balanced tree ((0, 1), (2, 3)), ((4, 5), (6, 7)).
+template <int N>
+__device__ __forceinline__ Moments fold_moments(const float* q, int stride) {
+  static_assert(N == 2 || N == 4 || N == 8, "2, 4 or 8 partial moments");
+  Moments e[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) e[i] = Moments{q[i * stride], q[i * stride + 1], q[i * stride + 2]};
+#pragma unroll
+  for (int w = 1; w < N; w *= 2)
+#pragma unroll
+    for (int i = 0; i < N; i += 2 * w) e[i] = merge_rcp(e[i], e[i + w]);
+  return e[0];
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -230,8 +255,9 @@ __device__ __forceinline__ void pair_moments(const V8 (&v)[NI], const bool (&ok)
 #pragma unroll
   for (int q = 0; q < 4; q++) s[q] = lane_group_sum<L>(s[q]);
   float mean[4], m2[4];
+  const float inv = cnt > 0.f ? 1.0f / cnt : 0.f;   // one division for the four pairs
 #pragma unroll
-  for (int q = 0; q < 4; q++) { mean[q] = cnt > 0.f ? s[q] / cnt : 0.f; m2[q] = 0.f; }
+  for (int q = 0; q < 4; q++) { mean[q] = s[q] * inv; m2[q] = 0.f; }
 #pragma unroll
   for (int i = 0; i < NI; i++)
     if (ok[i]) {

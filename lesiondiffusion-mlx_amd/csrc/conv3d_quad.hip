@@ -612,18 +612,13 @@ __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 
   // GroupNorm partial moments of the stored values, one block per brick: each wave's
   // channel pairs over its voxels (lanes l, l + 8, ... hold the same 8 channels) into LDS
-  // past the epilogue rows, then thread pp < 32 merges pair pp over the eight waves in order.
+  // past the epilogue rows, then thread pp < 32 merges pair pp over the eight waves (a fixed tree).
   if (p.stats) {
     float* mst = reinterpret_cast<float*>(smem + S::MST);   // [8 waves][32 pairs][3]
     pair_moments<6, 8>(outv, okv, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
     __syncthreads();
     if (tid < 32) {
-      Moments m = {0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < 8; w++) {
-        const float* q = mst + (w * 32 + tid) * 3;
-        m = merge(m, Moments{q[0], q[1], q[2]});
-      }
+      const Moments m = fold_moments<8>(mst + tid * 3, 32 * 3);   // the eight waves, a fixed tree
       float* dst = p.stats + (((int64_t)b * p.schunks + brick) * (p.O / 2) + oblk * 32 + tid) * 3;
       dst[0] = m.n; dst[1] = m.mean; dst[2] = m.m2;
     }

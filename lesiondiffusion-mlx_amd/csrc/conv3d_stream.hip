@@ -251,9 +251,10 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
     wsrc[i] = p.w + ((int64_t)((oblk * S::NOBT + ob) * 27 + kw) * p.NKC + k) * 512 + lane * 8;
     wdst[i] = lds_offset(smem) + (unsigned)(S::RING + f * 1024);
   }
-  const int nst = p.nchunk * NSTG;
+  const int nst = p.nchunk * NSTG, gend = ce * NSTG;
   auto issue_stage = [&](int g) {
-    // Past the last stage: repeat it (the data it writes is never read again).
+    // (Stages past the workgroup's last are not requested; the clamp keeps any index in
+    // range.)
     const int gg = g < nst ? g : nst - 1;
     const int ch = gg / NSTG, t = gg - ch * NSTG;
     const int64_t off = ((int64_t)(t * 3) * p.NKC + 2 * ch) * 512;   // tap (kd, kh, 0) = 3 t
@@ -340,13 +341,18 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
         }
       }
       // Stage g + 1 has landed once only the loads issued after it may be pending: stage
-      // g + 2's, and the next chunk's halo when it was requested in between. (A directly
-      // copied halo has landed with the stage after it, before this barrier.)
-      if (t == HS + 1 || t == HS + 2) vmcnt_wait<S::LW + (XF ? S::NHL : S::NR)>();
-      else vmcnt_wait<S::LW>();
+      // g + 2's (none past this workgroup's last stage), and the next chunk's halo when it
+      // was requested in between (none after the last chunk). (A directly copied halo has
+      // landed with the stage after it, before this barrier.)
+      const bool sp = g + 2 < gend, hp = (t == HS + 1 || t == HS + 2) && ch + 1 < ce;
+      if (sp && hp) vmcnt_wait<S::LW + (XF ? S::NHL : S::NR)>();
+      else if (sp) vmcnt_wait<S::LW>();
+      else if (hp) vmcnt_wait<(XF ? S::NHL : S::NR)>();
+      else vmcnt_wait<0>();
       __syncthreads();   // stage g + 1 visible; every wave done with stage g - 1's slot
-      issue_stage(g + 3);
-      if (t == HS) {
+      // Nothing is requested past the last stage and chunk: the epilogue would wait for it.
+      if (g + 3 < gend) issue_stage(g + 3);
+      if (t == HS && ch + 1 < ce) {
         // The next chunk's halo, into the buffer chunk ch - 1 used.
         if constexpr (XF) halo_issue(ch + 1);
         else halo_dma(ch + 1, (ch + 1) & 1);
@@ -370,7 +376,7 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
       load_b(2, kdn, khn, hn);
     }
   }
-  // The trailing (repeated) weight loads land before the LDS is reused or released.
+  // Every request has landed before the LDS is reused or released.
   vmcnt_wait<0>();
   __syncthreads();   // every wave done with the halo buffers
 
@@ -451,21 +457,23 @@ __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
   // GroupNorm partial moments of the stored values, one block per brick: each wave's
   // 32 voxels x 32 channel pairs (lanes l, l + 8, ... hold the same 8 channels) into LDS
   // past the epilogue rows, then thread pp < BO / 2 merges pair pp over the waves of its
-  // 64-channel half in a fixed order (K-group, then voxel block).
+  // 64-channel half as a fixed tree.
   if (p.stats && !partial) {
     float* mst = reinterpret_cast<float*>(smem + S::EPI);   // [8 waves][32 pairs][3]
     pair_moments<4, 8>(outv, okr, mst + (wave * 32 + g8 * 4) * 3, lane < 8);
     __syncthreads();
     if (tid < BO / 2) {
       const int wo_p = tid >> 5, pp = tid & 31;
-      Moments m = {0.f, 0.f, 0.f};
-#pragma unroll
-      for (int k2 = 0; k2 < 2; k2++)
-#pragma unroll
-        for (int v2 = 0; v2 < S::WV; v2++) {
-          const float* q = mst + ((k2 * 4 + wo_p * S::WV + v2) * 32 + pp) * 3;
-          m = merge(m, Moments{q[0], q[1], q[2]});
-        }
+      // The waves of this 64-channel half, (K-group, voxel block), folded as a fixed tree.
+      Moments m;
+      if constexpr (S::WV == 4) {
+        m = fold_moments<8>(mst + pp * 3, 32 * 3);
+      } else {
+        static_assert(S::WV == 2, "two or four voxel blocks per K-group");
+        const Moments m0 = fold_moments<2>(mst + ((wo_p * 2) * 32 + pp) * 3, 32 * 3);
+        const Moments m1 = fold_moments<2>(mst + ((4 + wo_p * 2) * 32 + pp) * 3, 32 * 3);
+        m = merge_rcp(m0, m1);
+      }
       float* dst = p.stats + (((int64_t)b * p.schunks + brick) * (p.O / 2) + oblk * (BO / 2) + tid) * 3;
       dst[0] = m.n; dst[1] = m.mean; dst[2] = m.m2;
     }
