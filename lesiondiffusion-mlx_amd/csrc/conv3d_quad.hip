@@ -676,22 +676,24 @@ bool conv3d_quad_plan(const ldx_conv3d_args* a, QuadParams* out) {
   if (force != 1) {
     // Grids that leave CUs idle go to the kernels built for them.
     if (nwg < 200) return false;
-    // Several rounds of workgroups with the input transform, several channel chunks or
-    // several output tiles: the streamed kernel, whose double-buffered halo hides the next
-    // chunk's staging (measured: 64x80x80 128 -> 128 with the transform 391 against 462 us,
-    // 128x160x160 64 -> 64 949 against 1062 us; one round of 32x40x40 up to 192 -> 64
-    // channels favours this kernel by 4-6 %).
-    if (nwg > 256 && (a->affine || a->silu || a->c0 + a->c1 > KC || a->out_c > 64)) return false;
     // Modelled workgroup time (cycles per 64 input channels): MFMA cycles of the busiest
     // SIMD at the measured main-loop efficiency of each kernel, plus the per-workgroup
-    // fixed cost, times the rounds of workgroups over 256 CUs. The streamed kernel's brick
-    // is 256 voxels.
+    // fixed cost, times the rounds of workgroups over 256 CUs (a partial last round counts
+    // whole). The streamed kernel's brick is 256 voxels. With the input transform this
+    // kernel stages every chunk's halo through registers before its taps (≈7k cycles a
+    // chunk), while the streamed kernel's double-buffered halo hides all but the first
+    // (≈3k). Same-box timings with the transform, µs, streamed / this kernel: 64x80x80
+    // 128 -> 128 415 / 460, 256 -> 128 783 / 859, 128x160x160 64 -> 64 1004 / 1128 (the
+    // streamed kernel), 32x40x40 256 -> 256 237 / 215, 256 -> 128 116 / 110 (this kernel:
+    // the streamed kernel's 800 or 400 workgroups leave its last round part-empty).
     const int ncol = (k.TD * k.TH * k.TW + 31) / 32;
     const int64_t nchunk = (a->c0 + a->c1) / KC;
-    const double quad = (double)ceil_div64(nwg, 256) * (nchunk * ncol * 54 * 32 / 0.95 + 6000.0);
+    const bool xf = a->affine || a->silu;
+    const double quad = (double)ceil_div64(nwg, 256) *
+                        (nchunk * ncol * 54 * 32 / 0.95 + 6000.0 + (xf ? 7000.0 * nchunk : 0.0));
     const int64_t snb = ceil_div64(a->in_d, 4) * ceil_div64(a->in_h, 8) * ceil_div64(a->in_w, 8);
     const int64_t swg = snb * (a->out_c / 64) * a->batch;
-    const double stream = (double)ceil_div64(swg, 256) * (nchunk * 432 * 32 / 0.7 + 9000.0);
+    const double stream = (double)ceil_div64(swg, 256) * (nchunk * 432 * 32 / 0.7 + 9000.0 + (xf ? 3000.0 : 0.0));
     if (!(quad < stream)) return false;
   }
   QuadParams& p = *out;
