@@ -136,6 +136,7 @@ template <int D, int SPLIT>
 __global__ __launch_bounds__(SPLIT == 1 ? 256 : 64 * SPLIT)
 __attribute__((amdgpu_waves_per_eu(AttnOcc<D, SPLIT>::waves, 8)))
 void attention_kernel(AttnParams p) {
+  touch_args(p);
   constexpr int NT = SPLIT == 1 ? 256 : 64 * SPLIT;
   constexpr int KB = 32;                      // keys per block
   constexpr int DK = D >= 16 ? D / 16 : 1;    // 16-wide k-steps of Q K^T
@@ -459,6 +460,7 @@ struct AttnPipeLds {
 template <int D, int SPLIT, int QG>
 __global__ __launch_bounds__(64 * SPLIT * QG) __attribute__((amdgpu_waves_per_eu(2, 8)))
 void attention_pipe_kernel(AttnParams p) {
+  touch_args(p);
   constexpr int NT = 64 * SPLIT * QG;
   constexpr int KB = 32;
   constexpr int DK = D / 16, DB = D / 32, KG = D / 8;
@@ -907,6 +909,7 @@ struct AttnWideLds {
 template <int D>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1, D == 128 ? 2 : 1)))
 void attention_wide_kernel(AttnParams p) {
+  touch_args(p);
   constexpr int KB = 32;
   constexpr int DK = D / 16, DB = D / 32, KG = D / 8;
   constexpr int TB = AttnWideLds<D>::TB;
@@ -1184,6 +1187,7 @@ void attention_wide_kernel(AttnParams p) {
 // tile, a wave per 32 of its queries.
 template <int D, int S>
 __global__ __launch_bounds__(256) void attention_wide_merge_kernel(AttnParams p) {
+  touch_args(p);
   constexpr int DB = D / 32, R4 = DB * 4 + 1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int hf = lane >> 5, col = lane & 31;

@@ -407,6 +407,7 @@ constexpr int NHL = NHMAX + 4;   // loads per thread of one planned halo request
 // has (the coarse UNet levels).
 template <int WO, int WV, int FO, int FV, int CC, int KSZ, bool VEC, bool PLAN, int TPS>
 __global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
+  touch_args(p);
   // One K-group of four waves takes every k-step of a tap (the indexing below keeps the
   // group variables: a two-group variant, two waves per SIMD on one output tile, measured
   // no faster and was taken out).
@@ -714,6 +715,7 @@ __global__ __launch_bounds__(256) void conv3d_kernel(ConvParams p) {
 // flattened (D = H = 1, W = voxels) so the conv epilogue maps voxel slots directly.
 template <int WO, int WV, int FO, int FV>
 __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
+  touch_args(p);
   constexpr int BO = WO * FO * 32, BV = WV * FV * 32;
   constexpr int PD = 4;                       // k-steps of operands in flight
   constexpr int EPW = FO * 32 + 4;
@@ -832,6 +834,7 @@ __global__ __launch_bounds__(256) void dense_kernel(ConvParams p) {
 // and wave, then fp16((x - mean) * rstd * gamma + beta) as the B operand.
 template <int FO, int FV, bool LN = false>
 __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
+  touch_args(p);
   constexpr int BO = FO * 32, BV = FV * 32;
   constexpr int PD = 8;                       // k-steps of operands in flight per wave
   constexpr int EPW = FO * 32 + 4;
@@ -1022,6 +1025,7 @@ __global__ __launch_bounds__(256) void dense_ksplit_kernel(ConvParams p) {
 // Split-K finish: sum the fp32 partial planes in split order, then the same epilogue
 // as the single-pass kernel (bias, scale, residual, one rounding, optional GELU).
 __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t nvox) {
+  touch_args(p);
   const int64_t n = nvox * p.O;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -1043,6 +1047,7 @@ __global__ __launch_bounds__(256) void conv_reduce_kernel(ConvParams p, int64_t 
 // below 2^31): thread per (voxel, 8 channels), partial planes summed in split order, then
 // conv_reduce_kernel's epilogue.
 __global__ __launch_bounds__(256) void conv_reduce8_kernel(ConvParams p, int nvox) {
+  touch_args(p);
   const int G8 = p.O >> 3;
   const int n8 = nvox * G8;
   const int vol = nvox / p.B;
@@ -1096,6 +1101,7 @@ __global__ __launch_bounds__(256) void conv_reduce8_kernel(ConvParams p, int nvo
 constexpr int RS_THREADS = 1024;
 constexpr int RS_PASSES = 2;   // 32 / VP passes: VP >= 16 for O <= 512
 __global__ __launch_bounds__(RS_THREADS) void conv_reduce_stats_kernel(ConvParams p, int ovol) {
+  touch_args(p);
   __shared__ float part4[RS_THREADS * 4];
   __shared__ float pmean[256];
   const int G8 = p.O >> 3, VP = RS_THREADS / G8;

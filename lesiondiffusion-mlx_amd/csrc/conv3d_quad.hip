@@ -96,6 +96,7 @@ __device__ __forceinline__ f32x16 mfma(E8 a, E8 b, f32x16 c) { return mfma_e(a, 
 
 template <int TD, int TH, int TW, bool XF>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2))) void conv3q_kernel(QuadParams p) {
+  touch_args(p);
   using S = QShape<TD, TH, TW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;

@@ -96,6 +96,7 @@ using ic = std::integral_constant<int, I>;
 // voxels outside the volume read zeros).
 template <int BO, int TD, int TH, int TW, bool XF>
 __global__ __launch_bounds__(NT) void conv3s1_kernel(StreamParams p) {
+  touch_args(p);
   using S = Shape<BO, TD, TH, TW>;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;

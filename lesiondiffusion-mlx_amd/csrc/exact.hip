@@ -247,6 +247,7 @@ __device__ __forceinline__ f32x16 mfma_h(f16x8 a, f16x8 b, f32x16 c) {
 
 template <int D>
 __global__ __launch_bounds__(256) void attention_split_kernel(SplitAttnParams p) {
+  touch_args(p);
   constexpr int KB = 32;                 // keys per block
   constexpr int DK = D / 16, DB = D / 32;
   constexpr int KP = D + 8;              // plane pitch (halves)
@@ -489,6 +490,7 @@ struct ExactConvShape {
 template <int KS, int S, int BD, int BH, int BW, int KG, int NCW>
 __global__ __launch_bounds__((ExactConvShape<KS, S, BD, BH, BW, KG, NCW>::NT)) void conv3d_exact_kernel(
     ExactConvParams p) {
+  touch_args(p);
   using SH = ExactConvShape<KS, S, BD, BH, BW, KG, NCW>;
   constexpr int TAPS = SH::TAPS, NIT = SH::NIT, PL = SH::PL, GPV = SH::GPV, WPG = SH::WPG;
   constexpr int CSETS = WPG / 2;   // column sets: wave w has columns w / 2 + CSETS j

@@ -96,6 +96,7 @@ __device__ __forceinline__ float src_x(const SrcConvParams& p, const SrcTap& tp,
 }
 
 __global__ __launch_bounds__(SC_THREADS) void src_conv_kernel(SrcConvParams p) {
+  touch_args(p);
   __shared__ float4 xs[SC_K][SC_P / 4];   // im2col tile, k-major: 16-byte reads of 4 positions
   __shared__ float4 ws[SC_K][SC_O / 4];   // weight tile, k-major: 16-byte reads of 4 channels
   float* xsf = reinterpret_cast<float*>(&xs[0][0]);
@@ -276,6 +277,7 @@ __device__ __forceinline__ float gn_value(const SrcGnParams& p, int n, int g, in
 // (16 k + j) * 8 + l for j < count, the reference's per-lane Welford chain
 // (_source_half.py:135-162); neighbouring lanes read neighbouring values.
 __global__ __launch_bounds__(256) void src_gn_partial_kernel(SrcGnParams p) {
+  touch_args(p);
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= (int64_t)p.B * p.G * p.chunks * GN_VEC) return;
   const int lane = (int)(idx & (GN_VEC - 1));
@@ -337,6 +339,7 @@ __device__ __forceinline__ void gn_take_chunk(const float4* part, unsigned count
 // set, node(L, i) = merge(merge(empty, node(L-1, 2i)), node(L-1, 2i+1)). The same merges,
 // done level by level across the wave, give the reference's level-6 result bit for bit.
 __global__ __launch_bounds__(64) void src_gn_cascade_kernel(SrcGnParams p) {
+  touch_args(p);
   __shared__ SrcMoments nodes[64];
   const int t = threadIdx.x;
   const int64_t blk = blockIdx.x;   // group * blocks + block
@@ -376,6 +379,7 @@ constexpr int GN_STAGE = 512;   // block cascades or chunk partials staged in LD
 // (_source_half.py:201-260), by one thread from LDS (the staging is cooperative); then the
 // channel affines (:263-278).
 __global__ __launch_bounds__(256) void src_gn_final_kernel(SrcGnParams p, int depth) {
+  touch_args(p);
   __shared__ float4 stage[GN_STAGE * 4];
   __shared__ SrcMoments stack[GN_MAX_DEPTH];   // the cascade's levels (thread 0's; in LDS, not scratch)
   __shared__ float red[2];
@@ -473,6 +477,7 @@ __device__ __forceinline__ f16 gn_apply1(float scale, float offset, f16 x) {
 }
 
 __global__ __launch_bounds__(256) void src_gn_apply_kernel(SrcGnParams p, int vec16) {
+  touch_args(p);
   const int c = blockIdx.y, n = blockIdx.z;
   const int64_t v0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (v0 >= p.S) return;
