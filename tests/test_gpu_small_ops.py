@@ -27,6 +27,10 @@ def host(t):
 @pytest.mark.parametrize(("shape", "groups", "split"), [
     ((2, 5, 6, 7, 64), 32, 0), ((1, 32, 40, 40, 64), 32, 0), ((1, 4, 5, 5, 9), 9, 0),
     ((2, 3, 4, 5, 96), 32, 64), ((1, 8, 10, 10, 512), 32, 256), ((1, 2, 2, 2, 4), 4, 0),
+    # one-launch path at the config-5 coarse levels: 8 channels per group, several passes of
+    # eight voxels per thread, a concat boundary, and 24 channels per group
+    ((1, 8, 10, 10, 256), 32, 0), ((2, 4, 5, 5, 256), 32, 0), ((1, 16, 20, 20, 256), 32, 128),
+    ((1, 4, 5, 5, 768), 32, 0),
 ])
 def test_group_norm_affine_matches_oracle(pkg, dev, shape, groups, split) -> None:
     rng = np.random.default_rng(sum(shape))
