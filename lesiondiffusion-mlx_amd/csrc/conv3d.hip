@@ -1370,11 +1370,13 @@ static int plan_conv(const ldx_conv3d_args* a, ConvParams& p, Tile& t, size_t& l
   // fewer than 128 such tiles and for the scalar-staged inputs (measured: the 16x20x20
   // stride-2 output 20.4 -> 15.0 us, the 9-channel conv_in at 32x40x40 20.9 -> 18.8 us).
   else if (p.O <= 64) t = vec && rows / 128 >= 128 ? Tile{1, 4, 2, 1, 32} : Tile{2, 2, 1, 1, 32};
-  else if (rows / 256 * ((p.O + 63) / 64) >= 512) t = {1, 4, 2, 2, 32};
-  // Upsampling convs below that, whose 128 x 128 tiles still make 256 workgroups or more
-  // (measured: 16x20x20 -> 32x40x40 at 128 channels 36.5 -> 24.3 us; 8x10x10 -> 16x20x20
-  // at 256 channels, 100 such tiles, stays below: 17.2 us there against 34.7).
+  // Upsampling convs whose 128 x 128 tiles make 256 workgroups or more (measured:
+  // 16x20x20 -> 32x40x40 at 128 channels 36.5 -> 24.3 us against 64 x 64 tiles; the VQ
+  // decoder's 32x40x40 -> 64x80x80 at 256 channels 624 -> 545 us and 64x80x80 ->
+  // 128x160x160 at 128 channels 1268 -> 1106 us against 64 x 256 tiles; 8x10x10 ->
+  // 16x20x20 at 256 channels, 100 such tiles, stays below: 17.2 us there against 34.7).
   else if (p.upsample && rows / 128 * ((p.O + 127) / 128) >= 256) t = {2, 2, 2, 2, 32};
+  else if (rows / 256 * ((p.O + 63) / 64) >= 512) t = {1, 4, 2, 2, 32};
   // Small volumes: 64-channel chunks, but 32-channel ones below 256 voxels, where the split
   // over channel chunks then spreads the weights over twice the workgroups (measured:
   // 4x5x5, 256 -> 256 channels 13.4 -> 12.0 us).
